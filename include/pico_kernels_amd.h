@@ -1,0 +1,177 @@
+/*
+ * pico_kernels_amd.h -- C ABI of the MI355X (gfx950) quantized-matmul library.
+ *
+ * This is the drop-in boundary for the quantized-matmul path of pico-kernels. In the
+ * reference, the operator API is a set of module-level Python functions that launch Triton
+ * kernels; each entry point below names the reference function it replaces (file:line in
+ * the reference repository). The Python modules gemm_int4.py / gemm_fp8.py / gemm_splitk.py
+ * / quantize.py in pico-kernels_amd/ keep the reference signatures and call these symbols
+ * through ctypes.
+ *
+ * Conventions
+ *  - Plain pointers and sizes only. Device pointers are HIP device memory; `stream` is a
+ *    hipStream_t passed as void* (NULL = the default stream). All launches are asynchronous
+ *    on `stream`; nothing here synchronises the device.
+ *  - The library never allocates device memory. Entry points that need scratch space take
+ *    a caller-owned `workspace` whose size is given by the matching *_workspace_bytes();
+ *    its contents need no initialisation. Calls ordered on one stream may reuse a
+ *    workspace; calls that overlap in time must not share one.
+ *  - Matrices are row-major with an explicit leading dimension (elements, or 32-bit words
+ *    for packed int4).
+ *  - Return value: PK_OK (0) or a negative PK_E* code; pk_last_error() then describes the
+ *    failure (thread-local, valid until the next failing call on the same thread).
+ */
+#ifndef PICO_KERNELS_AMD_H
+#define PICO_KERNELS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+enum {
+  PK_F32 = 0,
+  PK_F16 = 1,
+  PK_BF16 = 2,
+  PK_E4M3 = 3, /* OCP fp8 e4m3 ("e4m3fn"), one byte */
+  PK_I8 = 4,
+  PK_U8 = 5,
+  PK_I32 = 6
+};
+
+/* Status codes. */
+enum {
+  PK_OK = 0,
+  PK_EINVAL = -1,       /* bad argument: shape, dtype, alignment, null pointer */
+  PK_EUNSUPPORTED = -2, /* valid request this build does not implement */
+  PK_EWORKSPACE = -3,   /* workspace missing or too small */
+  PK_EHIP = -4          /* a HIP runtime call failed (launch error) */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int pk_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* pk_last_error(void);
+
+/* ------------------------------------------------------------------------------------- */
+/* Reductions and casts                                                                  */
+/* ------------------------------------------------------------------------------------- */
+
+/* out_dev[0] = max(|x|) over n elements as fp32 (NaN if any element is NaN).
+ * Replaces `w.abs().max()` in gemm_int4.quantize_int4 (gemm_int4.py:60) and
+ * `x.abs().max()` in gemm_fp8.quantize (gemm_fp8.py:94). */
+size_t pk_absmax_workspace_bytes(int64_t n);
+int pk_absmax(const void* x, int x_dtype, int64_t n, float* out_dev, void* workspace,
+              size_t workspace_bytes, void* stream);
+
+/* Per-tensor int4 codes: q[i] = int8(clamp(round(T(x[i] / scale)), -8, 7)) where T rounds
+ * the fp32 quotient to x's dtype (fp16/bf16) exactly as a torch tensor op does, round is
+ * half-to-even, and `scale` is the Python float narrowed to fp32. A NaN quotient gives 0.
+ * Replaces gemm_int4.quantize_int4 (gemm_int4.py:58-62); the scale itself
+ * (absmax / 7.0 in double) is computed by the caller from pk_absmax. */
+int pk_quantize_int4(const void* w, int w_dtype, int64_t n, float scale, int8_t* q,
+                     void* stream);
+
+/* Pack int4 codes two per byte along N: packed[k, j] = (q[k,2j] & 0xF) | (q[k,2j+1] << 4).
+ * q is (rows, cols) int8 with row stride ldq elements; packed is (rows, cols/2) contiguous.
+ * cols must be even. Replaces gemm_int4.pack_int4_n (gemm_int4.py:65-72). */
+int pk_pack_int4(const int8_t* q, int64_t rows, int64_t cols, int64_t ldq, uint8_t* packed,
+                 void* stream);
+
+/* Inverse of pk_pack_int4 with sign extension (codes in [-8, 7]). Mirrors the in-kernel
+ * unpack of gemm_int4.int4_gemm_kernel (gemm_int4.py:44-49). */
+int pk_unpack_int4(const uint8_t* packed, int64_t rows, int64_t cols, int8_t* q,
+                   void* stream);
+
+/* Group-wise symmetric round-to-nearest quantization along K of a (K, N) weight, the
+ * arithmetic of quantize.rtn_layer / quantize_col (quantize.py:42-68): for every column n
+ * and every group of `group_size` consecutive rows (the last group may be short),
+ *   s = max(max|w|, 1e-12) / qmax  (fp32),  q = clamp(round(w / s), -qmax, qmax),
+ * with qmax = 2^(bits-1) - 1 and all arithmetic in fp32 (w widened exactly).
+ * group_size <= 0 means one group per column (quantize_col with group_size=None).
+ * Outputs (each may be NULL):
+ *   qweight   (K, N/8) int32: 4-bit codes, byte-identical to pack_int4_n (bits must be 4,
+ *             N % 8 == 0)
+ *   scales    (ceil(K/G), N) in `scale_dtype` (PK_F16 or PK_F32), RNE-rounded from s
+ *   fake      (K, N) in `fake_dtype`: T(q * s), the tensor rtn_layer returns
+ * half_math != 0 reproduces quantize_col applied directly to an fp16 tensor (every op
+ * rounded to fp16, the 1e-12 floor becoming 0); it requires w_dtype == PK_F16.
+ * Replaces quantize.rtn_layer / quantize.quantize_col (quantize.py:42-68) and is the
+ * producer of the packed group-128 format consumed by pk_w4a16_gemm. */
+int pk_quantize_group(const void* w, int w_dtype, int64_t K, int64_t N, int64_t ldw, int bits,
+                      int group_size, int half_math, uint32_t* qweight, void* scales,
+                      int scale_dtype, void* fake, int fake_dtype, void* stream);
+
+/* Scaled cast to fp8 e4m3: out[i] = e4m3(T(x[i] * scale)) where T rounds the fp32 product to
+ * x's dtype (fp16/bf16/fp32), then round-to-nearest-even, non-saturating (overflow -> NaN).
+ * Replaces `(x * scale).to(torch.float8_e4m3fn)` in gemm_fp8.quantize (gemm_fp8.py:95). */
+int pk_cast_e4m3(const void* x, int x_dtype, int64_t n, float scale, uint8_t* out,
+                 void* stream);
+
+/* ------------------------------------------------------------------------------------- */
+/* W4A16 matmul                                                                          */
+/* ------------------------------------------------------------------------------------- */
+
+/* C[M,N] = tensor_scale * sum_k A[m,k] * Wdq[k,n] with fp32 accumulation, where
+ *   Wdq[k,n] = q[k,n] * S[k / group_size, n]   (scales given; fp16, row stride N)
+ *   Wdq[k,n] = q[k,n]                          (scales == NULL: per-tensor mode)
+ * A is fp16 (M, K) with row stride lda; qweight is (K, N/8) int32 with row stride ldq words,
+ * nibble i of word j holding column 8j+i (pack_int4_n byte order); C is fp32/fp16/bf16 with
+ * row stride ldc. Requires N % 8 == 0, K % 32 == 0 and, with scales, K % group_size == 0
+ * and group_size % 32 == 0.
+ * split_k: 0 = choose automatically; s >= 1 = split K into s contiguous slices of K/s rows
+ * (K/s a multiple of 8 for M <= 4, of 64 otherwise) whose fp32 partial sums are reduced in a
+ * fixed order (results are bitwise reproducible run to run).
+ * workspace: pk_w4a16_workspace_bytes() bytes (fp32 partials of the slices).
+ * Replaces gemm_int4.int4_gemm (gemm_int4.py:75-92, per-tensor mode, the `c * scale`
+ * epilogue fused) and provides the group-128 / split-K W4A16 path; the split-K semantics
+ * (contiguous K slices of K / split_k) follow gemm_splitk.triton_gemm_splitk
+ * (gemm_splitk.py:49-53, 67-80) without its fp32 atomics. */
+size_t pk_w4a16_workspace_bytes(int M, int N, int K, int group_size, int split_k);
+int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight, int64_t ldq,
+                  const void* scales, int group_size, float tensor_scale, void* c,
+                  int c_dtype, int64_t ldc, int M, int N, int K, int split_k, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* Which kernel pk_w4a16_gemm would run and its split factor (for reporting/benchmarks):
+ * writes kernel id (1 = skinny GEMV, 2 = MFMA GEMM) and the effective split. */
+int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_id,
+                  int* split_used);
+
+/* ------------------------------------------------------------------------------------- */
+/* Dense fp16 matmul with deterministic split-K                                          */
+/* ------------------------------------------------------------------------------------- */
+
+/* C[M,N] (fp32/fp16) = A[M,K] (fp16) @ B[K,N] (fp16, row-major, row stride ldb), fp32
+ * accumulate, K split into split_k contiguous slices reduced in fixed order.
+ * Requires K % (32 * split_k) == 0 and N % 8 == 0.
+ * Replaces gemm_splitk.triton_gemm_splitk (gemm_splitk.py:67-80); the reference reduces the
+ * slices with fp32 atomics, this reduction is ordered and reproducible. */
+size_t pk_gemm_f16_workspace_bytes(int M, int N, int K, int split_k);
+int pk_gemm_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int c_dtype,
+                int64_t ldc, int M, int N, int K, int split_k, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------- */
+/* fp8 e4m3 matmul                                                                       */
+/* ------------------------------------------------------------------------------------- */
+
+/* C[M,N] = out_scale * (A8[M,K] @ B8[K,N]) with e4m3 inputs, fp32 accumulation and the
+ * scale applied once in the epilogue; C is fp32/fp16/bf16.
+ * b_layout 0: B8 is (K, N) row-major with row stride ldb (the reference layout);
+ * b_layout 1: B8 is stored transposed, (N, K) row-major with row stride ldb.
+ * Requires K % 128 == 0, M, N >= 1, 16-byte aligned rows.
+ * Replaces gemm_fp8.fp8_gemm_precast / fp8_gemm_kernel (gemm_fp8.py:38-86, 98-117). */
+int pk_fp8_gemm(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb, int b_layout,
+                float out_scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PICO_KERNELS_AMD_H */

@@ -1,0 +1,279 @@
+"""ctypes binding to ``libpico_kernels_amd.so`` (the C ABI in ``include/pico_kernels_amd.h``).
+
+This module is the only place that touches the shared library. It turns torch tensors into
+(pointer, shape, stride, stream) arguments, owns the per-stream workspaces and raises on any
+non-zero status. It never computes anything itself: if the library or a GPU is missing it
+raises instead of falling back to another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+HERE = Path(__file__).resolve().parent
+LIB_NAME = "libpico_kernels_amd.so"
+LIB_PATH = Path(os.environ.get("PICO_KERNELS_AMD_LIB", str(HERE / LIB_NAME)))
+
+# dtype codes (include/pico_kernels_amd.h)
+PK_F32, PK_F16, PK_BF16, PK_E4M3, PK_I8, PK_U8, PK_I32 = range(7)
+_TORCH_TO_PK = {torch.float32: PK_F32, torch.float16: PK_F16, torch.bfloat16: PK_BF16}
+
+PK_OK, PK_EINVAL, PK_EUNSUPPORTED, PK_EWORKSPACE, PK_EHIP = 0, -1, -2, -3, -4
+
+KERNEL_GEMV, KERNEL_GEMM = 1, 2
+
+
+class PicoKernelsError(RuntimeError):
+    """A library call returned a non-zero status."""
+
+
+_lib = None
+_lib_lock = threading.Lock()
+
+_vp, _i32, _i64, _f32, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
+_SIGNATURES = {
+    "pk_version": (_i32, []),
+    "pk_last_error": (ctypes.c_char_p, []),
+    "pk_absmax_workspace_bytes": (_sz, [_i64]),
+    "pk_absmax": (_i32, [_vp, _i32, _i64, _vp, _vp, _sz, _vp]),
+    "pk_quantize_int4": (_i32, [_vp, _i32, _i64, _f32, _vp, _vp]),
+    "pk_pack_int4": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp]),
+    "pk_unpack_int4": (_i32, [_vp, _i64, _i64, _vp, _vp]),
+    "pk_quantize_group": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _i32,
+                                 _vp, _i32, _vp]),
+    "pk_cast_e4m3": (_i32, [_vp, _i32, _i64, _f32, _vp, _vp]),
+    "pk_w4a16_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "pk_w4a16_plan": (_i32, [_i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32),
+                             ctypes.POINTER(_i32)]),
+    "pk_w4a16_gemm": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
+                             _i32, _i32, _vp, _sz, _vp]),
+    "pk_gemm_f16_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
+    "pk_gemm_f16": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp,
+                           _sz, _vp]),
+    "pk_fp8_gemm": (_i32, [_vp, _i64, _vp, _i64, _i32, _f32, _vp, _i32, _i64, _i32, _i32, _i32,
+                           _vp]),
+}
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+def lib() -> ctypes.CDLL:
+    """Load the shared library once (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        with _lib_lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise ImportError(
+                        f"{LIB_PATH} is missing: build it with `python pico-kernels_amd/build.py`"
+                    )
+                handle = ctypes.CDLL(str(LIB_PATH))
+                for name, (res, args) in _SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = handle
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != PK_OK:
+        msg = lib().pk_last_error().decode(errors="replace")
+        raise PicoKernelsError(f"{what} failed (status {rc}): {msg}")
+
+
+def gpu_device() -> torch.device:
+    """The GPU the kernels run on; raises when no ROCm GPU is visible."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("pico-kernels_amd needs a ROCm GPU (torch.cuda.is_available() is False)")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def to_gpu(t: torch.Tensor) -> torch.Tensor:
+    """Tensors on the host are staged through the current GPU (results go back to the host)."""
+    return t if t.is_cuda else t.to(gpu_device())
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def pk_dtype(dt: torch.dtype) -> int:
+    try:
+        return _TORCH_TO_PK[dt]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dt}") from None
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------------------------------
+# Workspaces: one byte buffer per (device, stream), grown on demand and reused (it holds the
+# fp32 partials of split-K slices; nothing in it needs clearing). Calls on one stream are
+# ordered, so they never overlap on it.
+# ---------------------------------------------------------------------------------------
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    if nbytes <= 0:
+        return None
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 1 << 20)
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------------------------------
+# Thin wrappers (one per C entry point). Inputs must already be on the GPU.
+# ---------------------------------------------------------------------------------------
+def absmax(x: torch.Tensor) -> torch.Tensor:
+    """max|x| as a 0-d fp32 device tensor."""
+    assert x.is_cuda
+    x = x.contiguous()
+    n = x.numel()
+    out = torch.empty((), dtype=torch.float32, device=x.device)
+    nb = lib().pk_absmax_workspace_bytes(n)
+    ws = torch.empty(max(nb, 4), dtype=torch.uint8, device=x.device)
+    _check(lib().pk_absmax(x.data_ptr(), pk_dtype(x.dtype), n, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                           stream_of(x)), "pk_absmax")
+    return out
+
+
+def quantize_int4(w: torch.Tensor, scale: float) -> torch.Tensor:
+    w = w.contiguous()
+    q = torch.empty(w.shape, dtype=torch.int8, device=w.device)
+    _check(lib().pk_quantize_int4(w.data_ptr(), pk_dtype(w.dtype), w.numel(), float(scale),
+                                  q.data_ptr(), stream_of(w)), "pk_quantize_int4")
+    return q
+
+
+def pack_int4(q: torch.Tensor) -> torch.Tensor:
+    assert q.dim() == 2 and q.dtype == torch.int8
+    if q.stride(1) != 1:
+        q = q.contiguous()
+    rows, cols = q.shape
+    out = torch.empty((rows, cols // 2), dtype=torch.uint8, device=q.device)
+    _check(lib().pk_pack_int4(q.data_ptr(), rows, cols, max(q.stride(0), cols), out.data_ptr(),
+                              stream_of(q)), "pk_pack_int4")
+    return out
+
+
+def unpack_int4(packed: torch.Tensor) -> torch.Tensor:
+    assert packed.dim() == 2 and packed.dtype == torch.uint8
+    packed = packed.contiguous()
+    rows, half = packed.shape
+    q = torch.empty((rows, 2 * half), dtype=torch.int8, device=packed.device)
+    _check(lib().pk_unpack_int4(packed.data_ptr(), rows, 2 * half, q.data_ptr(), stream_of(packed)),
+           "pk_unpack_int4")
+    return q
+
+
+def quantize_group(w: torch.Tensor, bits: int, group_size: int | None, *, half_math: bool,
+                   want_qweight: bool, want_scales: bool, want_fake: bool,
+                   scale_dtype: torch.dtype = torch.float16,
+                   fake_dtype: torch.dtype | None = None):
+    """Group RTN along dim 0 of a 2-D (K, N) tensor. Returns (qweight, scales, fake)."""
+    assert w.dim() == 2 and w.is_cuda
+    if w.stride(1) != 1:
+        w = w.contiguous()
+    K, N = w.shape
+    g = int(group_size) if group_size else 0
+    ngroups = -(-K // g) if g else 1
+    qweight = torch.empty((K, N // 8), dtype=torch.int32, device=w.device) if want_qweight else None
+    scales = torch.empty((ngroups, N), dtype=scale_dtype, device=w.device) if want_scales else None
+    fdt = fake_dtype or w.dtype
+    fake = torch.empty((K, N), dtype=fdt, device=w.device) if want_fake else None
+    _check(lib().pk_quantize_group(
+        w.data_ptr(), pk_dtype(w.dtype), K, N, max(w.stride(0), N), int(bits), g, int(half_math),
+        ptr(qweight), ptr(scales), pk_dtype(scale_dtype), ptr(fake), pk_dtype(fdt), stream_of(w)),
+        "pk_quantize_group")
+    return qweight, scales, fake
+
+
+def cast_e4m3(x: torch.Tensor, scale: float) -> torch.Tensor:
+    x = x.contiguous()
+    out = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    _check(lib().pk_cast_e4m3(x.data_ptr(), pk_dtype(x.dtype), x.numel(), float(scale),
+                              out.data_ptr(), stream_of(x)), "pk_cast_e4m3")
+    return out
+
+
+def w4a16_plan(M: int, N: int, K: int, group_size: int, split_k: int) -> tuple[int, int]:
+    kid, spl = ctypes.c_int(0), ctypes.c_int(0)
+    _check(lib().pk_w4a16_plan(M, N, K, group_size, split_k, ctypes.byref(kid), ctypes.byref(spl)),
+           "pk_w4a16_plan")
+    return kid.value, spl.value
+
+
+def _rows_ok(t: torch.Tensor) -> torch.Tensor:
+    """Row-major with unit inner stride and 16-byte aligned rows, else a contiguous copy."""
+    es = t.element_size()
+    if (t.stride(-1) != 1 or (t.stride(0) * es) % 16 or t.data_ptr() % 16):
+        t = t.contiguous()
+        if t.data_ptr() % 16:
+            t = t.clone()
+    return t
+
+
+def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | None,
+               group_size: int, tensor_scale: float, out_dtype: torch.dtype,
+               split_k: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    M, K = a.shape
+    N = qweight.shape[1] * 8
+    a = _rows_ok(a)
+    if qweight.stride(1) != 1:
+        qweight = qweight.contiguous()
+    if scales is not None:
+        scales = scales.contiguous()
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    g = int(group_size) if scales is not None else 0
+    nbytes = lib().pk_w4a16_workspace_bytes(M, N, K, g, int(split_k))
+    ws = workspace(a.device, nbytes)
+    _check(lib().pk_w4a16_gemm(
+        a.data_ptr(), a.stride(0), qweight.data_ptr(), qweight.stride(0), ptr(scales), g,
+        float(tensor_scale), out.data_ptr(), pk_dtype(out.dtype), out.stride(0), M, N, K,
+        int(split_k), ptr(ws), 0 if ws is None else ws.numel(), stream_of(a)), "pk_w4a16_gemm")
+    return out
+
+
+def gemm_f16(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, split_k: int) -> torch.Tensor:
+    M, K = a.shape
+    N = b.shape[1]
+    a, b = _rows_ok(a), _rows_ok(b)
+    out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    nbytes = lib().pk_gemm_f16_workspace_bytes(M, N, K, int(split_k))
+    ws = workspace(a.device, nbytes)
+    _check(lib().pk_gemm_f16(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), out.data_ptr(),
+                             pk_dtype(out_dtype), out.stride(0), M, N, K, int(split_k), ptr(ws),
+                             0 if ws is None else ws.numel(), stream_of(a)), "pk_gemm_f16")
+    return out
+
+
+def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, out_scale: float, out_dtype: torch.dtype,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    M, K = a8.shape
+    N = b8.shape[1]
+    a8 = _rows_ok(a8)
+    # b8 is (K, N). A transposed view of a row-major (N, K) buffer is consumed in place.
+    if b8.stride(0) == 1 and b8.stride(1) >= K and (b8.stride(1) % 16 == 0) and b8.data_ptr() % 16 == 0:
+        b_layout, b_buf, ldb = 1, b8, b8.stride(1)
+    else:
+        b_buf = b8 if (b8.stride(1) == 1 and b8.stride(0) % 8 == 0 and b8.data_ptr() % 8 == 0) else b8.contiguous()
+        b_layout, ldb = 0, b_buf.stride(0)
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a8.device)
+    _check(lib().pk_fp8_gemm(a8.data_ptr(), a8.stride(0), b_buf.data_ptr(), ldb, b_layout,
+                             float(out_scale), out.data_ptr(), pk_dtype(out.dtype), out.stride(0),
+                             M, N, K, stream_of(a8)), "pk_fp8_gemm")
+    return out

@@ -1,0 +1,130 @@
+// Shared device/host helpers for the pico-kernels MI355X (gfx950) library.
+//
+// Everything here is written for CDNA4 only: 64-lane wavefronts, MFMA, 160 KB LDS.
+// No CUDA-compat headers, no alternate code paths.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/pico_kernels_amd.h"
+
+typedef _Float16 pk_half;
+typedef _Float16 pk_half2 __attribute__((ext_vector_type(2)));
+typedef _Float16 pk_half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 pk_half8 __attribute__((ext_vector_type(8)));
+typedef float pk_f4 __attribute__((ext_vector_type(4)));
+typedef float pk_f16v __attribute__((ext_vector_type(16)));
+typedef int pk_i8v __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------------------
+// Error reporting (host side). Every C-ABI entry point returns PK_OK or a negative code and
+// leaves a human-readable message retrievable with pk_last_error().
+// ---------------------------------------------------------------------------------------
+namespace pk {
+void set_error(const char* fmt, ...);
+int hip_status(hipError_t e, const char* what);
+}  // namespace pk
+
+#define PK_REQUIRE(cond, ...)                      \
+  do {                                             \
+    if (!(cond)) {                                 \
+      ::pk::set_error(__VA_ARGS__);                \
+      return PK_EINVAL;                            \
+    }                                              \
+  } while (0)
+
+#define PK_LAUNCH_CHECK(what) \
+  do { hipError_t _e = hipGetLastError(); if (_e != hipSuccess) return ::pk::hip_status(_e, what); } while (0)
+
+namespace pk {
+
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------------------
+// Scalar conversions
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+// Round-to-nearest-even float -> bf16 (NaN kept quiet). Used to reproduce bf16 tensor math.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Load element i of an fp32 / fp16 / bf16 array as float (exact widening).
+__device__ __forceinline__ float load_as_f32(const void* p, int dtype, int64_t i) {
+  if (dtype == PK_F32) return reinterpret_cast<const float*>(p)[i];
+  if (dtype == PK_F16) return (float)reinterpret_cast<const pk_half*>(p)[i];
+  return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+// Round a float to the storage precision of `dtype` and back (what a torch op producing a
+// tensor of that dtype does to its fp32 "opmath" result).
+__device__ __forceinline__ float round_to_dtype(float v, int dtype) {
+  if (dtype == PK_F16) return (float)(pk_half)v;  // v_cvt_f16_f32: round-to-nearest-even
+  if (dtype == PK_BF16) return bf16_to_f32(f32_to_bf16_rne(v));
+  return v;
+}
+
+__device__ __forceinline__ void store_from_f32(void* p, int dtype, int64_t i, float v) {
+  if (dtype == PK_F32) reinterpret_cast<float*>(p)[i] = v;
+  else if (dtype == PK_F16) reinterpret_cast<pk_half*>(p)[i] = (pk_half)v;
+  else reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_rne(v);
+}
+
+// OCP FP8 E4M3 ("e4m3fn": no infinities, S.1111.111 is NaN, max finite 448).
+// Round-to-nearest-even, NOT saturating: any magnitude that rounds above 448 (that is,
+// anything above 464, the tie point between 448 and the missing 480) and any Inf/NaN input
+// becomes NaN (0x7f | sign). Written from the format definition:
+//   normal:    (-1)^s * 2^(e-7) * (1 + m/8),   e in 1..15 (e=15,m=7 reserved for NaN)
+//   subnormal: (-1)^s * 2^-6 * (m/8)
+__host__ __device__ __forceinline__ uint8_t e4m3_from_f32(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x43e80000u) return sign | 0x7fu;           // > 464.0, Inf or NaN
+  if (a < 0x3c800000u) {                              // below 2^-6: subnormal grid of 2^-9
+    float mag = __builtin_bit_cast(float, a) * 512.0f;  // exact (power-of-two scaling)
+    return sign | (uint8_t)__builtin_rintf(mag);      // 0..8; 8 is the smallest normal
+  }
+  // Normal range [2^-6, 464]: keep 3 mantissa bits with round-to-nearest-even. Adding
+  // (half ulp - 1) plus the kept LSB then truncating is RNE; a mantissa carry correctly
+  // bumps the exponent field.
+  uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;  // = (f32 exp << 3) | mant3
+  return sign | (uint8_t)(r - ((127u - 7u) << 3));
+}
+
+__host__ __device__ __forceinline__ float e4m3_to_f32(uint8_t v) {
+  uint32_t s = (uint32_t)(v & 0x80u) << 24;
+  uint32_t e = (v >> 3) & 15u, m = v & 7u;
+  if (e == 15u && m == 7u) return __builtin_bit_cast(float, s | 0x7fc00000u);
+  float mag;
+  if (e == 0) mag = (float)m * (1.0f / 512.0f);
+  else mag = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, mag) | s);
+}
+
+// NaN-propagating max of non-negative values (torch's max propagates NaN).
+__device__ __forceinline__ float nanmax(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return a > b ? a : b;
+}
+
+// Clamp that propagates NaN the way torch.clamp does.
+__device__ __forceinline__ float clamp_nan(float x, float lo, float hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
+// ---------------------------------------------------------------------------------------
+// Wave-level helpers (wave64).
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+}  // namespace pk

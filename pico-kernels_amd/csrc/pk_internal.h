@@ -1,0 +1,33 @@
+// Internal planning/launch interfaces shared between the kernel files and the C-ABI layer.
+#pragma once
+#include "pk_common.h"
+
+namespace pk {
+
+// C = scale * sum over slices of the (S, M, N) fp32 partials, in slice order.
+int splitk_reduce(const float* partials, int S, int M, int N, float scale, void* c, int c_dtype,
+                  int64_t ldc, hipStream_t s);
+
+struct GemvPlan {
+  int rpt, rl, split, k_slice, tiles;
+};
+bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvPlan* out);
+size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N);
+int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
+                const void* scales, int group, float tensor_scale, void* c, int c_dtype,
+                int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s);
+
+struct GemmCfg {
+  int bm, bn, wm, wn;
+};
+struct GemmPlan {
+  GemmCfg cfg;
+  int split, k_slice, tiles_m, tiles_n;
+};
+bool gemm_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemmPlan* out);
+size_t gemm_workspace_bytes(const GemmPlan& pl, int M, int N);
+int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const void* b,
+                int64_t ldb, const void* scales, int group, float tensor_scale, void* c,
+                int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s);
+
+}  // namespace pk

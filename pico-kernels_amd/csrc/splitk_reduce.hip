@@ -1,0 +1,40 @@
+// Fixed-order split-K reduction shared by the GEMV and the MFMA GEMM:
+//   C[m, n] = scale * (((P[0][m][n] + P[1][m][n]) + P[2][m][n]) + ... + P[S-1][m][n])
+// where P is the (S, M, N) fp32 workspace written by the slices. Summing in slice order on
+// the same element by the same thread makes the result independent of launch timing
+// (the reference's split-K uses fp32 atomics instead, gemm_splitk.py:64).
+#include "pk_internal.h"
+
+namespace pk {
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partials,
+                                                            int S, int M, int N, float scale,
+                                                            void* __restrict__ c, int c_dtype,
+                                                            int64_t ldc) {
+  const int64_t plane = (int64_t)M * N;
+  const int64_t quads = plane / 4;  // N % 8 == 0, so rows hold whole quads
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += stride) {
+    const pk_f4* src = reinterpret_cast<const pk_f4*>(partials) + q;
+    pk_f4 v = __builtin_nontemporal_load(src);
+    for (int s = 1; s < S; ++s) v += __builtin_nontemporal_load(src + s * (plane / 4));
+    const int64_t e = q * 4;
+    const int64_t m = e / N, n = e - m * N;
+    const int64_t o = m * ldc + n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i] * scale);
+  }
+}
+
+int splitk_reduce(const float* partials, int S, int M, int N, float scale, void* c, int c_dtype,
+                  int64_t ldc, hipStream_t s) {
+  const int64_t quads = (int64_t)M * N / 4;
+  int64_t blocks = cdiv(quads, 256);
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(partials, S, M, N, scale, c, c_dtype, ldc);
+  PK_LAUNCH_CHECK("split-K reduce");
+  return PK_OK;
+}
+
+}  // namespace pk

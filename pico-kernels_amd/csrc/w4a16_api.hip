@@ -1,0 +1,142 @@
+// C ABI for the W4A16 matmul (gemm_int4.int4_gemm + the group-128 / split-K path) and the
+// dense fp16 split-K matmul (gemm_splitk.triton_gemm_splitk).
+//
+// Dispatch: M <= 4 runs the skinny HBM-bound GEMV (register dequant, v_dot2); larger M runs
+// the MFMA GEMM that dequantises B into LDS. Both honour an explicit split_k.
+#include "pk_internal.h"
+
+using namespace pk;
+
+namespace {
+
+enum { kKernelGemv = 1, kKernelGemm = 2 };
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int check_w4a16(const void* a, int64_t lda, const uint32_t* qw, int64_t ldq, const void* scales,
+                int group_size, const void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                int split_k) {
+  PK_REQUIRE(a != nullptr && qw != nullptr && c != nullptr, "pk_w4a16_gemm: null pointer");
+  PK_REQUIRE(M >= 1 && N >= 1 && K >= 1, "pk_w4a16_gemm: empty shape M=%d N=%d K=%d", M, N, K);
+  PK_REQUIRE(N % 8 == 0, "pk_w4a16_gemm: N=%d must be a multiple of 8 (one int32 word)", N);
+  PK_REQUIRE(K % 32 == 0, "pk_w4a16_gemm: K=%d must be a multiple of 32", K);
+  PK_REQUIRE(lda >= K && lda % 8 == 0 && aligned16(a),
+             "pk_w4a16_gemm: A rows must be 16-byte aligned (lda=%lld)", (long long)lda);
+  PK_REQUIRE(ldq >= N / 8, "pk_w4a16_gemm: ldq=%lld < N/8", (long long)ldq);
+  PK_REQUIRE(ldc >= N, "pk_w4a16_gemm: ldc < N");
+  PK_REQUIRE(c_dtype == PK_F32 || c_dtype == PK_F16 || c_dtype == PK_BF16,
+             "pk_w4a16_gemm: output dtype %d", c_dtype);
+  PK_REQUIRE(split_k >= 0, "pk_w4a16_gemm: split_k must be >= 0");
+  if (scales != nullptr) {
+    PK_REQUIRE(group_size >= 32 && group_size % 32 == 0 && K % group_size == 0,
+               "pk_w4a16_gemm: group_size=%d must be a multiple of 32 dividing K=%d",
+               group_size, K);
+    PK_REQUIRE(aligned16(scales), "pk_w4a16_gemm: scales must be 16-byte aligned");
+  }
+  return PK_OK;
+}
+
+struct W4Plan {
+  int kernel;
+  GemvPlan gemv;
+  GemmPlan gemm;
+};
+
+bool make_plan(int M, int N, int K, int group_size, bool has_gs, int split_k, W4Plan* pl) {
+  if (M <= 4 && gemv_plan(M, N, K, group_size, has_gs, split_k, &pl->gemv)) {
+    pl->kernel = kKernelGemv;
+    return true;
+  }
+  if (gemm_plan(M, N, K, group_size, has_gs, split_k, &pl->gemm)) {
+    pl->kernel = kKernelGemm;
+    return true;
+  }
+  return false;
+}
+
+size_t plan_ws(const W4Plan& pl, int M, int N) {
+  return pl.kernel == kKernelGemv ? gemv_workspace_bytes(pl.gemv, M, N)
+                                  : gemm_workspace_bytes(pl.gemm, M, N);
+}
+
+}  // namespace
+
+extern "C" int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_id,
+                             int* split_used) {
+  W4Plan pl;
+  const bool has_gs = group_size > 0;
+  if (!make_plan(M, N, K, has_gs ? group_size : K, has_gs, split_k, &pl)) {
+    set_error("pk_w4a16_plan: no kernel for M=%d N=%d K=%d group=%d split_k=%d", M, N, K,
+              group_size, split_k);
+    return PK_EUNSUPPORTED;
+  }
+  if (kernel_id) *kernel_id = pl.kernel;
+  if (split_used) *split_used = pl.kernel == kKernelGemv ? pl.gemv.split : pl.gemm.split;
+  return PK_OK;
+}
+
+extern "C" size_t pk_w4a16_workspace_bytes(int M, int N, int K, int group_size, int split_k) {
+  W4Plan pl;
+  const bool has_gs = group_size > 0;
+  if (!make_plan(M, N, K, has_gs ? group_size : K, has_gs, split_k, &pl)) return 0;
+  return plan_ws(pl, M, N);
+}
+
+extern "C" int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight, int64_t ldq,
+                             const void* scales, int group_size, float tensor_scale, void* c,
+                             int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_w4a16(a, lda, qweight, ldq, scales, group_size, c, c_dtype, ldc, M, N, K,
+                       split_k);
+  if (rc != PK_OK) return rc;
+  const bool has_gs = scales != nullptr;
+  const int group = has_gs ? group_size : K;
+  W4Plan pl;
+  if (!make_plan(M, N, K, group, has_gs, split_k, &pl)) {
+    set_error("pk_w4a16_gemm: split_k=%d does not divide K=%d into slices of whole groups "
+              "(group %d, multiple of 32 rows)", split_k, K, group);
+    return PK_EINVAL;
+  }
+  const size_t need = plan_ws(pl, M, N);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    set_error("pk_w4a16_gemm: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
+    return PK_EWORKSPACE;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (pl.kernel == kKernelGemv)
+    return gemv_launch(pl.gemv, a, lda, qweight, ldq, scales, group, tensor_scale, c, c_dtype,
+                       ldc, M, N, K, workspace, s);
+  return gemm_launch(pl.gemm, 1, a, lda, qweight, ldq, scales, group, tensor_scale, c, c_dtype,
+                     ldc, M, N, K, workspace, s);
+}
+
+extern "C" size_t pk_gemm_f16_workspace_bytes(int M, int N, int K, int split_k) {
+  GemmPlan pl;
+  if (!gemm_plan(M, N, K, K, false, split_k, &pl)) return 0;
+  return gemm_workspace_bytes(pl, M, N);
+}
+
+extern "C" int pk_gemm_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                           int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  PK_REQUIRE(a != nullptr && b != nullptr && c != nullptr, "pk_gemm_f16: null pointer");
+  PK_REQUIRE(M >= 1 && N >= 1 && K >= 1, "pk_gemm_f16: empty shape");
+  PK_REQUIRE(N % 8 == 0 && K % 32 == 0, "pk_gemm_f16: needs N %% 8 == 0 and K %% 32 == 0");
+  PK_REQUIRE(lda >= K && lda % 8 == 0 && aligned16(a), "pk_gemm_f16: A rows must be 16-byte aligned");
+  PK_REQUIRE(ldb >= N && ldb % 8 == 0 && aligned16(b), "pk_gemm_f16: B rows must be 16-byte aligned");
+  PK_REQUIRE(c_dtype == PK_F32 || c_dtype == PK_F16 || c_dtype == PK_BF16, "pk_gemm_f16: out dtype");
+  PK_REQUIRE(split_k >= 0, "pk_gemm_f16: split_k must be >= 0");
+  GemmPlan pl;
+  if (!gemm_plan(M, N, K, K, false, split_k, &pl)) {
+    set_error("pk_gemm_f16: split_k=%d must divide K=%d into slices that are multiples of 64",
+              split_k, K);
+    return PK_EINVAL;
+  }
+  const size_t need = gemm_workspace_bytes(pl, M, N);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    set_error("pk_gemm_f16: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
+    return PK_EWORKSPACE;
+  }
+  return gemm_launch(pl, 0, a, lda, b, ldb, nullptr, K, 1.0f, c, c_dtype, ldc, M, N, K, workspace,
+                     (hipStream_t)stream);
+}

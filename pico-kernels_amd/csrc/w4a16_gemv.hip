@@ -1,0 +1,350 @@
+// W4A16 skinny GEMV (M <= 4) with deterministic split-K -- the HBM-bound decode path.
+//
+// Computes C[m, n] = tensor_scale * sum_k A[m, k] * q[k, n] * S[k / G, n] for the packed
+// layout of gemm_int4.pack_int4_n (gemm_int4.py:65-72) viewed as int32 words: word j of
+// row k holds columns 8j..8j+7, nibble i = column 8j+i, two's complement.
+//
+// Work decomposition (one launch):
+//   grid.x = column tiles of 256 columns (32 words = 128 contiguous bytes per row),
+//   grid.y = split-K slices (contiguous K ranges of k_slice rows, as gemm_splitk.py:49-53).
+//   A workgroup is 8 x RL lanes: 8 lanes span the 128-byte row segment with one 16-byte load
+//   each (4 words = 32 columns per lane); RL row-lanes each own RPT consecutive rows per
+//   step. Every lane keeps 32 column accumulators per activation row.
+//
+// Dequantisation without a conversion instruction per nibble:
+//   * XOR each word with 0x88888888 turns the signed nibble v into u = v + 8 in [0, 15].
+//   * A byte permute gathers the same byte of rows k and k+1 into the low bytes of the two
+//     16-bit halves of one register; masking with 0x000F000F (or 0x00F000F0) leaves u in
+//     the mantissa of two fp16 *subnormals*, i.e. the values u * 2^-24 (or u * 2^-20).
+//   * v_dot2_f32_f16 multiplies that pair with the activation pair (x_k, x_k+1) and
+//     accumulates in fp32: products are exact (11-bit x 4-bit significands) and fp16
+//     subnormals are kept (the kernel's fp16 denormal mode is "preserve").
+//   * Per step the column sum is rescaled by 2^24 (2^20), the +8 offset is removed with
+//     -8 * sum(x) and the group scale is applied in fp32.
+//
+// Reduction: row-lanes inside a wave are folded with a reduce-scatter over lane masks
+// 32/16/8, waves through LDS. With split-K each slice writes an fp32 partial row and a
+// second small kernel (splitk_reduce_kernel) adds the slices in order 0..S-1. A kernel
+// boundary is the cheapest point where writes of every XCD's L2 become visible to all; a
+// last-workgroup handoff inside one kernel would need an L2 writeback and invalidate per
+// wave. There are no floating-point atomics, so the result is bitwise reproducible.
+#include "pk_internal.h"
+
+namespace pk {
+
+constexpr int kGemvCW = 8;          // lanes across a row segment
+constexpr int kGemvTileWords = 32;  // words per column tile
+constexpr int kGemvTileCols = 256;  // columns per column tile
+
+struct GemvParams {
+  const pk_half* a;
+  int64_t lda;
+  const uint32_t* qw;
+  int64_t ldq;
+  const pk_half* scales;  // (K/G, N) or null
+  int group;
+  float tensor_scale;
+  void* c;
+  int c_dtype;
+  int64_t ldc;
+  int M, N, K;
+  int split, k_slice;
+  int vec_ok;  // qweight rows are 16-byte aligned
+  float* partials;  // (split, M, N) fp32 when split > 1
+};
+
+__device__ __forceinline__ pk_half2 as_half2(uint32_t v) { return __builtin_bit_cast(pk_half2, v); }
+
+template <int MT, int RPT, int RL, bool HAS_GS>
+__global__ __launch_bounds__(kGemvCW* RL) void w4a16_gemv_kernel(GemvParams p) {
+  static_assert(RPT % 2 == 0 && RPT % 8 == 0, "RPT must be a multiple of 8");
+  constexpr int NT = kGemvCW * RL;
+  constexpr int NWAVES = (NT + 63) / 64;
+
+  const int t = threadIdx.x;
+  const int cl = t % kGemvCW, rl = t / kGemvCW;
+  const int tile = blockIdx.x, slice = blockIdx.y;
+  const int words_total = p.N >> 3;
+  const int word0 = tile * kGemvTileWords + cl * 4;
+  const int nvalid = max(0, min(4, words_total - word0));
+  const int k_begin = slice * p.k_slice;
+  const int k_end = min(k_begin + p.k_slice, p.K);
+  constexpr bool has_gs = HAS_GS;
+
+  float acc[MT][32];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int c = 0; c < 32; ++c) acc[m][c] = 0.0f;
+
+  for (int kb = k_begin + rl * RPT; kb < k_end; kb += RL * RPT) {
+    // ---- issue all loads of this step: activations and scales first, weights last ----
+    uint32_t xw[MT][RPT / 2];  // activation pairs (x_k, x_k+1) as packed fp16
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < p.M) {
+        const uint4* xa = reinterpret_cast<const uint4*>(p.a + (int64_t)m * p.lda + kb);
+#pragma unroll
+        for (int v = 0; v < RPT / 8; ++v) {
+          uint4 q = xa[v];
+          xw[m][4 * v + 0] = q.x; xw[m][4 * v + 1] = q.y;
+          xw[m][4 * v + 2] = q.z; xw[m][4 * v + 3] = q.w;
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < RPT / 2; ++v) xw[m][v] = 0u;
+      }
+    }
+    float sc[32];
+    if constexpr (has_gs) {
+      const int g = kb / p.group;
+      const pk_half* srow = p.scales + (int64_t)g * p.N + (int64_t)word0 * 8;
+      if (nvalid == 4) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          pk_half8 h = *reinterpret_cast<const pk_half8*>(srow + 8 * v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sc[8 * v + e] = (float)h[e];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 32; ++c) sc[c] = (c < 8 * nvalid) ? (float)srow[c] : 0.0f;
+      }
+    }
+
+    uint32_t w[RPT][4];
+    if (nvalid == 4 && p.vec_ok) {
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        uint4 v = *reinterpret_cast<const uint4*>(p.qw + (int64_t)(kb + r) * p.ldq + word0);
+        w[r][0] = v.x; w[r][1] = v.y; w[r][2] = v.z; w[r][3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < RPT; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          w[r][j] = (j < nvalid) ? p.qw[(int64_t)(kb + r) * p.ldq + word0 + j] : 0u;
+    }
+    // ---- dot products over the RPT rows ------------------------------------------------
+    float part[MT][32];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int c = 0; c < 32; ++c) part[m][c] = 0.0f;
+#pragma unroll
+    for (int r2 = 0; r2 < RPT / 2; ++r2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t w0 = w[2 * r2][j] ^ 0x88888888u;
+        const uint32_t w1 = w[2 * r2 + 1][j] ^ 0x88888888u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          // bytes: [w0.byte_b, 0, w1.byte_b, 0]
+          const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
+          const uint32_t pr = __builtin_amdgcn_perm(w1, w0, sel);
+          const pk_half2 lo = as_half2(pr & 0x000f000fu);  // column 8j+2b,   u * 2^-24
+          const pk_half2 hi = as_half2(pr & 0x00f000f0u);  // column 8j+2b+1, u * 2^-20
+          const int col = 8 * j + 2 * b;
+#pragma unroll
+          for (int m = 0; m < MT; ++m) {
+            const pk_half2 xv = as_half2(xw[m][r2]);
+            part[m][col] = __builtin_amdgcn_fdot2(lo, xv, part[m][col], false);
+            part[m][col + 1] = __builtin_amdgcn_fdot2(hi, xv, part[m][col + 1], false);
+          }
+        }
+      }
+    }
+    // ---- undo the encoding and apply the group scale -----------------------------------
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      float sx = 0.0f;
+      const pk_half2 ones = {(pk_half)1.0f, (pk_half)1.0f};
+#pragma unroll
+      for (int r2 = 0; r2 < RPT / 2; ++r2) sx = __builtin_amdgcn_fdot2(as_half2(xw[m][r2]), ones, sx, false);
+      const float off = -8.0f * sx;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) {
+        const float v = __builtin_fmaf(part[m][c], (c & 1) ? 1048576.0f : 16777216.0f, off);
+        if constexpr (has_gs) acc[m][c] = __builtin_fmaf(v, sc[c], acc[m][c]);
+        else acc[m][c] += v;
+      }
+    }
+  }
+
+  // ---- fold row-lanes inside the wave: reduce-scatter over lane masks 32, 16, 8 ---------
+  const int lane = t & 63;
+  float red4[MT][4];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    float v16[16], v8[8];
+    const bool u32 = (lane & 32) != 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float send = u32 ? acc[m][i] : acc[m][i + 16];
+      const float keep = u32 ? acc[m][i + 16] : acc[m][i];
+      v16[i] = keep + __shfl_xor(send, 32, 64);
+    }
+    const bool u16 = (lane & 16) != 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float send = u16 ? v16[i] : v16[i + 8];
+      const float keep = u16 ? v16[i + 8] : v16[i];
+      v8[i] = keep + __shfl_xor(send, 16, 64);
+    }
+    const bool u8 = (lane & 8) != 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float send = u8 ? v8[i] : v8[i + 4];
+      const float keep = u8 ? v8[i + 4] : v8[i];
+      red4[m][i] = keep + __shfl_xor(send, 8, 64);
+    }
+  }
+  // This lane now holds columns cbase..cbase+3 of its 32-column chunk.
+  const int cbase = ((lane >> 5) & 1) * 16 + ((lane >> 4) & 1) * 8 + ((lane >> 3) & 1) * 4;
+
+  // ---- fold waves through LDS ------------------------------------------------------------
+  __shared__ float red[NWAVES][MT][kGemvTileCols];
+  const int wave = t >> 6;
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][m][cl * 32 + cbase + i] = red4[m][i];
+  __syncthreads();
+
+  const int col_base = tile * kGemvTileCols;
+  const int M = p.M;
+  if (p.split == 1) {
+    for (int idx = t; idx < MT * kGemvTileCols; idx += NT) {
+      const int m = idx / kGemvTileCols, col = idx % kGemvTileCols;
+      if (m >= M || col_base + col >= p.N) continue;
+      float v = red[0][m][col];
+#pragma unroll
+      for (int wv = 1; wv < NWAVES; ++wv) v += red[wv][m][col];
+      store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + col_base + col, v * p.tensor_scale);
+    }
+    return;
+  }
+
+  // ---- split-K: publish this slice's partial row; splitk_reduce_kernel adds the slices ----
+  for (int idx = t; idx < MT * kGemvTileCols; idx += NT) {
+    const int m = idx / kGemvTileCols, col = idx % kGemvTileCols;
+    if (m >= M || col_base + col >= p.N) continue;
+    float v = red[0][m][col];
+#pragma unroll
+    for (int wv = 1; wv < NWAVES; ++wv) v += red[wv][m][col];
+    p.partials[((int64_t)slice * M + m) * p.N + col_base + col] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Planning: which (RPT, RL, split) to run.
+// ---------------------------------------------------------------------------------------
+static bool gemv_config_ok(int K, int group, bool has_gs, int split, int rpt) {
+  if (split < 1 || K % split) return false;
+  const int ks = K / split;
+  if (ks % rpt) return false;
+  if (has_gs && (group % rpt)) return false;
+  return true;
+}
+
+static int pick_rl(int k_slice, int rpt) {
+  const int steps = k_slice / rpt;  // row-lane steps available in one slice
+  if (steps >= 32) return 32;
+  if (steps >= 16) return 16;
+  return 8;
+}
+
+bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvPlan* out) {
+  if (M < 1 || M > 4 || N % 8 || K % 16) return false;
+  const int tiles = (int)cdiv(N, kGemvTileCols);
+  const int rpt_pref = (M <= 2) ? 16 : 8;
+  int rpts[2] = {rpt_pref, 8};
+  for (int ri = 0; ri < 2; ++ri) {
+    const int rpt = rpts[ri];
+    if (split_req > 0) {
+      if (!gemv_config_ok(K, group, has_gs, split_req, rpt)) continue;
+      const int ks = K / split_req;
+      *out = {rpt, pick_rl(ks, rpt), split_req, ks, tiles};
+      return true;
+    }
+    // Automatic: the smallest split that puts >= ~1024 waves in flight (4 per CU) with
+    // every row-lane busy, capped at 32 slices.
+    GemvPlan best{};
+    bool have = false;
+    for (int s = 1; s <= 32; s *= 2) {
+      if (!gemv_config_ok(K, group, has_gs, s, rpt)) continue;
+      const int ks = K / s;
+      const int rl = pick_rl(ks, rpt);
+      best = {rpt, rl, s, ks, tiles};
+      have = true;
+      const long waves = (long)tiles * s * (rl * kGemvCW / 64);
+      if (waves >= 1024 && ks <= rl * rpt) break;
+    }
+    if (have) {
+      *out = best;
+      return true;
+    }
+  }
+  return false;
+}
+
+size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N) {
+  if (pl.split <= 1) return 0;
+  return (size_t)pl.split * M * N * sizeof(float);
+}
+
+template <int MT, int RPT, int RL>
+static void launch_gemv_t(const GemvParams& p, int tiles, hipStream_t s) {
+  dim3 grid(tiles, p.split);
+  if (p.scales != nullptr) w4a16_gemv_kernel<MT, RPT, RL, true><<<grid, kGemvCW * RL, 0, s>>>(p);
+  else w4a16_gemv_kernel<MT, RPT, RL, false><<<grid, kGemvCW * RL, 0, s>>>(p);
+}
+
+template <int MT, int RPT>
+static void launch_gemv_rl(const GemvParams& p, int rl, int tiles, hipStream_t s) {
+  if (rl == 32) launch_gemv_t<MT, RPT, 32>(p, tiles, s);
+  else if (rl == 16) launch_gemv_t<MT, RPT, 16>(p, tiles, s);
+  else launch_gemv_t<MT, RPT, 8>(p, tiles, s);
+}
+
+template <int MT>
+static void launch_gemv_rpt(const GemvParams& p, int rpt, int rl, int tiles, hipStream_t s) {
+  if (rpt == 16) launch_gemv_rl<MT, 16>(p, rl, tiles, s);
+  else launch_gemv_rl<MT, 8>(p, rl, tiles, s);
+}
+
+int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
+                int64_t ldq, const void* scales, int group, float tensor_scale, void* c,
+                int c_dtype, int64_t ldc, int M, int N, int K, void* workspace,
+                hipStream_t s) {
+  GemvParams p;
+  p.a = reinterpret_cast<const pk_half*>(a);
+  p.lda = lda;
+  p.qw = qw;
+  p.ldq = ldq;
+  p.scales = reinterpret_cast<const pk_half*>(scales);
+  p.group = group > 0 ? group : K;
+  p.tensor_scale = tensor_scale;
+  p.c = c;
+  p.c_dtype = c_dtype;
+  p.ldc = ldc;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.split = pl.split;
+  p.k_slice = pl.k_slice;
+  p.vec_ok = ((reinterpret_cast<uintptr_t>(qw) & 15) == 0 && ldq % 4 == 0) ? 1 : 0;
+  p.partials = pl.split > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
+  switch (M) {
+    case 1: launch_gemv_rpt<1>(p, pl.rpt, pl.rl, pl.tiles, s); break;
+    case 2: launch_gemv_rpt<2>(p, pl.rpt, pl.rl, pl.tiles, s); break;
+    case 3: launch_gemv_rpt<3>(p, pl.rpt, pl.rl, pl.tiles, s); break;
+    default: launch_gemv_rpt<4>(p, pl.rpt, pl.rl, pl.tiles, s); break;
+  }
+  PK_LAUNCH_CHECK("w4a16 gemv");
+  if (pl.split > 1) return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);
+  return PK_OK;
+}
+
+}  // namespace pk

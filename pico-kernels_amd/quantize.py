@@ -1,0 +1,106 @@
+"""Round-to-nearest and GPTQ weight quantization on MI355X -- drop-in for the quantization
+primitives of the reference's ``quantize`` module.
+
+Reference entry points kept with their signatures (file:line in the reference repository):
+  * ``quantize_col(w, bits, group_size=None)``  quantize.py:42-60
+  * ``rtn_layer(w, bits, group_size=None)``     quantize.py:63-68
+  * ``gptq_layer(w, x, bits, damp=0.01, act_order=True, group_size=None)``
+                                                 quantize.py:71-115
+
+``quantize_col`` / ``rtn_layer`` run one HIP kernel (``pk_quantize_group``) that reproduces the
+reference's torch arithmetic bit for bit: fp32 for ``rtn_layer`` (which widens first) and the
+tensor's own dtype for ``quantize_col`` on an fp16/bf16 vector. ``gptq_layer`` keeps the
+reference's update rule (each column's rounding error is pushed onto the later columns with
+the fixed ratios ``H^-1[j, j+1:] / H^-1[j, j]``) but runs it on the GPU as a blocked
+("lazy batch") sweep: columns are quantized one by one inside a block of 128, the block's
+accumulated errors reach the remaining columns through one matmul. That is the same sum of
+rank-1 updates, reassociated, so results agree with the sequential form to fp32 rounding.
+
+The PicoLM perplexity driver of the reference (quantize.py:121-265) is not part of this path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import _pk
+
+__all__ = ["quantize_col", "rtn_layer", "gptq_layer"]
+
+_GPTQ_BLOCK = 128
+
+
+def quantize_col(w: torch.Tensor, bits: int, group_size: int | None = None) -> torch.Tensor:
+    """Symmetric round-to-nearest quantization of a column ``[out]`` (quantize.py:42-60).
+
+    ``group_size=None`` uses one scale for the whole vector; otherwise consecutive groups of
+    ``group_size`` elements share a scale (the last group may be shorter).
+    """
+    if bits >= 16:
+        return w
+    wg = _pk.to_gpu(w).reshape(-1, 1)
+    half_math = wg.dtype in (torch.float16, torch.bfloat16)
+    _, _, fake = _pk.quantize_group(wg, bits, group_size, half_math=half_math, want_qweight=False,
+                                    want_scales=False, want_fake=True, fake_dtype=w.dtype)
+    fake = fake.reshape(w.shape)
+    return fake if w.is_cuda else fake.to(w.device)
+
+
+def rtn_layer(w: torch.Tensor, bits: int, group_size: int | None = None) -> torch.Tensor:
+    """Naive round-to-nearest over every column -- the GPTQ baseline (quantize.py:63-68)."""
+    if bits >= 16:
+        return w.clone()
+    assert w.dim() == 2
+    wg = _pk.to_gpu(w)
+    _, _, fake = _pk.quantize_group(wg, bits, group_size, half_math=False, want_qweight=False,
+                                    want_scales=False, want_fake=True, fake_dtype=w.dtype)
+    return fake if w.is_cuda else fake.to(w.device)
+
+
+def gptq_layer(w: torch.Tensor, x: torch.Tensor, bits: int, damp: float = 0.01,
+               act_order: bool = True, group_size: int | None = None) -> torch.Tensor:
+    """GPTQ-quantize one linear layer ``w`` (``[out, in]``) given activations ``x`` (``[n, in]``).
+
+    Same algorithm as quantize.py:71-115 (Hessian ``X^T X / n`` with damping
+    ``damp * mean(diag)``, its inverse, optional activation ordering by ``diag(H)``, column
+    sweep with error feedback, un-permute). Output has ``w``'s dtype and device.
+    """
+    if bits >= 16:
+        return w.clone()
+    dev = _pk.gpu_device() if not w.is_cuda else w.device
+    W = w.to(dev).float()
+    X = x.to(dev).float()
+    out_dim, in_dim = W.shape
+    n = X.shape[0]
+
+    H = (X.t() @ X) / n
+    energy = torch.diagonal(H).clone()
+    H.diagonal().add_(damp * energy.mean())
+    Hinv = torch.linalg.inv(H)
+
+    order = None
+    if act_order:
+        order = torch.argsort(energy, descending=True)
+        W = W[:, order]
+        Hinv = Hinv[order][:, order]
+    # ratios[j, c] = Hinv[j, c] / Hinv[j, j] for c > j (strictly upper triangle).
+    ratios = torch.triu(Hinv / torch.diagonal(Hinv).unsqueeze(1), diagonal=1)
+
+    Q = W.clone()
+    for b0 in range(0, in_dim, _GPTQ_BLOCK):
+        b1 = min(b0 + _GPTQ_BLOCK, in_dim)
+        err = torch.empty((out_dim, b1 - b0), dtype=torch.float32, device=dev)
+        for j in range(b0, b1):
+            col = Q[:, j]
+            q = quantize_col(col, bits, group_size)
+            e = col - q
+            err[:, j - b0] = e
+            Q[:, j] = q
+            if j + 1 < b1:
+                Q[:, j + 1:b1].sub_(torch.outer(e, ratios[j, j + 1:b1]))
+        if b1 < in_dim:
+            Q[:, b1:].sub_(err @ ratios[b0:b1, b1:])
+
+    if order is not None:
+        Q = Q[:, torch.argsort(order)]
+    return Q.to(w.dtype).to(w.device)

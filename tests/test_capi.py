@@ -1,0 +1,98 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every declared symbol,
+plans the right kernels, and rejects bad arguments before launching anything."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import _pk
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "pico_kernels_amd.h"
+
+
+def _declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(pk_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_boundary():
+    syms = _declared_symbols()
+    for name in ("pk_w4a16_gemm", "pk_fp8_gemm", "pk_quantize_group", "pk_cast_e4m3", "pk_absmax",
+                 "pk_pack_int4", "pk_unpack_int4", "pk_quantize_int4", "pk_gemm_f16"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _pk.lib()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
+    assert set(_declared_symbols()) == set(_pk.EXPORTED_SYMBOLS)
+
+
+def test_version_and_error_string():
+    lib = _pk.lib()
+    assert lib.pk_version() >= 100
+    assert isinstance(lib.pk_last_error(), bytes)
+
+
+def test_w4a16_plans():
+    # headline decode shape: skinny GEMV, split chosen to fill the chip
+    kid, split = _pk.w4a16_plan(1, 11008, 4096, 128, 0)
+    assert kid == _pk.KERNEL_GEMV and split >= 4
+    for s in (1, 2, 4, 8, 16):
+        assert _pk.w4a16_plan(1, 11008, 4096, 128, s) == (_pk.KERNEL_GEMV, s)
+    # prefill: MFMA GEMM, no split needed at 2048 rows
+    assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (_pk.KERNEL_GEMM, 1)
+    assert _pk.w4a16_plan(128, 4096, 4096, 128, 0)[0] == _pk.KERNEL_GEMM
+    # per-tensor mode (group_size 0) for the drop-in int4_gemm
+    assert _pk.w4a16_plan(128, 512, 256, 0, 0)[0] == _pk.KERNEL_GEMM
+    # slices may cut a group (scales are applied per 16-row chunk) ...
+    assert _pk.w4a16_plan(1, 4096, 4096, 128, 64) == (_pk.KERNEL_GEMV, 64)
+    # ... but a split must divide K into multiples of the row chunk
+    with pytest.raises(_pk.PicoKernelsError):
+        _pk.w4a16_plan(1, 4096, 4096, 128, 3)
+    with pytest.raises(_pk.PicoKernelsError):
+        _pk.w4a16_plan(64, 4096, 4096, 128, 128)
+
+
+def test_workspace_sizes():
+    lib = _pk.lib()
+    assert lib.pk_w4a16_workspace_bytes(2048, 4096, 4096, 128, 1) == 0
+    n = lib.pk_w4a16_workspace_bytes(1, 11008, 4096, 128, 8)
+    assert n >= 8 * 11008 * 4
+    assert lib.pk_gemm_f16_workspace_bytes(512, 512, 1024, 4) >= 4 * 512 * 512 * 4
+
+
+@pytest.mark.parametrize("args,code", [
+    # N not a multiple of 8
+    (dict(M=1, N=12, K=64), _pk.PK_EINVAL),
+    # K not a multiple of 32
+    (dict(M=1, N=64, K=48), _pk.PK_EINVAL),
+    # null A
+    (dict(M=1, N=64, K=64, a=0), _pk.PK_EINVAL),
+])
+def test_w4a16_argument_errors(args, code):
+    lib = _pk.lib()
+    M, N, K = args["M"], args["N"], args["K"]
+    a = args.get("a", 256)  # a fake, aligned, never-dereferenced address
+    rc = lib.pk_w4a16_gemm(a, K, 256, N // 8 or 1, None, 0, 1.0, 256, _pk.PK_F32, N, M, N, K, 0,
+                           None, 0, None)
+    assert rc == code
+    assert lib.pk_last_error()
+
+
+def test_fp8_argument_errors():
+    lib = _pk.lib()
+    rc = lib.pk_fp8_gemm(256, 100, 256, 100, 0, 1.0, 256, _pk.PK_F32, 100, 4, 100, 100, None)
+    assert rc == _pk.PK_EINVAL and b"multiple of 128" in lib.pk_last_error()
+
+
+def test_product_modules_never_import_the_oracle():
+    for f in (ROOT / "pico-kernels_amd").glob("*.py"):
+        src = f.read_text()
+        assert not re.search(r"^\s*(import|from)\s+oracle\b", src, re.M), f.name

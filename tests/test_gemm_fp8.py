@@ -1,0 +1,151 @@
+"""fp8 (OCP e4m3) parity on the GPU: the drop-in gemm_fp8 API.
+
+  * quantize: bit for bit against the reference's golden vectors, and the cast kernel against
+    the oracle's encoder over every fp16 value;
+  * matmul: against the closed form (a8.float() @ b8.float()) * out_scale of the reference,
+    and the fp8-vs-fp32 error within 0.1 percentage points of that closed form's own error.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import _pk
+import gemm_fp8
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+ERR_PP = 1e-3  # |err_gpu - err_reference| on the fp8-vs-fp32 relative Frobenius error
+# The fp8 MFMA adds its 128 products per lane-group with a reduced-precision internal adder
+# (about 2^-15 relative observed), so its result sits ~1e-5 from the exact fp32 closed form.
+CLOSED_FORM_TOL = 1e-4
+
+
+def _gen(seed: int) -> torch.Generator:
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def _u8(t: torch.Tensor) -> np.ndarray:
+    return t.view(torch.uint8).cpu().numpy()
+
+
+# ---------------------------------------------------------------------------------------
+# the reference's own tests, with CPU-seeded inputs
+# ---------------------------------------------------------------------------------------
+def test_fp8_gemm_accuracy(cuda):
+    a = torch.randn(512, 512, generator=_gen(0)).half().to(cuda)
+    b = torch.randn(512, 512, generator=_gen(1)).half().to(cuda)
+    c = gemm_fp8.fp8_gemm(a, b)
+    ref = a.float() @ b.float()
+    rel = torch.norm(c - ref) / torch.norm(ref)
+    assert rel.item() < 0.10, f"rel Frobenius err {rel.item():.4f} too high for fp8"
+
+
+def test_fp8_gemm_output_dtype_is_fp32(cuda):
+    a = torch.randn(256, 256, generator=_gen(2)).half().to(cuda)
+    b = torch.randn(256, 256, generator=_gen(3)).half().to(cuda)
+    assert gemm_fp8.fp8_gemm(a, b).dtype == torch.float32
+
+
+def test_quantize_roundtrip(cuda):
+    x = torch.randn(256, 256, generator=_gen(1)).half().to(cuda)
+    x8, scale = gemm_fp8.quantize(x)
+    back = x8.to(torch.float32) / scale
+    rel = torch.norm(back - x.float()) / torch.norm(x.float())
+    assert rel.item() < 0.05, f"quantize round-trip rel err {rel.item():.4f}"
+
+
+def test_e4m3_max_constant():
+    assert gemm_fp8._E4M3_MAX == 448.0
+
+
+# ---------------------------------------------------------------------------------------
+# bit-exact casts
+# ---------------------------------------------------------------------------------------
+def test_quantize_golden(golden, cuda):
+    arrays, meta = golden
+    for name in ("fp8_f16_n01", "fp8_f16_wide", "fp8_f32"):
+        x = torch.from_numpy(arrays[name + "_in"]).to(cuda)
+        x8, scale = gemm_fp8.quantize(x)
+        assert x8.dtype == torch.float8_e4m3fn
+        assert scale == meta["cases"][name]["scale"], name
+        assert np.array_equal(_u8(x8), arrays[name + "_out"]), name
+
+
+def test_cast_every_fp16_value(cuda):
+    x16 = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    for scale in (1.0, 0.37, 3.0):
+        out = _pk.cast_e4m3(x16.to(cuda), scale)
+        with np.errstate(over="ignore"):
+            y = (x16.float().numpy() * np.float32(scale)).astype(np.float16).astype(np.float32)
+        expect = oracle.e4m3_from_f32(y)
+        assert np.array_equal(_u8(out), expect), f"scale {scale}"
+
+
+def test_cast_fp32_samples(cuda):
+    bits = torch.randint(-2**31, 2**31 - 1, (1 << 20,), generator=_gen(9), dtype=torch.int64)
+    x = bits.to(torch.int32).view(torch.float32)
+    out = _pk.cast_e4m3(x.to(cuda), 1.0)
+    assert np.array_equal(_u8(out), oracle.e4m3_from_f32(x.numpy()))
+
+
+# ---------------------------------------------------------------------------------------
+# matmul parity
+# ---------------------------------------------------------------------------------------
+def _fp8_case(M, K, N, seed, cuda):
+    a = torch.randn(M, K, generator=_gen(seed)).half()
+    b = torch.randn(K, N, generator=_gen(seed + 1)).half()
+    a8, sa = gemm_fp8.quantize(a.to(cuda))
+    b8, sb = gemm_fp8.quantize(b.to(cuda))
+    return a, b, a8, sa, b8, sb
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 256, 256), (100, 384, 264), (1, 128, 8), (513, 1024, 520),
+                                   (2048, 2048, 2048)])
+def test_fp8_gemm_matches_closed_form(M, K, N, cuda):
+    a, b, a8, sa, b8, sb = _fp8_case(M, K, N, M + K + N, cuda)
+    c = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb)
+    assert c.dtype == torch.float32 and c.shape == (M, N)
+    ref8 = oracle.fp8_gemm_ref(_u8(a8), sa, _u8(b8), sb)
+    assert oracle.rel_fro(c.cpu().numpy(), ref8) < CLOSED_FORM_TOL
+    ref32 = a.float().numpy() @ b.float().numpy()
+    err_gpu = oracle.rel_fro(c.cpu().numpy(), ref32)
+    err_ref = oracle.rel_fro(ref8, ref32)
+    assert abs(err_gpu - err_ref) <= ERR_PP, (err_gpu, err_ref)
+
+
+def test_fp8_full_size_4096(cuda):
+    """BASELINE config: M=N=K=4096, fp16 inputs N(0,1), fp16 output; error vs fp32."""
+    M = K = N = 4096
+    a, b, a8, sa, b8, sb = _fp8_case(M, K, N, 4096, cuda)
+    c16 = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb, out_dtype=torch.float16)
+    c32 = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb)
+    assert torch.equal(c16, c32.half())
+    ref8 = oracle.fp8_gemm_ref(_u8(a8), sa, _u8(b8), sb)
+    assert oracle.rel_fro(c32.cpu().numpy(), ref8) < CLOSED_FORM_TOL
+    ref32 = a.float().numpy() @ b.float().numpy()
+    err_gpu = oracle.rel_fro(c16.float().cpu().numpy(), ref32)
+    err_ref = oracle.rel_fro(ref8, ref32)
+    assert abs(err_gpu - err_ref) <= ERR_PP, (err_gpu, err_ref)
+    assert 0.02 < err_gpu < 0.06  # the ~3.7% the reference reports for N(0,1) inputs
+
+
+def test_fp8_transposed_b_layout(cuda):
+    a, b, a8, sa, b8, sb = _fp8_case(256, 512, 384, 77, cuda)
+    c0 = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb)
+    bt = b8.t().contiguous()  # (N, K) buffer
+    c1 = gemm_fp8.fp8_gemm_precast(a8, sa, bt.t(), sb)  # (K, N) view of it
+    assert torch.equal(c0, c1)
+
+
+def test_fp8_host_inputs_quantize(cuda):
+    x = torch.randn(64, 128, generator=_gen(5)).half()
+    x8, scale = gemm_fp8.quantize(x)
+    assert not x8.is_cuda
+    b, s = oracle.fp8_quantize(x.numpy())
+    assert s == scale and np.array_equal(x8.view(torch.uint8).numpy(), b)

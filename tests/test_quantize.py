@@ -1,0 +1,116 @@
+"""Quantization primitives on the GPU (drop-in quantize.quantize_col / rtn_layer / gptq_layer).
+
+quantize_col and rtn_layer must reproduce the reference bit for bit (golden vectors written
+by the reference's own functions); gptq_layer is fp32 linear algebra and is held to a
+tolerance plus the reference's own invariants.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import quantize
+from quantize import gptq_layer, quantize_col, rtn_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint8)
+
+
+def test_quantize_col_golden(golden, cuda):
+    arrays, meta = golden
+    for name, case in meta["cases"].items():
+        if case["fn"] != "quantize.quantize_col":
+            continue
+        w = torch.from_numpy(arrays[name + "_in"])
+        for dev in (cuda, torch.device("cpu")):  # host tensors are staged through the GPU
+            out = quantize_col(w.to(dev), case["bits"], case["group_size"])
+            assert out.device.type == dev.type and out.dtype == w.dtype
+            assert np.array_equal(_bits(out), arrays[name + "_out"].view(np.uint8)), name
+
+
+def test_rtn_layer_golden(golden, cuda):
+    arrays, meta = golden
+    for name, case in meta["cases"].items():
+        if case["fn"] != "quantize.rtn_layer":
+            continue
+        w = torch.from_numpy(arrays[name + "_in"]).to(cuda)
+        out = rtn_layer(w, case["bits"], case["group_size"])
+        assert out.dtype == w.dtype
+        assert np.array_equal(_bits(out), arrays[name + "_out"].view(np.uint8)), name
+
+
+def test_quantize_col_group_size_matches_manual(cuda):
+    """The reference's test (tests/test_quantize.py:35-42)."""
+    g = torch.Generator()
+    g.manual_seed(1)
+    w = torch.randn(64, generator=g)
+    q = quantize_col(w.to(cuda), 4, group_size=16).cpu()
+    for s in range(0, 64, 16):
+        scale = w[s:s + 16].abs().max() / 7.0
+        expected = torch.clamp(torch.round(w[s:s + 16] / scale), -7, 7) * scale
+        assert torch.allclose(q[s:s + 16], expected, atol=1e-5)
+
+
+def test_gptq_golden(golden, cuda):
+    arrays, meta = golden
+    W = torch.from_numpy(arrays["gptq_w"])
+    X = torch.from_numpy(arrays["gptq_x"])
+    for name, case in meta["cases"].items():
+        if case["fn"] != "quantize.gptq_layer":
+            continue
+        out = gptq_layer(W.to(cuda), X.to(cuda), case["bits"], act_order=case["act_order"],
+                         group_size=case["group_size"])
+        close = np.isclose(out.cpu().numpy(), arrays[name + "_out"], atol=1e-4, rtol=1e-4)
+        assert close.mean() > 0.99, f"{name}: {(~close).sum()} of {close.size} differ"
+
+
+def test_gptq_act_order_is_permutation_consistent(cuda):
+    """The reference's test (tests/test_quantize.py:15-32)."""
+    g = torch.Generator()
+    g.manual_seed(0)
+    W = torch.randn(64, 32, generator=g)
+    X = torch.randn(16, 32, generator=g)
+    X[:, :8] *= 4.0
+    w_ao = gptq_layer(W, X, 4, act_order=True)
+    H = X.t() @ X / X.shape[0]
+    order = torch.argsort(torch.diag(H), descending=True)
+    w_manual = gptq_layer(W[:, order], X[:, order], 4, act_order=False)[:, torch.argsort(order)]
+    assert torch.allclose(w_ao, w_manual, atol=1e-5)
+
+
+def test_gptq_beats_rtn_at_4bit(cuda):
+    """The reference's test (tests/test_quantize.py:45-53)."""
+    g = torch.Generator()
+    g.manual_seed(2)
+    W = torch.randn(128, 256, generator=g) * 0.1
+    X = torch.randn(64, 256, generator=g)
+
+    def mse(wq):
+        return ((X @ wq.T - X @ W.T) ** 2).mean().item()
+
+    assert mse(gptq_layer(W, X, 4)) < mse(rtn_layer(W, 4))
+
+
+def test_gptq_blocked_sweep_matches_sequential_oracle(cuda):
+    """More columns than one 128-column block: the blocked GPU sweep equals the sequential
+    column-by-column oracle to fp32 rounding."""
+    rng = np.random.default_rng(11)
+    W = (rng.standard_normal((48, 300)) * 0.1).astype(np.float32)
+    X = rng.standard_normal((96, 300)).astype(np.float32)
+    ours = gptq_layer(torch.from_numpy(W).to(cuda), torch.from_numpy(X).to(cuda), 4).cpu().numpy()
+    ref = oracle.gptq_layer(W, X, 4)
+    close = np.isclose(ours, ref, atol=1e-4, rtol=1e-3)
+    assert close.mean() > 0.99
+    assert oracle.rel_fro(ours, ref) < 1e-3
+
+
+def test_bits16_passthrough(cuda):
+    w = torch.randn(8, 4)
+    assert torch.equal(rtn_layer(w, 16), w) and rtn_layer(w, 16) is not w
+    assert quantize_col(w[:, 0], 16) is w[:, 0] or torch.equal(quantize_col(w[:, 0], 16), w[:, 0])
