@@ -142,6 +142,20 @@ int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight, int64_t l
 int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_id,
                   int* split_used);
 
+/* The two phases of a split-K pk_w4a16_gemm, for callers that reduce elsewhere (for example
+ * across devices) or time the phases separately. pk_w4a16_gemm_partials writes the fp32
+ * partial sums of every slice to `partials`, laid out (split, M, N) -- the per-slice products
+ * of gemm_splitk.gemm_splitk_kernel (gemm_splitk.py:26-61) before its atomic add -- and
+ * pk_splitk_reduce forms C = scale * sum over slices in slice order 0..split-1, the ordered
+ * replacement of that atomic add (gemm_splitk.py:64). `split` must be the effective split of
+ * pk_w4a16_plan (>= 2); partials_bytes >= split * M * N * 4. */
+int pk_w4a16_gemm_partials(const void* a, int64_t lda, const uint32_t* qweight, int64_t ldq,
+                           const void* scales, int group_size, float* partials,
+                           size_t partials_bytes, int M, int N, int K, int split_k,
+                           void* stream);
+int pk_splitk_reduce(const float* partials, int split, int M, int N, float scale, void* c,
+                     int c_dtype, int64_t ldc, void* stream);
+
 /* ------------------------------------------------------------------------------------- */
 /* Dense fp16 matmul with deterministic split-K                                          */
 /* ------------------------------------------------------------------------------------- */

@@ -52,6 +52,9 @@ _SIGNATURES = {
                              ctypes.POINTER(_i32)]),
     "pk_w4a16_gemm": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
                              _i32, _i32, _vp, _sz, _vp]),
+    "pk_w4a16_gemm_partials": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _vp, _sz, _i32, _i32, _i32,
+                                      _i32, _vp]),
+    "pk_splitk_reduce": (_i32, [_vp, _i32, _i32, _i32, _f32, _vp, _i32, _i64, _vp]),
     "pk_gemm_f16_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "pk_gemm_f16": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp,
                            _sz, _vp]),
@@ -244,6 +247,31 @@ def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | No
         a.data_ptr(), a.stride(0), qweight.data_ptr(), qweight.stride(0), ptr(scales), g,
         float(tensor_scale), out.data_ptr(), pk_dtype(out.dtype), out.stride(0), M, N, K,
         int(split_k), ptr(ws), 0 if ws is None else ws.numel(), stream_of(a)), "pk_w4a16_gemm")
+    return out
+
+
+def w4a16_gemm_partials(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | None,
+                        group_size: int, split_k: int, partials: torch.Tensor | None = None
+                        ) -> torch.Tensor:
+    """Per-slice fp32 partial sums (split, M, N) of a split-K W4A16 matmul."""
+    M, K = a.shape
+    N = qweight.shape[1] * 8
+    g = int(group_size) if scales is not None else 0
+    kid, split = w4a16_plan(M, N, K, g, int(split_k))
+    if partials is None:
+        partials = torch.empty((split, M, N), dtype=torch.float32, device=a.device)
+    _check(lib().pk_w4a16_gemm_partials(
+        a.data_ptr(), a.stride(0), qweight.data_ptr(), qweight.stride(0), ptr(scales), g,
+        partials.data_ptr(), partials.numel() * 4, M, N, K, int(split_k), stream_of(a)),
+        "pk_w4a16_gemm_partials")
+    return partials
+
+
+def splitk_reduce(partials: torch.Tensor, scale: float, out: torch.Tensor) -> torch.Tensor:
+    split, M, N = partials.shape
+    _check(lib().pk_splitk_reduce(partials.data_ptr(), split, M, N, float(scale), out.data_ptr(),
+                                  pk_dtype(out.dtype), out.stride(0), stream_of(partials)),
+           "pk_splitk_reduce")
     return out
 
 

@@ -13,9 +13,12 @@ struct GemvPlan {
 };
 bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvPlan* out);
 size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N);
+// Launches the GEMV; with split > 1 the slices' partials go to `workspace` and, unless
+// partials_only, the ordered reduction into C follows.
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
                 const void* scales, int group, float tensor_scale, void* c, int c_dtype,
-                int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s);
+                int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
+                bool partials_only = false);
 
 struct GemmCfg {
   int bm, bn, wm, wn;
@@ -28,6 +31,7 @@ bool gemm_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemmP
 size_t gemm_workspace_bytes(const GemmPlan& pl, int M, int N);
 int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const void* b,
                 int64_t ldb, const void* scales, int group, float tensor_scale, void* c,
-                int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s);
+                int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
+                bool partials_only = false);
 
 }  // namespace pk

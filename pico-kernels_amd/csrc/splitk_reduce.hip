@@ -7,32 +7,61 @@
 
 namespace pk {
 
+// One thread per 4 consecutive outputs; the S slice loads are unrolled so they are all in
+// flight at once (the kernel is one memory round trip, not S of them).
+template <int S>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partials,
-                                                            int S, int M, int N, float scale,
+                                                            int M, int N, float scale,
                                                             void* __restrict__ c, int c_dtype,
                                                             int64_t ldc) {
-  const int64_t plane = (int64_t)M * N;
-  const int64_t quads = plane / 4;  // N % 8 == 0, so rows hold whole quads
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += stride) {
-    const pk_f4* src = reinterpret_cast<const pk_f4*>(partials) + q;
-    pk_f4 v = __builtin_nontemporal_load(src);
-    for (int s = 1; s < S; ++s) v += __builtin_nontemporal_load(src + s * (plane / 4));
-    const int64_t e = q * 4;
-    const int64_t m = e / N, n = e - m * N;
-    const int64_t o = m * ldc + n;
+  const int64_t plane4 = (int64_t)M * N / 4;  // N % 8 == 0, so rows hold whole quads
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= plane4) return;
+  const pk_f4* src = reinterpret_cast<const pk_f4*>(partials) + q;
+  pk_f4 part[S];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i] * scale);
-  }
+  for (int s = 0; s < S; ++s) part[s] = __builtin_nontemporal_load(src + s * plane4);
+  pk_f4 v = part[0];
+#pragma unroll
+  for (int s = 1; s < S; ++s) v += part[s];
+  const int64_t e = q * 4;
+  const int64_t m = e / N, n = e - m * N;
+  const int64_t o = m * ldc + n;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i] * scale);
+}
+
+// Generic slice count: the same fixed order, loads in batches of 8.
+__global__ __launch_bounds__(256) void splitk_reduce_any_kernel(const float* __restrict__ partials,
+                                                                int S, int M, int N, float scale,
+                                                                void* __restrict__ c, int c_dtype,
+                                                                int64_t ldc) {
+  const int64_t plane4 = (int64_t)M * N / 4;
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= plane4) return;
+  const pk_f4* src = reinterpret_cast<const pk_f4*>(partials) + q;
+  pk_f4 v = __builtin_nontemporal_load(src);
+  for (int s = 1; s < S; ++s) v += __builtin_nontemporal_load(src + s * plane4);
+  const int64_t e = q * 4;
+  const int64_t m = e / N, n = e - m * N;
+  const int64_t o = m * ldc + n;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i] * scale);
 }
 
 int splitk_reduce(const float* partials, int S, int M, int N, float scale, void* c, int c_dtype,
                   int64_t ldc, hipStream_t s) {
   const int64_t quads = (int64_t)M * N / 4;
-  int64_t blocks = cdiv(quads, 256);
-  if (blocks > 4096) blocks = 4096;
-  if (blocks < 1) blocks = 1;
-  splitk_reduce_kernel<<<(unsigned)blocks, 256, 0, s>>>(partials, S, M, N, scale, c, c_dtype, ldc);
+  const unsigned blocks = (unsigned)cdiv(quads, 256);
+  switch (S) {
+    case 2: splitk_reduce_kernel<2><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
+    case 4: splitk_reduce_kernel<4><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
+    case 8: splitk_reduce_kernel<8><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
+    case 16: splitk_reduce_kernel<16><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
+    case 32: splitk_reduce_kernel<32><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
+    default:
+      splitk_reduce_any_kernel<<<blocks, 256, 0, s>>>(partials, S, M, N, scale, c, c_dtype, ldc);
+  }
   PK_LAUNCH_CHECK("split-K reduce");
   return PK_OK;
 }

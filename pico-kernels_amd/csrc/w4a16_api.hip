@@ -140,3 +140,43 @@ extern "C" int pk_gemm_f16(const void* a, int64_t lda, const void* b, int64_t ld
   return gemm_launch(pl, 0, a, lda, b, ldb, nullptr, K, 1.0f, c, c_dtype, ldc, M, N, K, workspace,
                      (hipStream_t)stream);
 }
+
+extern "C" int pk_w4a16_gemm_partials(const void* a, int64_t lda, const uint32_t* qweight,
+                                      int64_t ldq, const void* scales, int group_size,
+                                      float* partials, size_t partials_bytes, int M, int N, int K,
+                                      int split_k, void* stream) {
+  int rc = check_w4a16(a, lda, qweight, ldq, scales, group_size, partials, PK_F32, N, M, N, K,
+                       split_k);
+  if (rc != PK_OK) return rc;
+  const bool has_gs = scales != nullptr;
+  const int group = has_gs ? group_size : K;
+  W4Plan pl;
+  if (!make_plan(M, N, K, group, has_gs, split_k, &pl)) {
+    set_error("pk_w4a16_gemm_partials: no plan for split_k=%d, K=%d", split_k, K);
+    return PK_EINVAL;
+  }
+  const int split = pl.kernel == kKernelGemv ? pl.gemv.split : pl.gemm.split;
+  PK_REQUIRE(split >= 2, "pk_w4a16_gemm_partials: the plan has no split (split=%d)", split);
+  const size_t need = plan_ws(pl, M, N);
+  if (partials_bytes < need) {
+    set_error("pk_w4a16_gemm_partials: %zu bytes of partials needed (got %zu)", need, partials_bytes);
+    return PK_EWORKSPACE;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (pl.kernel == kKernelGemv)
+    return gemv_launch(pl.gemv, a, lda, qweight, ldq, scales, group, 1.0f, nullptr, PK_F32, N, M,
+                       N, K, partials, s, true);
+  return gemm_launch(pl.gemm, 1, a, lda, qweight, ldq, scales, group, 1.0f, nullptr, PK_F32, N, M,
+                     N, K, partials, s, true);
+}
+
+extern "C" int pk_splitk_reduce(const float* partials, int split, int M, int N, float scale,
+                                void* c, int c_dtype, int64_t ldc, void* stream) {
+  PK_REQUIRE(partials != nullptr && c != nullptr, "pk_splitk_reduce: null pointer");
+  PK_REQUIRE(split >= 1 && M >= 1 && N >= 1 && N % 8 == 0, "pk_splitk_reduce: bad shape");
+  PK_REQUIRE(ldc >= N, "pk_splitk_reduce: ldc < N");
+  PK_REQUIRE(c_dtype == PK_F32 || c_dtype == PK_F16 || c_dtype == PK_BF16,
+             "pk_splitk_reduce: output dtype %d", c_dtype);
+  PK_REQUIRE((reinterpret_cast<uintptr_t>(partials) & 15) == 0, "pk_splitk_reduce: partials alignment");
+  return splitk_reduce(partials, split, M, N, scale, c, c_dtype, ldc, (hipStream_t)stream);
+}

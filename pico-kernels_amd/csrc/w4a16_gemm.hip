@@ -346,7 +346,8 @@ static int launch_mode(const GemmPlan& pl, const GemmParams& p, hipStream_t s) {
 
 int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const void* b,
                 int64_t ldb, const void* scales, int group, float tensor_scale, void* c,
-                int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s) {
+                int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
+                bool partials_only) {
   GemmParams p;
   p.a = reinterpret_cast<const pk_half*>(a);
   p.lda = lda;
@@ -367,7 +368,7 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
   p.tiles_n = pl.tiles_n;
   p.partials = pl.split > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
   int rc = bmode == kBInt4 ? launch_mode<kBInt4>(pl, p, s) : launch_mode<kBF16Dense>(pl, p, s);
-  if (rc != PK_OK || pl.split <= 1) return rc;
+  if (rc != PK_OK || pl.split <= 1 || partials_only) return rc;
   return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);
 }
 

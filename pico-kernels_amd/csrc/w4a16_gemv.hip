@@ -49,13 +49,17 @@ struct GemvParams {
   int64_t ldc;
   int M, N, K;
   int split, k_slice;
-  int vec_ok;  // qweight rows are 16-byte aligned
+  int vec_ok;  // N % 32 == 0 and 16-byte aligned rows: whole-uint4 loads everywhere
   float* partials;  // (split, M, N) fp32 when split > 1
 };
 
 __device__ __forceinline__ pk_half2 as_half2(uint32_t v) { return __builtin_bit_cast(pk_half2, v); }
 
-template <int MT, int RPT, int RL, bool HAS_GS>
+// VEC: every lane owns 4 whole words with 16-byte aligned rows (N % 32 == 0), so weight
+// loads need no per-lane branch. Loads are never predicated in the hot loop: a branch
+// between a load and its first use makes the compiler wait for *all* outstanding loads at
+// the join, which serialises memory and compute.
+template <int MT, int RPT, int RL, bool HAS_GS, bool VEC>
 __global__ __launch_bounds__(kGemvCW* RL) void w4a16_gemv_kernel(GemvParams p) {
   static_assert(RPT % 2 == 0 && RPT % 8 == 0, "RPT must be a multiple of 8");
   constexpr int NT = kGemvCW * RL;
@@ -66,7 +70,6 @@ __global__ __launch_bounds__(kGemvCW* RL) void w4a16_gemv_kernel(GemvParams p) {
   const int tile = blockIdx.x, slice = blockIdx.y;
   const int words_total = p.N >> 3;
   const int word0 = tile * kGemvTileWords + cl * 4;
-  const int nvalid = max(0, min(4, words_total - word0));
   const int k_begin = slice * p.k_slice;
   const int k_end = min(k_begin + p.k_slice, p.K);
   constexpr bool has_gs = HAS_GS;
@@ -78,54 +81,50 @@ __global__ __launch_bounds__(kGemvCW* RL) void w4a16_gemv_kernel(GemvParams p) {
     for (int c = 0; c < 32; ++c) acc[m][c] = 0.0f;
 
   for (int kb = k_begin + rl * RPT; kb < k_end; kb += RL * RPT) {
-    // ---- issue all loads of this step: activations and scales first, weights last ----
+    // ---- issue all loads of this step: activations, weights in row order, then scales ----
     uint32_t xw[MT][RPT / 2];  // activation pairs (x_k, x_k+1) as packed fp16
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      if (m < p.M) {
-        const uint4* xa = reinterpret_cast<const uint4*>(p.a + (int64_t)m * p.lda + kb);
+      // rows past M re-read row M-1; their results are never stored
+      const uint4* xa = reinterpret_cast<const uint4*>(p.a + (int64_t)min(m, p.M - 1) * p.lda + kb);
 #pragma unroll
-        for (int v = 0; v < RPT / 8; ++v) {
-          uint4 q = xa[v];
-          xw[m][4 * v + 0] = q.x; xw[m][4 * v + 1] = q.y;
-          xw[m][4 * v + 2] = q.z; xw[m][4 * v + 3] = q.w;
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < RPT / 2; ++v) xw[m][v] = 0u;
+      for (int v = 0; v < RPT / 8; ++v) {
+        const uint4 q = xa[v];
+        xw[m][4 * v + 0] = q.x; xw[m][4 * v + 1] = q.y;
+        xw[m][4 * v + 2] = q.z; xw[m][4 * v + 3] = q.w;
       }
+    }
+    uint32_t w[RPT][4];
+    if constexpr (VEC) {
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p.qw + (int64_t)(kb + r) * p.ldq + word0);
+        w[r][0] = v.x; w[r][1] = v.y; w[r][2] = v.z; w[r][3] = v.w;
+      }
+    } else {
+      const int wlast = words_total - 1;
+#pragma unroll
+      for (int r = 0; r < RPT; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[r][j] = p.qw[(int64_t)(kb + r) * p.ldq + min(word0 + j, wlast)];
     }
     float sc[32];
     if constexpr (has_gs) {
       const int g = kb / p.group;
-      const pk_half* srow = p.scales + (int64_t)g * p.N + (int64_t)word0 * 8;
-      if (nvalid == 4) {
+      const pk_half* srow = p.scales + (int64_t)g * p.N;
+      if constexpr (VEC) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          pk_half8 h = *reinterpret_cast<const pk_half8*>(srow + 8 * v);
+          const pk_half8 h = *reinterpret_cast<const pk_half8*>(srow + (int64_t)word0 * 8 + 8 * v);
 #pragma unroll
           for (int e = 0; e < 8; ++e) sc[8 * v + e] = (float)h[e];
         }
       } else {
 #pragma unroll
-        for (int c = 0; c < 32; ++c) sc[c] = (c < 8 * nvalid) ? (float)srow[c] : 0.0f;
+        for (int c = 0; c < 32; ++c) sc[c] = (float)srow[min(word0 * 8 + c, p.N - 1)];
       }
     }
 
-    uint32_t w[RPT][4];
-    if (nvalid == 4 && p.vec_ok) {
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        uint4 v = *reinterpret_cast<const uint4*>(p.qw + (int64_t)(kb + r) * p.ldq + word0);
-        w[r][0] = v.x; w[r][1] = v.y; w[r][2] = v.z; w[r][3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < RPT; ++r)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          w[r][j] = (j < nvalid) ? p.qw[(int64_t)(kb + r) * p.ldq + word0 + j] : 0u;
-    }
     // ---- dot products over the RPT rows ------------------------------------------------
     float part[MT][32];
 #pragma unroll
@@ -258,7 +257,7 @@ static int pick_rl(int k_slice, int rpt) {
 bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvPlan* out) {
   if (M < 1 || M > 4 || N % 8 || K % 16) return false;
   const int tiles = (int)cdiv(N, kGemvTileCols);
-  const int rpt_pref = (M <= 2) ? 16 : 8;
+  const int rpt_pref = 8;
   int rpts[2] = {rpt_pref, 8};
   for (int ri = 0; ri < 2; ++ri) {
     const int rpt = rpts[ri];
@@ -279,7 +278,7 @@ bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvP
       best = {rpt, rl, s, ks, tiles};
       have = true;
       const long waves = (long)tiles * s * (rl * kGemvCW / 64);
-      if (waves >= 1024 && ks <= rl * rpt) break;
+      if (waves >= 2048 && ks <= rl * rpt) break;
     }
     if (have) {
       *out = best;
@@ -297,8 +296,14 @@ size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N) {
 template <int MT, int RPT, int RL>
 static void launch_gemv_t(const GemvParams& p, int tiles, hipStream_t s) {
   dim3 grid(tiles, p.split);
-  if (p.scales != nullptr) w4a16_gemv_kernel<MT, RPT, RL, true><<<grid, kGemvCW * RL, 0, s>>>(p);
-  else w4a16_gemv_kernel<MT, RPT, RL, false><<<grid, kGemvCW * RL, 0, s>>>(p);
+  const bool gs = p.scales != nullptr;
+  if (p.vec_ok) {
+    if (gs) w4a16_gemv_kernel<MT, RPT, RL, true, true><<<grid, kGemvCW * RL, 0, s>>>(p);
+    else w4a16_gemv_kernel<MT, RPT, RL, false, true><<<grid, kGemvCW * RL, 0, s>>>(p);
+  } else {
+    if (gs) w4a16_gemv_kernel<MT, RPT, RL, true, false><<<grid, kGemvCW * RL, 0, s>>>(p);
+    else w4a16_gemv_kernel<MT, RPT, RL, false, false><<<grid, kGemvCW * RL, 0, s>>>(p);
+  }
 }
 
 template <int MT, int RPT>
@@ -317,7 +322,7 @@ static void launch_gemv_rpt(const GemvParams& p, int rpt, int rl, int tiles, hip
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
                 int64_t ldq, const void* scales, int group, float tensor_scale, void* c,
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace,
-                hipStream_t s) {
+                hipStream_t s, bool partials_only) {
   GemvParams p;
   p.a = reinterpret_cast<const pk_half*>(a);
   p.lda = lda;
@@ -334,7 +339,8 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
   p.K = K;
   p.split = pl.split;
   p.k_slice = pl.k_slice;
-  p.vec_ok = ((reinterpret_cast<uintptr_t>(qw) & 15) == 0 && ldq % 4 == 0) ? 1 : 0;
+  p.vec_ok = ((reinterpret_cast<uintptr_t>(qw) & 15) == 0 && ldq % 4 == 0 && N % 32 == 0 &&
+              (scales == nullptr || (reinterpret_cast<uintptr_t>(scales) & 15) == 0)) ? 1 : 0;
   p.partials = pl.split > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
   switch (M) {
     case 1: launch_gemv_rpt<1>(p, pl.rpt, pl.rl, pl.tiles, s); break;
@@ -343,7 +349,8 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
     default: launch_gemv_rpt<4>(p, pl.rpt, pl.rl, pl.tiles, s); break;
   }
   PK_LAUNCH_CHECK("w4a16 gemv");
-  if (pl.split > 1) return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);
+  if (pl.split > 1 && !partials_only)
+    return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);
   return PK_OK;
 }
 

@@ -228,3 +228,23 @@ def test_int4_gemm_any_m_no_oob(cuda):
         c = gemm_int4.int4_gemm(a.to(cuda), wp, scale)
         ref = oracle.int4_gemm_ref(a.numpy(), w_q.cpu().numpy(), scale)
         assert oracle.rel_fro(c.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("M,split", [(1, 8), (3, 16), (64, 4)])
+def test_partials_then_reduce_equals_fused(M, split, cuda):
+    """The two phases of split-K (per-slice partials, ordered reduce) reproduce the fused
+    call bit for bit, and each slice's partial is that K range's product."""
+    K, N = 2048, 1024
+    a, w, qw, sc, codes, s16 = _group_case(M, K, N, 700 + M, cuda)
+    ag = a.to(cuda)
+    parts = _pk.w4a16_gemm_partials(ag, qw, sc, 128, split)
+    assert tuple(parts.shape) == (split, M, N)
+    out = torch.empty((M, N), dtype=torch.float32, device=cuda)
+    _pk.splitk_reduce(parts, 1.0, out)
+    fused = gemm_int4.w4a16_gemm(ag, qw, sc, 128, split_k=split, out_dtype=torch.float32)
+    assert torch.equal(out, fused)
+    ks = K // split
+    for s in (0, split - 1):
+        sl = slice(s * ks, (s + 1) * ks)
+        ref = oracle.w4a16_ref(a.numpy()[:, sl], codes[sl], s16[s * ks // 128:(s + 1) * ks // 128], 128)
+        assert oracle.rel_fro(parts[s].cpu().numpy(), ref) <= W4A16_TOL
