@@ -79,6 +79,14 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
+    # Resolve every symbol now (a kernel whose host stub was dropped shows up here, not at
+    # the first test on a GPU box).
+    import ctypes
+
+    try:
+        ctypes.CDLL(str(tmp), mode=os.RTLD_NOW)
+    except OSError as e:
+        raise RuntimeError(f"built library does not load: {e}") from None
     os.replace(tmp, out)
     return out
 

@@ -15,7 +15,7 @@
 // Tiling: 256 x 256 output tile, BK = 128, eight waves each owning 128 x 64 (8 x 4 MFMA
 // fragments, 128 fp32 accumulators per lane), LDS double-buffered; 128 x 128 tiles with four
 // waves for small problems.
-#include "pk_common.h"
+#include "pk_internal.h"
 
 namespace pk {
 
@@ -277,6 +277,12 @@ extern "C" int pk_fp8_gemm(const uint8_t* a8, int64_t lda, const uint8_t* b8, in
   p.N = N;
   p.K = K;
   hipStream_t s = (hipStream_t)stream;
+  // Large-tile 32x32x64 kernel (buffer DMA, swizzled LDS) when its loaders fit the shape.
+  const bool v2_ok = M >= 64 && N >= 64 && N % 16 == 0 && lda % 16 == 0 && ldb % 16 == 0 &&
+                     (reinterpret_cast<uintptr_t>(b8) & 15) == 0 &&
+                     (int64_t)M * lda < (1ll << 31) &&
+                     (b_layout == 1 ? (int64_t)N * ldb : (int64_t)K * ldb) < (1ll << 31);
+  if (v2_ok) return v2_f8_launch(a8, lda, b8, ldb, b_layout, out_scale, c, c_dtype, ldc, M, N, K, s);
   const bool big = (int64_t)M * N >= (int64_t)2048 * 2048;
   if (b_layout == 1)
     return big ? fp8_launch_cfg<256, 256, 2, 4, 1>(p, s) : fp8_launch_cfg<128, 128, 2, 2, 1>(p, s);

@@ -1,0 +1,535 @@
+// Large-tile MFMA GEMMs for gfx950: W4A16 / dense fp16 (v_mfma_f32_32x32x16_f16) and
+// e4m3 fp8 (v_mfma_f32_32x32x64_f8f6f4).
+//
+// Design (f16: 4 waves, 2 x 2, each a 128 x 64 block; fp8 256 x 256: 8 waves, 2 x 4, each a
+// 128 x 64 block):
+//  * LDS tiles are rows of 128 bytes (64 fp16 or 128 fp8 values of k) in 8 chunks of 16 B;
+//    chunk c of row r is stored in slot c ^ ((r >> 1) & 7). Sixteen lanes reading 16
+//    consecutive rows at one chunk then touch 16 distinct 16-byte bank groups.
+//  * A (and a (N, K) fp8 B) go global -> LDS by buffer DMA (buffer_load ... lds): no VGPR
+//    staging, no ds_write. Each pipeline stage is its own __shared__ array so the compiler's
+//    wait-count insertion only waits for DMA into the stage being read.
+//  * int4 B is loaded into registers, dequantised (exact codes via the 0x6400 fp16 exponent
+//    trick, times the fp16 group scale) and written k-contiguous; (K, N) fp16/fp8 B is
+//    transposed with byte permutes on the same path.
+//  * Double buffering: the loads of tile t+1 are issued before the MFMAs of tile t and
+//    consumed after them; one barrier per tile.
+//  * Addresses: one buffer resource per operand, per-lane byte offsets computed once, the K
+//    advance folded into the scalar offset. Rows/columns past the matrix are clamped to the
+//    last valid one (never read out of bounds); their results are not stored.
+#include "pk_internal.h"
+
+namespace pk {
+
+typedef unsigned pk_u4v __attribute__((ext_vector_type(4)));
+typedef unsigned pk_u2v __attribute__((ext_vector_type(2)));
+#define PK_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+constexpr unsigned kRsrcWord3 = 0x00020000u;  // raw (untyped) buffer, gfx9-family encoding
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+// 16 bytes per lane, global -> LDS (lane L writes lds + 16 L). A device-only helper: the
+// generic-to-LDS pointer cast must not appear in host-visible code (lambdas are host+device
+// and the host pass would otherwise drop the kernel that uses them).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, PK_LDS(lds), 16, voff, soff, 0, 0);
+}
+
+// Byte offset of chunk c of row r in a swizzled 128-byte-row tile.
+__device__ __forceinline__ int swz(int r, int c) { return (r << 7) + ((c ^ ((r >> 1) & 7)) << 4); }
+
+__device__ __forceinline__ pk_half2 h2v(uint32_t v) { return __builtin_bit_cast(pk_half2, v); }
+__device__ __forceinline__ uint32_t u32v(pk_half2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// XCD-aware tile order (see w4a16_gemm.hip): regroup the round-robin XCD dispatch so each XCD
+// owns a compact block of output tiles, then walk them GROUP_M tiles tall.
+__device__ __forceinline__ void v2_tile_of(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int total = tiles_m * tiles_n;
+  int logical = bid;
+  if (total % 8 == 0) logical = (bid % 8) * (total / 8) + bid / 8;
+  constexpr int GROUP_M = 4;
+  const int per_group = GROUP_M * tiles_n;
+  const int g = logical / per_group;
+  const int first_m = g * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  const int in_g = logical - g * per_group;
+  *tm = first_m + in_g % gm;
+  *tn = in_g / gm;
+}
+
+struct V2Params {
+  const void* a;
+  int64_t lda;            // elements
+  const void* b;          // int4 words / fp16 / fp8
+  int64_t ldb;            // words (int4) or elements
+  const pk_half* scales;  // int4 group scales (K/G, N) or null
+  int group;
+  float scale;            // epilogue scale (tensor scale / fp8 out_scale)
+  void* c;
+  int c_dtype;
+  int64_t ldc;
+  int M, N, K;
+  int split, k_slice;
+  int tiles_m, tiles_n;
+  float* partials;        // (split, M, N) when split > 1
+};
+
+enum V2B { kV2Int4 = 0, kV2F16KN = 1 };
+
+// ---------------------------------------------------------------------------------------
+// f16 MFMA kernel (A fp16 (M, K); B int4 words or fp16 (K, N)); BK = 64.
+// ---------------------------------------------------------------------------------------
+template <int BM, int BN, int BMODE, bool GS>
+__global__ __launch_bounds__(256) void gemm_v2_f16_kernel(V2Params p) {
+  constexpr int WTM = BM / 2, WTN = BN / 2;  // wave tile
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int A_DMA = BM / 32;             // 1 KB DMA instructions per wave per tile
+  static_assert(BN == 128 || BN == 64, "B loader assumes 16 or 8 word columns");
+  constexpr int BCG = BN / 8;                // 8-column groups
+  constexpr int BROWS = 256 / BCG;           // rows-per-thread groups: BK / rows per thread
+  constexpr int RPT = 64 / BROWS;            // k rows per thread (4 for BN=128, 2 for BN=64)
+
+  __shared__ __align__(16) char sA0[BM * 128];
+  __shared__ __align__(16) char sA1[BM * 128];
+  __shared__ __align__(16) char sB0[BN * 128];
+  __shared__ __align__(16) char sB1[BN * 128];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm0 = (wave >> 1) * WTM, wn0 = (wave & 1) * WTN;
+  int tm, tn;
+  v2_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int k_begin = blockIdx.y * p.k_slice;
+  const int ktiles = p.k_slice / 64;
+
+  // ---- A: per-lane DMA source offsets (bytes), k advance in the scalar offset ----
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda * 2));
+  int a_off[A_DMA];
+#pragma unroll
+  for (int i = 0; i < A_DMA; ++i) {
+    const int r = (wave * A_DMA + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_off[i] = (int)((int64_t)min(m0 + r, p.M - 1) * p.lda * 2) + c * 16;
+  }
+  auto issue_a = [&](int kt, char* sA) {
+    const int soff = (k_begin + kt * 64) * 2;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i)
+      dma16(ra, sA + (wave * A_DMA + i) * 1024, a_off[i], soff);
+  };
+
+  // ---- B: RPT rows x 8 columns per thread ----
+  const int brg = t % BROWS, bcg = t / BROWS;  // row group, 8-column group
+  const int bn = min(n0 + bcg * 8, p.N - 8);   // first column (clamped)
+  __amdgpu_buffer_rsrc_t rb;
+  int b_off;
+  if (BMODE == kV2Int4) {
+    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.K * p.ldb * 4));
+    b_off = (int)(((int64_t)brg * RPT * p.ldb + (bn >> 3)) * 4);
+  } else {
+    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.K * p.ldb * 2));
+    b_off = (int)(((int64_t)brg * RPT * p.ldb + bn) * 2);
+  }
+  constexpr bool has_gs = GS;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales, has_gs ? (uint32_t)((int64_t)(p.K / p.group) * p.N * 2) : 16u);
+  uint32_t breg[RPT][4];
+  pk_u4v sreg = {0u, 0u, 0u, 0u};
+  auto load_b = [&](int kt) {
+    const int k0 = k_begin + kt * 64;
+    if (BMODE == kV2Int4) {
+      const int soff = (int)((int64_t)k0 * p.ldb * 4);
+#pragma unroll
+      for (int r = 0; r < RPT; ++r)
+        breg[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rb, b_off + (int)(r * p.ldb * 4), soff, 0);
+      if constexpr (has_gs) sreg = __builtin_amdgcn_raw_buffer_load_b128(rs, bn * 2, (k0 / p.group) * p.N * 2, 0);
+    } else {
+      const int soff = (int)((int64_t)k0 * p.ldb * 2);
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        const pk_u4v v = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off + (int)(r * p.ldb * 2), soff, 0);
+        breg[r][0] = v[0]; breg[r][1] = v[1]; breg[r][2] = v[2]; breg[r][3] = v[3];
+      }
+    }
+  };
+  // Columns 8*bcg .. 8*bcg+7 of the tile, k rows RPT*brg .. +RPT-1 -> swizzled [n][k] LDS.
+  auto store_b = [&](char* sB) {
+    uint32_t col[8][RPT / 2];  // (k, k+1) half pairs per column
+    if (BMODE == kV2Int4) {
+      uint32_t w[RPT];
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) w[r] = breg[r][0] ^ 0x88888888u;
+      const pk_half2 bias = {(pk_half)1032.0f, (pk_half)1032.0f};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
+#pragma unroll
+        for (int r2 = 0; r2 < RPT / 2; ++r2) {
+          const uint32_t pr = __builtin_amdgcn_perm(w[2 * r2 + 1], w[2 * r2], sel);
+#pragma unroll
+          for (int hs = 0; hs < 2; ++hs) {
+            const int cidx = 2 * b + hs;
+            const uint32_t nib = hs ? (pr >> 4) : pr;
+            pk_half2 q = h2v((nib & 0x000f000fu) | 0x64006400u) - bias;  // exact codes
+            if constexpr (has_gs) {
+              const uint32_t sv = sreg[cidx >> 1];
+              const uint32_t s1 = (cidx & 1) ? (sv >> 16) : (sv & 0xffffu);
+              q = q * h2v(s1 | (s1 << 16));
+            }
+            col[cidx][r2] = u32v(q);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+        for (int r2 = 0; r2 < RPT / 2; ++r2)
+          col[c][r2] = __builtin_amdgcn_perm(breg[2 * r2 + 1][c >> 1], breg[2 * r2][c >> 1], sel);
+      }
+    }
+    // k offset of this thread's rows inside the 128-byte row: RPT*brg halves
+    const int kb = RPT * brg * 2;  // bytes
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int n = bcg * 8 + c;
+      char* dst = sB + swz(n, kb >> 4) + (kb & 15);
+      if (RPT == 4) {
+        pk_u2v v = {col[c][0], col[c][1]};
+        *reinterpret_cast<pk_u2v*>(dst) = v;
+      } else {
+        *reinterpret_cast<uint32_t*>(dst) = col[c][0];
+      }
+    }
+  };
+
+  // ---- MFMA operand offsets (bytes within a stage), per fragment and k16 step ----
+  int aoff[FM][4], boff[FN][4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) aoff[i][ks] = swz(wm0 + 32 * i + (lane & 31), 2 * ks + (lane >> 5));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) boff[j][ks] = swz(wn0 + 32 * j + (lane & 31), 2 * ks + (lane >> 5));
+  }
+
+  pk_f16v acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = (pk_f16v){};
+
+  auto compute = [&](const char* sA, const char* sB) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      pk_half8 af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const pk_half8*>(sA + aoff[i][ks]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const pk_half8*>(sB + boff[j][ks]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // ---- pipeline: tiles in pairs (stage 0, stage 1); an odd last tile sits in stage 0 ----
+  issue_a(0, sA0);
+  load_b(0);
+  store_b(sB0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < ktiles; kt += 2) {
+    issue_a(kt + 1, sA1);
+    load_b(kt + 1);
+    compute(sA0, sB0);
+    store_b(sB1);
+    __syncthreads();
+    const int n2 = min(kt + 2, ktiles - 1);  // the last pair re-reads a valid tile, unused
+    issue_a(n2, sA0);
+    load_b(n2);
+    compute(sA1, sB1);
+    store_b(sB0);
+    __syncthreads();
+  }
+  if (kt < ktiles) compute(sA0, sB0);
+
+  // ---- epilogue: C[m][n], fragment (i, j) register r at row 8*(r/4) + 4*(lane/32) + r%4 ----
+  const int erow = 4 * (lane >> 5), ecol = lane & 31;
+  float* part = p.split > 1 ? p.partials + (int64_t)blockIdx.y * p.M * p.N : nullptr;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = m0 + wm0 + 32 * i + 8 * (r >> 2) + erow + (r & 3);
+        const int gn = n0 + wn0 + 32 * j + ecol;
+        if (gm < p.M && gn < p.N) {
+          if (part) part[(int64_t)gm * p.N + gn] = acc[i][j][r];
+          else store_from_f32(p.c, p.c_dtype, (int64_t)gm * p.ldc + gn, acc[i][j][r] * p.scale);
+        }
+      }
+}
+
+// ---------------------------------------------------------------------------------------
+// fp8 MFMA kernel (A e4m3 (M, K); B e4m3 (K, N) or (N, K)); BK = 128.
+// ---------------------------------------------------------------------------------------
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BLAYOUT>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_v2_f8_kernel(V2Params p) {
+  constexpr int NW = WAVES_M * WAVES_N, T = 64 * NW;
+  constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int A_DMA = BM / (8 * NW), B_DMA = BN / (8 * NW);
+  constexpr int BCG = BN / 16;           // (K,N): 16-byte column groups
+  constexpr int BROWS = T / BCG;         // row groups
+  constexpr int RPT = 128 / BROWS;       // k rows per thread
+  static_assert(RPT == 8 || RPT == 4, "(K,N) loader handles 8 or 4 rows per thread");
+
+  __shared__ __align__(16) char sA0[BM * 128];
+  __shared__ __align__(16) char sA1[BM * 128];
+  __shared__ __align__(16) char sB0[BN * 128];
+  __shared__ __align__(16) char sB1[BN * 128];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm0 = (wave / WAVES_N) * WTM, wn0 = (wave % WAVES_N) * WTN;
+  int tm, tn;
+  v2_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int ktiles = p.K / 128;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
+  int a_off[A_DMA];
+#pragma unroll
+  for (int i = 0; i < A_DMA; ++i) {
+    const int r = (wave * A_DMA + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_off[i] = (int)((int64_t)min(m0 + r, p.M - 1) * p.lda) + c * 16;
+  }
+  auto issue_a = [&](int kt, char* sA) {
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i)
+      dma16(ra, sA + (wave * A_DMA + i) * 1024, a_off[i], kt * 128);
+  };
+
+  // B (N, K): DMA like A. B (K, N): RPT rows x 16 bytes per thread through registers.
+  __amdgpu_buffer_rsrc_t rb;
+  int b_off[BLAYOUT == 1 ? B_DMA : 1];
+  const int brg = t % BROWS, bcg = t / BROWS;
+  const int bn = min(n0 + bcg * 16, p.N - 16);
+  if (BLAYOUT == 1) {
+    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) {
+      const int r = (wave * B_DMA + i) * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      b_off[i] = (int)((int64_t)min(n0 + r, p.N - 1) * p.ldb) + c * 16;
+    }
+  } else {
+    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.K * p.ldb));
+    b_off[0] = (int)((int64_t)brg * RPT * p.ldb + bn);
+  }
+  pk_u4v breg[BLAYOUT == 0 ? RPT : 1];
+  auto issue_b = [&](int kt, char* sB) {
+    if (BLAYOUT == 1) {
+#pragma unroll
+      for (int i = 0; i < B_DMA; ++i)
+        dma16(rb, sB + (wave * B_DMA + i) * 1024, b_off[i], kt * 128);
+    } else {
+      const int soff = (int)((int64_t)kt * 128 * p.ldb);
+#pragma unroll
+      for (int r = 0; r < RPT; ++r)
+        breg[r] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[0] + (int)(r * p.ldb), soff, 0);
+    }
+  };
+  // (K, N) B: RPT (8 or 4) rows x 16 bytes -> 16 columns x RPT k bytes, swizzled [n][k] LDS.
+  auto tr4 = [](const uint32_t in[4], uint32_t out[4]) {  // 4x4 byte transpose
+    const uint32_t t01a = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);
+    const uint32_t t01b = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);
+    const uint32_t t23a = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
+    const uint32_t t23b = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
+    out[0] = __builtin_amdgcn_perm(t23a, t01a, 0x05040100u);
+    out[1] = __builtin_amdgcn_perm(t23a, t01a, 0x07060302u);
+    out[2] = __builtin_amdgcn_perm(t23b, t01b, 0x05040100u);
+    out[3] = __builtin_amdgcn_perm(t23b, t01b, 0x07060302u);
+  };
+  auto store_b = [&](char* sB) {
+    if constexpr (BLAYOUT == 0) {
+      const int kb = RPT * brg;  // byte offset of the thread's k rows within the 128-byte row
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {  // dword d = columns 4d..4d+3
+        uint32_t lo[4], tl[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lo[r] = breg[r][d];
+        tr4(lo, tl);
+        if constexpr (RPT == 8) {
+          uint32_t hi[4], th[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) hi[r] = breg[4 + r][d];
+          tr4(hi, th);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = bcg * 16 + 4 * d + q;
+            pk_u2v v = {tl[q], th[q]};
+            *reinterpret_cast<pk_u2v*>(sB + swz(n, kb >> 4) + (kb & 15)) = v;
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = bcg * 16 + 4 * d + q;
+            *reinterpret_cast<uint32_t*>(sB + swz(n, kb >> 4) + (kb & 15)) = tl[q];
+          }
+        }
+      }
+    }
+  };
+
+  // operand offsets: per fragment, per k64 step, two 16-byte chunks (the lane's 32 bytes)
+  int aoff[FM][2], boff[FN][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) aoff[i][ks] = swz(wm0 + 32 * i + (lane & 31), 4 * ks + 2 * (lane >> 5));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) boff[j][ks] = swz(wn0 + 32 * j + (lane & 31), 4 * ks + 2 * (lane >> 5));
+  }
+  // the second chunk (c + 1) of a row r sits at slot (c + 1) ^ s = (c ^ s) ^ 1 for even c
+  auto chunk2 = [](int off) { return off ^ 16; };
+
+  pk_f16v acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = (pk_f16v){};
+
+  auto compute = [&](const char* sA, const char* sB) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      pk_i8v bf[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sB + boff[j][ks]);
+        const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sB + chunk2(boff[j][ks]));
+        bf[j] = (pk_i8v){(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sA + aoff[i][ks]);
+        const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sA + chunk2(aoff[i][ks]));
+        const pk_i8v af = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, bf[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+      }
+    }
+  };
+
+  issue_a(0, sA0);
+  issue_b(0, sB0);
+  store_b(sB0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < ktiles; kt += 2) {
+    issue_a(kt + 1, sA1);
+    issue_b(kt + 1, sB1);
+    compute(sA0, sB0);
+    store_b(sB1);
+    __syncthreads();
+    const int n2 = min(kt + 2, ktiles - 1);
+    issue_a(n2, sA0);
+    issue_b(n2, sB0);
+    compute(sA1, sB1);
+    store_b(sB0);
+    __syncthreads();
+  }
+  if (kt < ktiles) compute(sA0, sB0);
+
+  const int erow = 4 * (lane >> 5), ecol = lane & 31;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = m0 + wm0 + 32 * i + 8 * (r >> 2) + erow + (r & 3);
+        const int gn = n0 + wn0 + 32 * j + ecol;
+        if (gm < p.M && gn < p.N)
+          store_from_f32(p.c, p.c_dtype, (int64_t)gm * p.ldc + gn, acc[i][j][r] * p.scale);
+      }
+}
+
+// ---------------------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------------------
+bool v2_f16_ok(int M, int N, int K, int k_slice, int group, bool has_gs, int64_t lda, int64_t ldb,
+               bool int4) {
+  if (M < 64 || N < 64 || N % 8 || k_slice % 64) return false;
+  if (has_gs && group % 64) return false;
+  // 32-bit buffer offsets
+  if ((int64_t)M * lda * 2 >= (1ll << 31)) return false;
+  if ((int64_t)K * ldb * (int4 ? 4 : 2) >= (1ll << 31)) return false;
+  return true;
+}
+
+int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, int64_t ldb,
+                  const void* scales, int group, float scale, void* c, int c_dtype, int64_t ldc,
+                  int M, int N, int K, int split, void* workspace, hipStream_t s,
+                  bool partials_only) {
+  V2Params p;
+  p.a = a; p.lda = lda; p.b = b; p.ldb = ldb;
+  p.scales = reinterpret_cast<const pk_half*>(scales);
+  p.group = group > 0 ? group : K;
+  p.scale = scale; p.c = c; p.c_dtype = c_dtype; p.ldc = ldc;
+  p.M = M; p.N = N; p.K = K; p.split = split; p.k_slice = K / split;
+  p.partials = split > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
+  const int bn = 128;
+  p.tiles_m = (int)cdiv(M, bm);
+  p.tiles_n = (int)cdiv(N, bn);
+  dim3 grid(p.tiles_m * p.tiles_n, split);
+  const bool gs = scales != nullptr;
+  if (bmode == kV2Int4) {
+    if (bm == 256) {
+      if (gs) gemm_v2_f16_kernel<256, 128, kV2Int4, true><<<grid, 256, 0, s>>>(p);
+      else gemm_v2_f16_kernel<256, 128, kV2Int4, false><<<grid, 256, 0, s>>>(p);
+    } else {
+      if (gs) gemm_v2_f16_kernel<128, 128, kV2Int4, true><<<grid, 256, 0, s>>>(p);
+      else gemm_v2_f16_kernel<128, 128, kV2Int4, false><<<grid, 256, 0, s>>>(p);
+    }
+  } else {
+    if (bm == 256) gemm_v2_f16_kernel<256, 128, kV2F16KN, false><<<grid, 256, 0, s>>>(p);
+    else gemm_v2_f16_kernel<128, 128, kV2F16KN, false><<<grid, 256, 0, s>>>(p);
+  }
+  PK_LAUNCH_CHECK("gemm v2 f16");
+  if (split > 1 && !partials_only) return splitk_reduce(p.partials, split, M, N, scale, c, c_dtype, ldc, s);
+  return PK_OK;
+}
+
+int v2_f8_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb, int b_layout,
+                 float out_scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                 hipStream_t s) {
+  V2Params p;
+  p.a = a8; p.lda = lda; p.b = b8; p.ldb = ldb; p.scales = nullptr; p.group = K;
+  p.scale = out_scale; p.c = c; p.c_dtype = c_dtype; p.ldc = ldc;
+  p.M = M; p.N = N; p.K = K; p.split = 1; p.k_slice = K; p.partials = nullptr;
+  const bool big = (int64_t)M * N >= (int64_t)2048 * 2048;
+  const int bm = big ? 256 : 128, bn = big ? 256 : 128;
+  p.tiles_m = (int)cdiv(M, bm);
+  p.tiles_n = (int)cdiv(N, bn);
+  const int grid = p.tiles_m * p.tiles_n;
+  if (big) {
+    if (b_layout == 1) gemm_v2_f8_kernel<256, 256, 2, 4, 1><<<grid, 512, 0, s>>>(p);
+    else gemm_v2_f8_kernel<256, 256, 2, 4, 0><<<grid, 512, 0, s>>>(p);
+  } else {
+    if (b_layout == 1) gemm_v2_f8_kernel<128, 128, 2, 2, 1><<<grid, 256, 0, s>>>(p);
+    else gemm_v2_f8_kernel<128, 128, 2, 2, 0><<<grid, 256, 0, s>>>(p);
+  }
+  PK_LAUNCH_CHECK("gemm v2 fp8");
+  return PK_OK;
+}
+
+}  // namespace pk

@@ -34,4 +34,15 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only = false);
 
+// Large-tile MFMA GEMMs (gemm_v2.hip).
+bool v2_f16_ok(int M, int N, int K, int k_slice, int group, bool has_gs, int64_t lda, int64_t ldb,
+               bool int4);
+int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, int64_t ldb,
+                  const void* scales, int group, float scale, void* c, int c_dtype, int64_t ldc,
+                  int M, int N, int K, int split, void* workspace, hipStream_t s,
+                  bool partials_only);
+int v2_f8_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb, int b_layout,
+                 float out_scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                 hipStream_t s);
+
 }  // namespace pk

@@ -273,8 +273,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmP
 static const GemmCfg kCfg16 = {16, 256, 1, 4};
 static const GemmCfg kCfg32 = {32, 256, 1, 4};
 static const GemmCfg kCfg64 = {64, 256, 1, 4};
-static const GemmCfg kCfg128 = {128, 128, 2, 2};
-static const GemmCfg kCfg256 = {256, 128, 2, 2};
+static const GemmCfg kCfg128 = {128, 128, 2, 2};  // large-tile kernel: 128 x 128, 4 waves
+static const GemmCfg kCfg256 = {256, 128, 2, 2};  // large-tile kernel: 256 x 128, 4 waves
 
 static GemmCfg pick_cfg(int M) {
   if (M <= 16) return kCfg16;
@@ -348,6 +348,12 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
                 int64_t ldb, const void* scales, int group, float tensor_scale, void* c,
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only) {
+  // 128/256-row tiles: the large-tile 32x32-MFMA kernel when its constraints hold.
+  if (pl.cfg.bm >= 128 &&
+      v2_f16_ok(M, N, K, pl.k_slice, group, scales != nullptr, lda, ldb, bmode == kBInt4))
+    return v2_f16_launch(pl.cfg.bm, bmode == kBInt4 ? 0 : 1, a, lda, b, ldb, scales, group,
+                         tensor_scale, c, c_dtype, ldc, M, N, K, pl.split, workspace, s,
+                         partials_only);
   GemmParams p;
   p.a = reinterpret_cast<const pk_half*>(a);
   p.lda = lda;
