@@ -21,15 +21,7 @@
 
 namespace pk {
 
-typedef unsigned pk_u4v __attribute__((ext_vector_type(4)));
-typedef unsigned pk_u2v __attribute__((ext_vector_type(2)));
 #define PK_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-
-constexpr unsigned kRsrcWord3 = 0x00020000u;  // raw (untyped) buffer, gfx9-family encoding
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
-}
 
 // 16 bytes per lane, global -> LDS (lane L writes lds + 16 L). A device-only helper: the
 // generic-to-LDS pointer cast must not appear in host-visible code (lambdas are host+device

@@ -18,6 +18,16 @@ typedef _Float16 pk_half8 __attribute__((ext_vector_type(8)));
 typedef float pk_f4 __attribute__((ext_vector_type(4)));
 typedef float pk_f16v __attribute__((ext_vector_type(16)));
 typedef int pk_i8v __attribute__((ext_vector_type(8)));
+typedef unsigned pk_u4v __attribute__((ext_vector_type(4)));
+typedef unsigned pk_u2v __attribute__((ext_vector_type(2)));
+
+constexpr unsigned kRsrcWord3 = 0x00020000u;  // raw (untyped) buffer, gfx9-family encoding
+
+// Raw buffer resource over [p, p + bytes): loads take a per-lane byte offset (VGPR) plus a
+// wave-uniform one (SGPR), so row strides cost no vector instructions.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
 
 // ---------------------------------------------------------------------------------------
 // Error reporting (host side). Every C-ABI entry point returns PK_OK or a negative code and

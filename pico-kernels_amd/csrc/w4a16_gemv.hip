@@ -24,10 +24,14 @@
 //
 // Reduction: row-lanes inside a wave are folded with a reduce-scatter over lane masks
 // 32/16/8, waves through LDS. With split-K each slice writes an fp32 partial row and a
-// second small kernel (splitk_reduce_kernel) adds the slices in order 0..S-1. A kernel
-// boundary is the cheapest point where writes of every XCD's L2 become visible to all; a
-// last-workgroup handoff inside one kernel would need an L2 writeback and invalidate per
-// wave. There are no floating-point atomics, so the result is bitwise reproducible.
+// second small kernel (splitk_reduce_kernel) adds the slices in order 0..S-1, so the result
+// is bitwise reproducible (no floating-point atomics). A kernel boundary is the cheapest
+// point where writes from every XCD's L2 become visible to all; measured on MI355X, a
+// last-workgroup handoff inside the kernel costs more: with agent-scope release/acquire
+// fences (an L2 writeback per releasing workgroup) it is 2.6x slower at 16 slices, and with
+// device-coherent relaxed atomics it still adds a ~2.3 us chain of dependent memory round
+// trips (store acknowledgement, arrival counter, partial loads) to the kernel, no faster
+// end to end than the second kernel.
 #include "pk_internal.h"
 
 namespace pk {
@@ -54,6 +58,25 @@ struct GemvParams {
 };
 
 __device__ __forceinline__ pk_half2 as_half2(uint32_t v) { return __builtin_bit_cast(pk_half2, v); }
+
+// Output stage shared by the GEMV kernels. `fold(m, col)` returns this workgroup's sum for
+// activation row m and tile column col (after its __syncthreads). With split == 1 the value
+// is scaled and stored, otherwise it goes to the (split, M, N) fp32 partials that
+// splitk_reduce_kernel adds.
+template <int MT, int NT, typename Fold>
+__device__ __forceinline__ void gemv_finish(const GemvParams& p, int tile, int slice, int t,
+                                            Fold fold) {
+  const int col_base = tile * kGemvTileCols;
+  for (int idx = t; idx < MT * kGemvTileCols; idx += NT) {
+    const int m = idx / kGemvTileCols, col = idx % kGemvTileCols;
+    if (m >= p.M || col_base + col >= p.N) continue;
+    const float v = fold(m, col);
+    if (p.split == 1)
+      store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + col_base + col, v * p.tensor_scale);
+    else
+      p.partials[((int64_t)slice * p.M + m) * p.N + col_base + col] = v;
+  }
+}
 
 // VEC: every lane owns 4 whole words with 16-byte aligned rows (N % 32 == 0), so weight
 // loads need no per-lane branch. Loads are never predicated in the hot loop: a branch
@@ -211,29 +234,133 @@ __global__ __launch_bounds__(kGemvCW* RL) void w4a16_gemv_kernel(GemvParams p) {
     for (int i = 0; i < 4; ++i) red[wave][m][cl * 32 + cbase + i] = red4[m][i];
   __syncthreads();
 
-  const int col_base = tile * kGemvTileCols;
-  const int M = p.M;
-  if (p.split == 1) {
-    for (int idx = t; idx < MT * kGemvTileCols; idx += NT) {
-      const int m = idx / kGemvTileCols, col = idx % kGemvTileCols;
-      if (m >= M || col_base + col >= p.N) continue;
-      float v = red[0][m][col];
-#pragma unroll
-      for (int wv = 1; wv < NWAVES; ++wv) v += red[wv][m][col];
-      store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + col_base + col, v * p.tensor_scale);
-    }
-    return;
-  }
-
-  // ---- split-K: publish this slice's partial row; splitk_reduce_kernel adds the slices ----
-  for (int idx = t; idx < MT * kGemvTileCols; idx += NT) {
-    const int m = idx / kGemvTileCols, col = idx % kGemvTileCols;
-    if (m >= M || col_base + col >= p.N) continue;
+  gemv_finish<MT, NT>(p, tile, slice, t, [&](int m, int col) {
     float v = red[0][m][col];
 #pragma unroll
     for (int wv = 1; wv < NWAVES; ++wv) v += red[wv][m][col];
-    p.partials[((int64_t)slice * M + m) * p.N + col_base + col] = v;
+    return v;
+  });
+}
+
+// ---------------------------------------------------------------------------------------
+// MFMA variant (M <= 4, N % 32 == 0, K % 256 == 0, group % 64 == 0, aligned operands).
+//
+// Slices of 256 rows; a workgroup is 4 waves and each wave owns one 64-row x 128-byte block
+// (lane: cl = lane % 8 picks 4 words = 32 columns, rl = lane / 8 picks 8 consecutive rows),
+// so every wave issues all its loads at once and its rows lie in a single scale group.
+// The products run on v_mfma_f32_16x16x32_f16, which also performs most of the row
+// reduction:
+//   * B operand of lane L: 8 fp16 values = the lane's 8 rows of one column pair. Output
+//     column j = L % 16 of the MFMA sums lanes j, j+16, j+32, j+48, i.e. row lanes
+//     rl = 2g + j/8 (g = 0..3) of column set cl = j % 8: four of the wave's eight row lanes.
+//   * A operand of lane L: activation row m = L % 8 at the lane's own rows, so A-row
+//     i = L % 16 carries the rows of parity i / 8, and C[m + 8p][j] is a complete sum over
+//     the row lanes of parity p exactly when j / 8 == p. Lanes 0-7 (p = 0) and 40-47 (p = 1)
+//     hold those outputs in their C registers m = 0..3; parities, waves and slices remain.
+//   * B values are fp16 *subnormals* (MFMA keeps them exactly): after XOR 0x88888888 and a
+//     byte permute of rows (k, k+1), a 16-bit half holds (u_lo + 16 u_hi) * 2^-24 for the
+//     two nibbles of one byte (u = v + 8). With C_off = the MFMA of the constant 8 * 2^-24,
+//       lo:  MFMA(A, halves & 0x000F000F, -C_off)    = 2^-24 * sum x * v_lo,
+//       raw: MFMA(A, halves,              -17 C_off) and raw - lo = 2^-20 * sum x * v_hi,
+//     so the nibble offset is folded into the accumulator input. Products are exact.
+//   * The group scale multiplies each wave's column sums in the final fold (one scale per
+//     wave and column), and the powers of two are applied there too.
+// Per word that is 1 XOR, 2 permutes and 2 ANDs plus one MFMA, against 4 dot2 products, a
+// 28-shuffle reduction and a per-step epilogue in the VALU kernel. Loads are raw buffer
+// loads: a per-lane byte offset plus a wave-uniform row offset in a scalar register.
+constexpr int kMfmaRows = 256;  // rows per workgroup = slice length
+constexpr int kMfmaSeg = 36;    // LDS floats per 32-column segment (padding spreads banks)
+
+template <int MT, bool HAS_GS>
+__global__ __launch_bounds__(256, MT == 1 ? 4 : 2) void w4a16_gemv_mfma_kernel(GemvParams p) {
+  constexpr int NW = 4;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int cl = lane & 7, rl = lane >> 3;
+  const int tile = blockIdx.x, slice = blockIdx.y;
+  const int words_total = p.N >> 3;
+  // the ragged last tile re-reads in-bounds words; those columns are never stored
+  const int word0 = min(tile * kGemvTileWords + cl * 4, words_total - 4);
+  const int kb = slice * kMfmaRows + wave * 64;  // this wave's rows: kb .. kb + 63
+  const int xrow = min(cl, p.M - 1);
+
+  // Scales for the fold, requested first: thread t folds tile column t.
+  const int col_base = tile * kGemvTileCols;
+  float sc[NW];
+  if constexpr (HAS_GS) {
+    const int scol = min(col_base + t, p.N - 1);
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      sc[w] = (float)p.scales[(int64_t)((slice * kMfmaRows + w * 64) / p.group) * p.N + scol];
   }
+
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.qw, (uint32_t)((int64_t)p.K * p.ldq * 4));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda * 2));
+  const int ldq4 = (int)p.ldq * 4;
+  const pk_u4v xq = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(xrow * p.lda + rl * 8) * 2, kb * 2, 0);
+  const int q_voff = rl * 8 * ldq4 + word0 * 4;
+  pk_u4v w[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) w[r] = __builtin_amdgcn_raw_buffer_load_b128(rq, q_voff, (kb + r) * ldq4, 0);
+
+  const pk_f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  const pk_u4v eight_u = {0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u};
+  const pk_half8 a = __builtin_bit_cast(pk_half8, xq);
+  const pk_f4 coff = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(pk_half8, eight_u), zero4, 0, 0, 0);
+  const pk_f4 cin_lo = -coff;
+  const pk_f4 cin_raw = coff * -17.0f;
+  float lo_out[MT][16], hi_out[MT][16];  // byte column jb = tile columns 2jb (lo), 2jb+1 (hi)
+#pragma unroll
+  for (int j4 = 0; j4 < 4; ++j4) {
+    uint32_t wx[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) wx[r] = w[r][j4] ^ 0x88888888u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
+      pk_u4v raw, lo;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        raw[d] = __builtin_amdgcn_perm(wx[2 * d + 1], wx[2 * d], sel);
+        lo[d] = raw[d] & 0x000f000fu;
+      }
+      const pk_f4 clo = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(pk_half8, lo), cin_lo, 0, 0, 0);
+      const pk_f4 craw = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(pk_half8, raw), cin_raw, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < MT; ++r) {
+        lo_out[r][4 * j4 + b] = clo[r];
+        hi_out[r][4 * j4 + b] = craw[r] - clo[r];
+      }
+    }
+  }
+
+  // ---- lanes whose C rows are complete write them; fold parities and waves -----------
+  __shared__ float red[NW][2][MT][8 * kMfmaSeg];
+  {
+    const int par = lane >> 5;
+    const bool valid = ((lane & 15) >> 3) == par && ((lane >> 4) & 1) == 0;  // lanes 0-7, 40-47
+    if (valid) {
+#pragma unroll
+      for (int r = 0; r < MT; ++r)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const pk_f4 v = {lo_out[r][2 * q], hi_out[r][2 * q], lo_out[r][2 * q + 1], hi_out[r][2 * q + 1]};
+          *reinterpret_cast<pk_f4*>(&red[wave][par][r][cl * kMfmaSeg + 4 * q]) = v;
+        }
+    }
+  }
+  __syncthreads();
+  gemv_finish<MT, 256>(p, tile, slice, t, [&](int m, int col) {
+    const int o = (col >> 5) * kMfmaSeg + (col & 31);
+    float v = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < NW; ++wv) {
+      const float part = red[wv][0][m][o] + red[wv][1][m][o];
+      if constexpr (HAS_GS) v = __builtin_fmaf(part, sc[wv], v);
+      else v += part;
+    }
+    return v * ((col & 1) ? 1048576.0f : 16777216.0f);  // exact: powers of two
+  });
 }
 
 // ---------------------------------------------------------------------------------------
@@ -247,6 +374,10 @@ static bool gemv_config_ok(int K, int group, bool has_gs, int split, int rpt) {
   return true;
 }
 
+static int mfma_ok(int k_slice, int group, bool has_gs) {
+  return k_slice == kMfmaRows && (!has_gs || group % 64 == 0) ? 1 : 0;
+}
+
 static int pick_rl(int k_slice, int rpt) {
   const int steps = k_slice / rpt;  // row-lane steps available in one slice
   if (steps >= 32) return 32;
@@ -257,35 +388,32 @@ static int pick_rl(int k_slice, int rpt) {
 bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvPlan* out) {
   if (M < 1 || M > 4 || N % 8 || K % 16) return false;
   const int tiles = (int)cdiv(N, kGemvTileCols);
-  const int rpt_pref = 8;
-  int rpts[2] = {rpt_pref, 8};
-  for (int ri = 0; ri < 2; ++ri) {
-    const int rpt = rpts[ri];
-    if (split_req > 0) {
-      if (!gemv_config_ok(K, group, has_gs, split_req, rpt)) continue;
-      const int ks = K / split_req;
-      *out = {rpt, pick_rl(ks, rpt), split_req, ks, tiles};
-      return true;
-    }
-    // Automatic: the smallest split that puts >= ~1024 waves in flight (4 per CU) with
-    // every row-lane busy, capped at 32 slices.
-    GemvPlan best{};
-    bool have = false;
-    for (int s = 1; s <= 32; s *= 2) {
-      if (!gemv_config_ok(K, group, has_gs, s, rpt)) continue;
-      const int ks = K / s;
-      const int rl = pick_rl(ks, rpt);
-      best = {rpt, rl, s, ks, tiles};
-      have = true;
-      const long waves = (long)tiles * s * (rl * kGemvCW / 64);
-      if (waves >= 2048 && ks <= rl * rpt) break;
-    }
-    if (have) {
-      *out = best;
-      return true;
-    }
+  const int rpt = 8;
+  if (split_req > 0) {
+    if (!gemv_config_ok(K, group, has_gs, split_req, rpt)) return false;
+    const int ks = K / split_req;
+    *out = {rpt, pick_rl(ks, rpt), split_req, ks, tiles, mfma_ok(ks, group, has_gs)};
+    return true;
   }
-  return false;
+  // Automatic: the MFMA kernel's 256-row slices when it applies; otherwise the smallest
+  // split that puts >= 2048 waves in flight (8 per CU) with every row-lane busy, capped at
+  // 32 slices.
+  if (K % kMfmaRows == 0 && mfma_ok(kMfmaRows, group, has_gs)) {
+    const int s = K / kMfmaRows;
+    *out = {rpt, pick_rl(kMfmaRows, rpt), s, kMfmaRows, tiles, 1};
+    return true;
+  }
+  bool have = false;
+  for (int s = 1; s <= 32; s *= 2) {
+    if (!gemv_config_ok(K, group, has_gs, s, rpt)) continue;
+    const int ks = K / s;
+    const int rl = pick_rl(ks, rpt);
+    *out = {rpt, rl, s, ks, tiles, mfma_ok(ks, group, has_gs)};
+    have = true;
+    const long waves = (long)tiles * s * (rl * kGemvCW / 64);
+    if (waves >= 2048 && ks <= rl * rpt) break;
+  }
+  return have;
 }
 
 size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N) {
@@ -306,17 +434,18 @@ static void launch_gemv_t(const GemvParams& p, int tiles, hipStream_t s) {
   }
 }
 
-template <int MT, int RPT>
+template <int MT>
 static void launch_gemv_rl(const GemvParams& p, int rl, int tiles, hipStream_t s) {
-  if (rl == 32) launch_gemv_t<MT, RPT, 32>(p, tiles, s);
-  else if (rl == 16) launch_gemv_t<MT, RPT, 16>(p, tiles, s);
-  else launch_gemv_t<MT, RPT, 8>(p, tiles, s);
+  if (rl == 32) launch_gemv_t<MT, 8, 32>(p, tiles, s);
+  else if (rl == 16) launch_gemv_t<MT, 8, 16>(p, tiles, s);
+  else launch_gemv_t<MT, 8, 8>(p, tiles, s);
 }
 
 template <int MT>
-static void launch_gemv_rpt(const GemvParams& p, int rpt, int rl, int tiles, hipStream_t s) {
-  if (rpt == 16) launch_gemv_rl<MT, 16>(p, rl, tiles, s);
-  else launch_gemv_rl<MT, 8>(p, rl, tiles, s);
+static void launch_gemv_mfma(const GemvParams& p, int tiles, hipStream_t s) {
+  dim3 grid(tiles, p.split);
+  if (p.scales) w4a16_gemv_mfma_kernel<MT, true><<<grid, 256, 0, s>>>(p);
+  else w4a16_gemv_mfma_kernel<MT, false><<<grid, 256, 0, s>>>(p);
 }
 
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
@@ -342,11 +471,26 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
   p.vec_ok = ((reinterpret_cast<uintptr_t>(qw) & 15) == 0 && ldq % 4 == 0 && N % 32 == 0 &&
               (scales == nullptr || (reinterpret_cast<uintptr_t>(scales) & 15) == 0)) ? 1 : 0;
   p.partials = pl.split > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
-  switch (M) {
-    case 1: launch_gemv_rpt<1>(p, pl.rpt, pl.rl, pl.tiles, s); break;
-    case 2: launch_gemv_rpt<2>(p, pl.rpt, pl.rl, pl.tiles, s); break;
-    case 3: launch_gemv_rpt<3>(p, pl.rpt, pl.rl, pl.tiles, s); break;
-    default: launch_gemv_rpt<4>(p, pl.rpt, pl.rl, pl.tiles, s); break;
+  // buffer offsets are 32-bit: the MFMA kernel needs the weights and activations below 2 GiB
+  const bool mfma = pl.mfma && pl.k_slice == kMfmaRows && K % kMfmaRows == 0 &&
+                    (scales == nullptr || group % 64 == 0) && p.vec_ok &&
+                    (reinterpret_cast<uintptr_t>(a) & 15) == 0 &&
+                    lda % 8 == 0 && (int64_t)K * ldq * 4 < (1ll << 31) &&
+                    (int64_t)M * lda * 2 < (1ll << 31);
+  if (mfma) {
+    switch (M) {
+      case 1: launch_gemv_mfma<1>(p, pl.tiles, s); break;
+      case 2: launch_gemv_mfma<2>(p, pl.tiles, s); break;
+      case 3: launch_gemv_mfma<3>(p, pl.tiles, s); break;
+      default: launch_gemv_mfma<4>(p, pl.tiles, s); break;
+    }
+  } else {
+    switch (M) {
+      case 1: launch_gemv_rl<1>(p, pl.rl, pl.tiles, s); break;
+      case 2: launch_gemv_rl<2>(p, pl.rl, pl.tiles, s); break;
+      case 3: launch_gemv_rl<3>(p, pl.rl, pl.tiles, s); break;
+      default: launch_gemv_rl<4>(p, pl.rl, pl.tiles, s); break;
+    }
   }
   PK_LAUNCH_CHECK("w4a16 gemv");
   if (pl.split > 1 && !partials_only)
