@@ -35,6 +35,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2516.6  # dense fp16 (256 CU x 2.4 GHz x 4096 FLOP/clk)
 MFMA_F8_PEAK_TFLOPS = 5033.2   # dense fp8
 N_ROTATE = 40
+KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v2_f16_kernel"}
 
 
 def _gen(seed: int):
@@ -87,6 +88,26 @@ class GraphTimer:
         return best
 
 
+def per_launch_ms(fn, n: int) -> float:
+    """Mean duration of single launches: a HIP event pair around each fn(i) on one
+    stream (fn launches on the current stream), after a warm-up."""
+    import torch
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(10):
+            fn(i)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(n)]
+        for i, (e0, e1) in enumerate(ev):
+            e0.record(stream)
+            fn(i)
+            e1.record(stream)
+        torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / n
+
+
 def gemv_inputs(M: int, K: int, N: int, nrot: int, dev):
     import torch
 
@@ -124,7 +145,11 @@ def bench_gemv(args, dev) -> dict:
     def step_partials(i):
         _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
 
+    # Average launch of the slice kernel: K launches back to back in one graph, HIP events
+    # around the replay on the launch stream (agrees with rocprof's kernel-trace average);
+    # single launches bracketed by their own events read ~1.5 us longer (event overhead).
     ms_kernel = GraphTimer(step_partials, args.steps, args.warmup).run()
+    ms_kernel_events = per_launch_ms(step_partials, min(args.steps, 500))
 
     sweep = {}
     for s in (1, 2, 4, 8, 16):
@@ -136,7 +161,8 @@ def bench_gemv(args, dev) -> dict:
         sweep[str(s)] = round(nbytes / (ms_s * 1e-3) / 1e9, 1)
     return {
         "M": M, "K": K, "N": N, "split": split, "kernel_id": kid, "bytes": nbytes,
-        "ms_per_step": ms, "ms_kernel": ms_kernel, "split_sweep_GBs": sweep,
+        "ms_per_step": ms, "ms_kernel": ms_kernel, "ms_kernel_events": ms_kernel_events,
+        "split_sweep_GBs": sweep,
         "inputs": (a, w),
     }
 
@@ -299,8 +325,9 @@ def main() -> int:
                    "split_k_sweep_GBs": g["split_sweep_GBs"]},
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "w4a16_gemv_kernel (split-K slices)",
+                     "kernel": KERNEL_NAMES.get(g["kernel_id"], "?") + " (split-K slices)",
                      "kernel_us": round(g["ms_kernel"] * 1e3, 3),
+                     "kernel_us_single_launch_events": round(g["ms_kernel_events"] * 1e3, 3),
                      "bytes_per_launch": g["bytes"]},
     }
     if not args.no_secondary:
