@@ -275,6 +275,47 @@ def cpu_baseline(a, w, seconds: float) -> dict:
             "check": float(np.abs(y).sum())}
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "w4a16_gemv_decode_traffic.md"
+COPY_PROBE_BYTES = 256 << 20
+
+
+def traffic_probe(dev) -> int:
+    """Short run for the rocprofv3 --pmc passes: 50 launches of the GEMV slice kernel on
+    rotating weights, then 10 device copies of COPY_PROBE_BYTES (the calibration kernel:
+    it must read and write exactly that many bytes)."""
+    import torch
+
+    import _pk
+
+    M, K, N = 1, 4096, 11008
+    a, w, qws, scs = gemv_inputs(M, K, N, N_ROTATE, dev)
+    ag = a.to(dev)
+    kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
+    parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
+    for i in range(50):
+        _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
+    torch.cuda.synchronize()
+    src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"traffic probe done: split={split} copy_bytes={COPY_PROBE_BYTES}", flush=True)
+    return 0
+
+
+def measured_traffic():
+    """HBM bytes per slice-kernel launch from the committed --pmc summary, or None."""
+    import re
+
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", TRAFFIC_PROFILE.read_text())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -284,6 +325,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true", help="skip the GEMM lines")
     ap.add_argument("--sweep", action="store_true", help="add the Llama-3-8B layer sweep")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the short kernel + copy sequence profiled with --pmc")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -302,6 +345,8 @@ def main() -> int:
         return 1
     _pk.lib()
     dev = torch.device("cuda", 0)
+    if args.traffic_probe:
+        return traffic_probe(dev)
 
     g = bench_gemv(args, dev)
     gbs = g["bytes"] / (g["ms_per_step"] * 1e-3) / 1e9
@@ -324,7 +369,8 @@ def main() -> int:
                    "group_size": 128, "split_k": g["split"], "out_dtype": "fp16",
                    "split_k_sweep_GBs": g["split_sweep_GBs"]},
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
                      "kernel": KERNEL_NAMES.get(g["kernel_id"], "?") + " (split-K slices)",
                      "kernel_us": round(g["ms_kernel"] * 1e3, 3),
                      "kernel_us_single_launch_events": round(g["ms_kernel_events"] * 1e3, 3),
