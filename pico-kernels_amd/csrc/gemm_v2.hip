@@ -236,16 +236,23 @@ __global__ __launch_bounds__(256) void gemm_v2_f16_kernel(V2Params p) {
   store_b(sB0);
   __syncthreads();
   int kt = 0;
+  // The scheduling barriers keep the next tile's loads at the top of each step: left to
+  // itself the compiler sinks them next to their first use, which leaves no time to hide
+  // their latency. B goes first so its dequantisation does not wait for the A DMA.
   for (; kt + 1 < ktiles; kt += 2) {
-    issue_a(kt + 1, sA1);
     load_b(kt + 1);
+    issue_a(kt + 1, sA1);
+    __builtin_amdgcn_sched_barrier(0);
     compute(sA0, sB0);
+    __builtin_amdgcn_sched_barrier(0);
     store_b(sB1);
     __syncthreads();
     const int n2 = min(kt + 2, ktiles - 1);  // the last pair re-reads a valid tile, unused
-    issue_a(n2, sA0);
     load_b(n2);
+    issue_a(n2, sA0);
+    __builtin_amdgcn_sched_barrier(0);
     compute(sA1, sB1);
+    __builtin_amdgcn_sched_barrier(0);
     store_b(sB0);
     __syncthreads();
   }
@@ -426,16 +433,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_v2_f8_kernel(V2Pa
   store_b(sB0);
   __syncthreads();
   int kt = 0;
+  // Scheduling barriers pin the next tile's loads at the top of each step (the compiler
+  // otherwise issues them after the MFMAs, just before the barrier that waits for them).
   for (; kt + 1 < ktiles; kt += 2) {
-    issue_a(kt + 1, sA1);
     issue_b(kt + 1, sB1);
+    issue_a(kt + 1, sA1);
+    __builtin_amdgcn_sched_barrier(0);
     compute(sA0, sB0);
+    __builtin_amdgcn_sched_barrier(0);
     store_b(sB1);
     __syncthreads();
     const int n2 = min(kt + 2, ktiles - 1);
-    issue_a(n2, sA0);
     issue_b(n2, sB0);
+    issue_a(n2, sA0);
+    __builtin_amdgcn_sched_barrier(0);
     compute(sA1, sB1);
+    __builtin_amdgcn_sched_barrier(0);
     store_b(sB0);
     __syncthreads();
   }
