@@ -226,7 +226,7 @@ __global__ __launch_bounds__(256) void gemm_v2_f16_kernel(V2Params p) {
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
     }
   };
 
@@ -258,22 +258,36 @@ __global__ __launch_bounds__(256) void gemm_v2_f16_kernel(V2Params p) {
   }
   if (kt < ktiles) compute(sA0, sB0);
 
-  // ---- epilogue: C[m][n], fragment (i, j) register r at row 8*(r/4) + 4*(lane/32) + r%4 ----
-  const int erow = 4 * (lane >> 5), ecol = lane & 31;
+  // ---- epilogue. The MFMAs take B as the first operand, so fragment (i, j) holds C^T:
+  // register r of a lane is C[m][n] with m = 32i + lane%32 and n = 32j + 8(r/4) + 4(lane/32)
+  // + r%4, i.e. four consecutive columns per register quad -> one 8- or 16-byte store. ----
   float* part = p.split > 1 ? p.partials + (int64_t)blockIdx.y * p.M * p.N : nullptr;
+  const int esz = part ? 4 : (p.c_dtype == PK_F32 ? 4 : 2);
+  const bool vec = part ? true
+                        : (p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & (4 * esz - 1)) == 0);
+  const int em = lane & 31, en = 4 * (lane >> 5);
+  auto epilogue = [&](auto DT) {
+    constexpr int dt = decltype(DT)::value;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + wm0 + 32 * i + 8 * (r >> 2) + erow + (r & 3);
-        const int gn = n0 + wn0 + 32 * j + ecol;
-        if (gm < p.M && gn < p.N) {
-          if (part) part[(int64_t)gm * p.N + gn] = acc[i][j][r];
-          else store_from_f32(p.c, p.c_dtype, (int64_t)gm * p.ldc + gn, acc[i][j][r] * p.scale);
+        for (int q = 0; q < 4; ++q) {
+          const int gm = m0 + wm0 + 32 * i + em;
+          const int gn = n0 + wn0 + 32 * j + 8 * q + en;  // N % 4 == 0: all four in or out
+          if (gm < p.M && gn < p.N) {
+            pk_f4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            if (part) {
+              store4_as<PK_F32>(part, (int64_t)gm * p.N + gn, v, true);
+            } else {
+              v *= p.scale;
+              store4_as<dt>(p.c, (int64_t)gm * p.ldc + gn, v, vec);
+            }
+          }
         }
-      }
+  };
+  with_dtype(part ? PK_F32 : p.c_dtype, epilogue);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -423,7 +437,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_v2_f8_kernel(V2Pa
         const pk_i8v af = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, bf[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af, acc[i][j], 0, 0, 0, 0, 0, 0);
       }
     }
   };
@@ -454,18 +468,28 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_v2_f8_kernel(V2Pa
   }
   if (kt < ktiles) compute(sA0, sB0);
 
-  const int erow = 4 * (lane >> 5), ecol = lane & 31;
+  // epilogue: fragments hold C^T (B is the first MFMA operand), so each register quad is
+  // four consecutive columns of one row -> one 8- or 16-byte store
+  const int esz = p.c_dtype == PK_F32 ? 4 : 2;
+  const bool vec = p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & (4 * esz - 1)) == 0;
+  const int em = lane & 31, en = 4 * (lane >> 5);
+  with_dtype(p.c_dtype, [&](auto DT) {
+    constexpr int dt = decltype(DT)::value;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + wm0 + 32 * i + 8 * (r >> 2) + erow + (r & 3);
-        const int gn = n0 + wn0 + 32 * j + ecol;
-        if (gm < p.M && gn < p.N)
-          store_from_f32(p.c, p.c_dtype, (int64_t)gm * p.ldc + gn, acc[i][j][r] * p.scale);
-      }
+        for (int q = 0; q < 4; ++q) {
+          const int gm = m0 + wm0 + 32 * i + em;
+          const int gn = n0 + wn0 + 32 * j + 8 * q + en;  // N % 16 == 0: all four in or out
+          if (gm < p.M && gn < p.N) {
+            pk_f4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            v *= p.scale;
+            store4_as<dt>(p.c, (int64_t)gm * p.ldc + gn, v, vec);
+          }
+        }
+  });
 }
 
 // ---------------------------------------------------------------------------------------

@@ -88,6 +88,41 @@ __device__ __forceinline__ void store_from_f32(void* p, int dtype, int64_t i, fl
   else reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_rne(v);
 }
 
+// Four consecutive outputs p[i .. i+3] of dtype DT: one 16-byte (fp32) or 8-byte (fp16/bf16)
+// global store when `vec` (the caller has checked alignment), element stores otherwise.
+#define PK_GLOBAL(T, ptr) ((__attribute__((address_space(1))) T*)(ptr))
+template <int DT>
+__device__ __forceinline__ void store4_as(void* p, int64_t i, pk_f4 v, bool vec) {
+  if (!vec) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_from_f32(p, DT, i + e, v[e]);
+    return;
+  }
+  if constexpr (DT == PK_F32) {
+    *PK_GLOBAL(pk_f4, reinterpret_cast<float*>(p) + i) = v;
+  } else if constexpr (DT == PK_F16) {
+    const pk_half4 h = {(pk_half)v[0], (pk_half)v[1], (pk_half)v[2], (pk_half)v[3]};
+    *PK_GLOBAL(pk_u2v, reinterpret_cast<pk_half*>(p) + i) = __builtin_bit_cast(pk_u2v, h);
+  } else {
+    const pk_u2v b = {(uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16),
+                      (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16)};
+    *PK_GLOBAL(pk_u2v, reinterpret_cast<uint16_t*>(p) + i) = b;
+  }
+}
+
+// Calls f(std::integral_constant<int, DT>) for the runtime dtype, so loops inside f see a
+// compile-time dtype.
+template <int V>
+struct pk_int_c {
+  static constexpr int value = V;
+};
+template <typename F>
+__device__ __forceinline__ void with_dtype(int dtype, F f) {
+  if (dtype == PK_F32) f(pk_int_c<PK_F32>{});
+  else if (dtype == PK_F16) f(pk_int_c<PK_F16>{});
+  else f(pk_int_c<PK_BF16>{});
+}
+
 // OCP FP8 E4M3 ("e4m3fn": no infinities, S.1111.111 is NaN, max finite 448).
 // Round-to-nearest-even, NOT saturating: any magnitude that rounds above 448 (that is,
 // anything above 464, the tie point between 448 and the missing 480) and any Inf/NaN input
