@@ -1,0 +1,276 @@
+// e4m3 fp8 GEMM for gfx950, 256 x 256 tiles, 4-stage LDS pipeline, B in either layout
+// through LDS DMA (v_mfma_f32_32x32x64_f8f6f4).
+//
+// C[m, n] = out_scale * sum_k A[m, k] * B[k, n] (gemm_fp8.py:38-117), A (M, K) row-major,
+// B (K, N) row-major (BLAYOUT 0) or (N, K) row-major (BLAYOUT 1, a transposed view).
+//
+// Design:
+//  * 8 waves (2 x 4), each a 128 x 64 block: 4 x 2 fragments of 32 x 32, 64 k per MFMA.
+//  * K tiles of 64. A tile = 256 rows x 64 bytes, B tile = 64 k x 256 n (BLAYOUT 0) or
+//    256 n x 64 k (BLAYOUT 1); both go global -> LDS with buffer DMA (no VGPR staging).
+//  * Four LDS stages (32 KB each); the loads of tile t+3 are issued right after the barrier
+//    of tile t, so three tiles of loads are in flight while one is multiplied. One barrier
+//    per tile; the wait before it lets the two younger tiles' DMAs stay outstanding.
+//  * k-contiguous tiles (A; B^T) use 64-byte rows in 4 chunks of 16 B, chunk c of row r in
+//    slot c ^ ((r >> 2) & 3): 16 lanes reading 16 consecutive rows at one chunk hit 16
+//    distinct 16-byte bank groups.
+//  * (K, N) B keeps n contiguous (256-byte rows, 16 chunks, chunk c of row k in slot
+//    c ^ 2(k & 7)) and is read with ds_read_b64_tr_b8: within a 16-lane group lane j gets
+//    byte b from the address of lane 2b + j/8 at offset j % 8. Even lanes address row k0 + b
+//    at column n, odd lanes the same row at column n + 8, so lane j receives 8 consecutive
+//    k of column n + j -- the MFMA operand layout -- with no transposing in registers.
+//  * The MFMAs take B as the first operand, so each accumulator is C^T and every lane ends
+//    with four consecutive columns of one row per register quad: 8- or 16-byte stores.
+#include "pk_internal.h"
+
+namespace pk {
+
+#define PK_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+typedef int pk_i2v __attribute__((ext_vector_type(2)));
+
+struct F8Params {
+  const uint8_t* a;
+  int64_t lda;
+  const uint8_t* b;
+  int64_t ldb;
+  float scale;
+  void* c;
+  int c_dtype;
+  int64_t ldc;
+  int M, N, K;
+  int tiles_m, tiles_n;
+};
+
+// 16 bytes per lane, global -> LDS (lane L writes lds + 16 L).
+__device__ __forceinline__ void f8_dma16(__amdgpu_buffer_rsrc_t r, char* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, PK_LDS(lds), 16, voff, soff, 0, 0);
+}
+
+__device__ __forceinline__ pk_i2v f8_read_tr(const char* lds) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) pk_i2v*)(lds));
+}
+
+// slot of chunk c of row r in a 64-byte-row tile
+__device__ __forceinline__ int f8_swz64(int r, int c) { return (r << 6) + ((c ^ ((r >> 2) & 3)) << 4); }
+// slot of chunk c of row k in a 256-byte-row tile
+__device__ __forceinline__ int f8_swz256(int k, int c) { return (k << 8) + ((c ^ (2 * (k & 7))) << 4); }
+
+// XCD-aware tile order: consecutive logical tiles on one XCD, grouped 4 tile rows deep.
+__device__ __forceinline__ void f8_tile_of(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int total = tiles_m * tiles_n;
+  int logical = bid;
+  if (total % 8 == 0) logical = (bid % 8) * (total / 8) + bid / 8;
+  constexpr int GROUP_M = 4;
+  const int per_group = GROUP_M * tiles_n;
+  const int g = logical / per_group;
+  const int first_m = g * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  const int in_g = logical - g * per_group;
+  *tm = first_m + in_g % gm;
+  *tn = in_g / gm;
+}
+
+template <int BLAYOUT>
+__global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
+  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int WTM = 128, WTN = 64, FM = 4, FN = 2;
+  constexpr int STAGE = BM * BK;  // bytes per operand per stage (16 KB)
+
+  __shared__ __align__(16) char sA0[STAGE];
+  __shared__ __align__(16) char sA1[STAGE];
+  __shared__ __align__(16) char sA2[STAGE];
+  __shared__ __align__(16) char sA3[STAGE];
+  __shared__ __align__(16) char sB0[STAGE];
+  __shared__ __align__(16) char sB1[STAGE];
+  __shared__ __align__(16) char sB2[STAGE];
+  __shared__ __align__(16) char sB3[STAGE];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm0 = (wave >> 2) * WTM, wn0 = (wave & 3) * WTN;
+  int tm, tn;
+  f8_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int ktiles = p.K / BK;
+
+  // ---- DMA sources: two 1 KB instructions per wave per operand per tile ----
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
+  int a_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (wave * 2 + i) * 16 + (lane >> 2);  // 16 rows of 64 bytes per instruction
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    a_off[i] = (int)((int64_t)min(m0 + r, p.M - 1) * p.lda) + c * 16;
+  }
+  __amdgpu_buffer_rsrc_t rb;
+  int b_off[2];
+  if constexpr (BLAYOUT == 1) {
+    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = (wave * 2 + i) * 16 + (lane >> 2);
+      const int c = (lane & 3) ^ ((r >> 2) & 3);
+      b_off[i] = (int)((int64_t)min(n0 + r, p.N - 1) * p.ldb) + c * 16;
+    }
+  } else {
+    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.K * p.ldb));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int k = (wave * 2 + i) * 4 + (lane >> 4);  // 4 rows of 256 bytes per instruction
+      const int c = (lane & 15) ^ (2 * (k & 7));
+      b_off[i] = (int)((int64_t)k * p.ldb) + min(n0 + c * 16, p.N - 16);
+    }
+  }
+  auto issue = [&](int kt, char* sA, char* sB) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) f8_dma16(ra, sA + (wave * 2 + i) * 1024, a_off[i], kt * BK);
+    const int bs = BLAYOUT == 1 ? kt * BK : (int)((int64_t)kt * BK * p.ldb);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) f8_dma16(rb, sB + (wave * 2 + i) * 1024, b_off[i], bs);
+  };
+
+  // ---- fragment offsets inside a stage ----
+  int aoff[FM][2];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) aoff[i][h] = f8_swz64(wm0 + 32 * i + (lane & 31), 2 * (lane >> 5) + h);
+  int boff[FN][4];  // BLAYOUT 1: [j][h] chunk pair; BLAYOUT 0: [j][q] transposing reads
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    if constexpr (BLAYOUT == 1) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) boff[j][h] = f8_swz64(wn0 + 32 * j + (lane & 31), 2 * (lane >> 5) + h);
+      boff[j][2] = boff[j][3] = 0;
+    } else {
+      const int i16 = lane & 15;
+      const int cs = wn0 + 32 * j + 16 * ((lane >> 4) & 1) + 8 * (i16 & 1);  // first column
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int k = 32 * (lane >> 5) + 8 * q + (i16 >> 1);
+        boff[j][q] = f8_swz256(k, cs >> 4) + (cs & 15);
+      }
+    }
+  }
+
+  pk_f16v acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = (pk_f16v){};
+
+  auto compute = [&](const char* sA, const char* sB) {
+    pk_i8v bf[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (BLAYOUT == 1) {
+        const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sB + boff[j][0]);
+        const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sB + boff[j][1]);
+        bf[j] = (pk_i8v){(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+      } else {
+        const pk_i2v y0 = f8_read_tr(sB + boff[j][0]);
+        const pk_i2v y1 = f8_read_tr(sB + boff[j][1]);
+        const pk_i2v y2 = f8_read_tr(sB + boff[j][2]);
+        const pk_i2v y3 = f8_read_tr(sB + boff[j][3]);
+        bf[j] = (pk_i8v){y0[0], y0[1], y1[0], y1[1], y2[0], y2[1], y3[0], y3[1]};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sA + aoff[i][0]);
+      const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sA + aoff[i][1]);
+      const pk_i8v af = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af, acc[i][j], 0, 0, 0, 0, 0, 0);
+    }
+  };
+
+  // ---- pipeline. Tiles past the end are re-reads of the last tile into a stage nobody
+  // reads, so every step has exactly the same number of DMAs in flight (4 per tile). ----
+  const int last = ktiles - 1;
+  issue(0, sA0, sB0);
+  issue(min(1, last), sA1, sB1);
+  issue(min(2, last), sA2, sB2);
+  // s_waitcnt vmcnt(8) expcnt(7) lgkmcnt(15): this wave's DMAs of the oldest tile landed.
+  // The barrier is a bare s_barrier: __syncthreads() adds a workgroup release fence, which
+  // waits for *every* outstanding LDS DMA (vmcnt(0)) and would serialise the pipeline. The
+  // explicit wait above already covers the data this barrier publishes, and the asm memory
+  // clobber keeps the compiler from moving LDS accesses across it.
+  constexpr int kWaitOldest = 0x0f78;
+  auto step = [&](int kt, char* sAc, char* sBc, char* sAn, char* sBn) {
+    __builtin_amdgcn_s_waitcnt(kWaitOldest);
+    asm volatile("s_barrier" ::: "memory");
+    issue(min(kt + 3, last), sAn, sBn);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sAc, sBc);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int kt = 0;
+  for (; kt + 3 < ktiles; kt += 4) {
+    step(kt, sA0, sB0, sA3, sB3);
+    step(kt + 1, sA1, sB1, sA0, sB0);
+    step(kt + 2, sA2, sB2, sA1, sB1);
+    step(kt + 3, sA3, sB3, sA2, sB2);
+  }
+  if (kt < ktiles) step(kt, sA0, sB0, sA3, sB3);
+  if (kt + 1 < ktiles) step(kt + 1, sA1, sB1, sA0, sB0);
+  if (kt + 2 < ktiles) step(kt + 2, sA2, sB2, sA1, sB1);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no DMA into LDS outlives the waves
+  mfma_drain();
+
+  // ---- epilogue: register quad q of fragment (i, j) = C[m][n .. n+3] ----
+  const int esz = p.c_dtype == PK_F32 ? 4 : 2;
+  const bool vec = p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & (4 * esz - 1)) == 0;
+  const int em = lane & 31, en = 4 * (lane >> 5);
+  with_dtype(p.c_dtype, [&](auto DT) {
+    constexpr int dt = decltype(DT)::value;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int gm = m0 + wm0 + 32 * i + em;
+          const int gn = n0 + wn0 + 32 * j + 8 * q + en;  // N % 16 == 0: all four in or out
+          if (gm < p.M && gn < p.N) {
+            pk_f4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            v *= p.scale;
+            store4_as<dt>(p.c, (int64_t)gm * p.ldc + gn, v, vec);
+          }
+        }
+  });
+}
+
+bool f8_v3_ok(int M, int N, int K, int64_t lda, int64_t ldb, int b_layout, const void* b) {
+  if (M < 256 || N < 256 || K % 64 || N % 16 || lda % 16 || ldb % 16) return false;
+  if ((reinterpret_cast<uintptr_t>(b) & 15) != 0) return false;
+  if ((int64_t)M * lda >= (1ll << 31)) return false;
+  return (b_layout == 1 ? (int64_t)N * ldb : (int64_t)K * ldb) < (1ll << 31);
+}
+
+int f8_v3_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb, int b_layout,
+                 float out_scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                 hipStream_t s) {
+  F8Params p;
+  p.a = a8;
+  p.lda = lda;
+  p.b = b8;
+  p.ldb = ldb;
+  p.scale = out_scale;
+  p.c = c;
+  p.c_dtype = c_dtype;
+  p.ldc = ldc;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.tiles_m = (int)cdiv(M, 256);
+  p.tiles_n = (int)cdiv(N, 256);
+  const dim3 grid(p.tiles_m * p.tiles_n);
+  if (b_layout == 1) gemm_f8_v3_kernel<1><<<grid, 512, 0, s>>>(p);
+  else gemm_f8_v3_kernel<0><<<grid, 512, 0, s>>>(p);
+  PK_LAUNCH_CHECK("fp8 gemm (v3)");
+  return PK_OK;
+}
+
+}  // namespace pk

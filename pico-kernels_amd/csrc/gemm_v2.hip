@@ -257,6 +257,7 @@ __global__ __launch_bounds__(256) void gemm_v2_f16_kernel(V2Params p) {
     __syncthreads();
   }
   if (kt < ktiles) compute(sA0, sB0);
+  mfma_drain();
 
   // ---- epilogue. The MFMAs take B as the first operand, so fragment (i, j) holds C^T:
   // register r of a lane is C[m][n] with m = 32i + lane%32 and n = 32j + 8(r/4) + 4(lane/32)
@@ -467,6 +468,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_v2_f8_kernel(V2Pa
     __syncthreads();
   }
   if (kt < ktiles) compute(sA0, sB0);
+  mfma_drain();
 
   // epilogue: fragments hold C^T (B is the first MFMA operand), so each register quad is
   // four consecutive columns of one row -> one 8- or 16-byte store

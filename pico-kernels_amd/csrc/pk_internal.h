@@ -46,4 +46,11 @@ int v2_f8_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb,
                  float out_scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
                  hipStream_t s);
 
+// 256 x 256 fp8 GEMM with a 4-stage DMA pipeline and transposing LDS reads for (K, N) B
+// (gemm_f8_v3.hip).
+bool f8_v3_ok(int M, int N, int K, int64_t lda, int64_t ldb, int b_layout, const void* b);
+int f8_v3_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb, int b_layout,
+                 float out_scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                 hipStream_t s);
+
 }  // namespace pk

@@ -239,6 +239,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmP
     __syncthreads();
   }
 
+  mfma_drain();
   // ---------------- epilogue --------------------------------------------------------------
   // Fragment (i, j), register r holds C[m0+wm0+16i+4*(lane/16)+r][n0+wn0+16j+lane%16].
   const int erow = 4 * (lane >> 4), ecol = lane & 15;

@@ -106,7 +106,11 @@ def _fp8_case(M, K, N, seed, cuda):
 
 
 @pytest.mark.parametrize("M,K,N", [(256, 256, 256), (100, 384, 264), (1, 128, 8), (513, 1024, 520),
-                                   (2048, 2048, 2048)])
+                                   (2048, 2048, 2048),
+                                   # large-tile kernel: ragged M/N tiles, 2-, 6- and 10-tile K loops
+                                   (600, 384, 784), (300, 128, 272), (257, 640, 528),
+                                   # 128 x 128 kernel, (K, N) B, odd tile count
+                                   (100, 384, 272), (128, 384, 256)])
 def test_fp8_gemm_matches_closed_form(M, K, N, cuda):
     a, b, a8, sa, b8, sb = _fp8_case(M, K, N, M + K + N, cuda)
     c = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb)
@@ -135,8 +139,9 @@ def test_fp8_full_size_4096(cuda):
     assert 0.02 < err_gpu < 0.06  # the ~3.7% the reference reports for N(0,1) inputs
 
 
-def test_fp8_transposed_b_layout(cuda):
-    a, b, a8, sa, b8, sb = _fp8_case(256, 512, 384, 77, cuda)
+@pytest.mark.parametrize("M,K,N", [(256, 512, 384), (600, 384, 784), (100, 384, 272)])
+def test_fp8_transposed_b_layout(M, K, N, cuda):
+    a, b, a8, sa, b8, sb = _fp8_case(M, K, N, 77, cuda)
     c0 = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb)
     bt = b8.t().contiguous()  # (N, K) buffer
     c1 = gemm_fp8.fp8_gemm_precast(a8, sa, bt.t(), sb)  # (K, N) view of it

@@ -127,6 +127,18 @@ def test_w4a16_shapes(M, cuda):
         assert err <= 1e-4, f"M={M}: rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("M,K,N", [(128, 192, 528), (300, 320, 256), (600, 448, 784), (256, 64, 256)])
+def test_w4a16_odd_k_tile_counts(M, K, N, cuda):
+    """Odd numbers of 64-row K tiles end the MFMA kernels' two-stage loop on a lone tile; its
+    accumulators must be complete before the epilogue reads them (group 64 so K can be 192)."""
+    a, w, qw, sc, codes, s16 = _group_case(M, K, N, 5 * M + K, cuda, G=64)
+    for out_dtype in (torch.float32, torch.float16):
+        out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, 64, out_dtype=out_dtype)
+        ref = oracle.w4a16_ref(a.numpy(), codes, s16, 64)
+        err = oracle.rel_fro(out.float().cpu().numpy(), ref)
+        assert err <= (W4A16_TOL if out_dtype == torch.float32 else 2e-3), (M, K, N, out_dtype, err)
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_w4a16_output_dtypes(out_dtype, cuda):
     a, w, qw, sc, codes, s16 = _group_case(64, 512, 256, 7, cuda)

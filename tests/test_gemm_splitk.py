@@ -54,3 +54,13 @@ def test_splitk_divisibility_contract(cuda):
     b = torch.randn(192, 64, generator=_gen(6)).half().to(cuda)
     with pytest.raises(AssertionError):
         gemm_splitk.triton_gemm_splitk(a, b, split_k=4)  # 192 % (4 * 64) != 0
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 192, 256), (300, 320, 528), (128, 448, 384)])
+def test_dense_odd_k_tile_counts(M, K, N, cuda):
+    """Odd numbers of 64-wide K tiles through the large-tile MFMA kernel, against fp32."""
+    a = torch.randn(M, K, generator=_gen(M + K)).half()
+    b = torch.randn(K, N, generator=_gen(M + N)).half()
+    c = gemm_splitk.triton_gemm_splitk(a.to(cuda), b.to(cuda), split_k=1)
+    ref = (a.float() @ b.float()).numpy()
+    assert oracle.rel_fro(c.cpu().numpy(), ref) < 1e-5
