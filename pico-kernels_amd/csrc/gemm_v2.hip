@@ -292,6 +292,233 @@ __global__ __launch_bounds__(256) void gemm_v2_f16_kernel(V2Params p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// 3-stage f16 MFMA kernel, 256 x 128 tiles (A fp16 (M, K); B int4 words or fp16 (K, N)).
+//
+// Same tile, wave layout, swizzle, B dequantisation and epilogue as gemm_v2_f16_kernel, with
+// a deeper pipeline: three LDS stages of 48 KB, the A DMA of tile t+2 and the B words of
+// tile t+2 issued after the barrier of tile t, and the B words of tile t+1 dequantised into
+// their stage while tile t is multiplied. Per tile one bare s_barrier: __syncthreads() would
+// add a release fence that waits for every outstanding LDS DMA and undo the prefetch; the
+// explicit wait before the barrier (this wave's DMA of tile t and its ds_writes of tile t's
+// B) publishes exactly what the next step reads.
+// ---------------------------------------------------------------------------------------
+template <int BMODE, bool GS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_v3_f16_kernel(V2Params p) {
+  constexpr int BM = 256, BN = 128;
+  constexpr int WTM = 128, WTN = 64, FM = 4, FN = 2;
+  constexpr int A_DMA = BM / 32;  // 1 KB DMA instructions per wave per tile
+  constexpr int BCG = BN / 8, BROWS = 256 / BCG, RPT = 64 / BROWS;  // 16, 16, 4
+  constexpr bool has_gs = GS;
+
+  __shared__ __align__(16) char sA0[BM * 128];
+  __shared__ __align__(16) char sA1[BM * 128];
+  __shared__ __align__(16) char sA2[BM * 128];
+  __shared__ __align__(16) char sB0[BN * 128];
+  __shared__ __align__(16) char sB1[BN * 128];
+  __shared__ __align__(16) char sB2[BN * 128];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm0 = (wave >> 1) * WTM, wn0 = (wave & 1) * WTN;
+  int tm, tn;
+  v2_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int k_begin = blockIdx.y * p.k_slice;
+  const int ktiles = p.k_slice / 64;
+  const int last = ktiles - 1;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda * 2));
+  int a_off[A_DMA];
+#pragma unroll
+  for (int i = 0; i < A_DMA; ++i) {
+    const int r = (wave * A_DMA + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_off[i] = (int)((int64_t)min(m0 + r, p.M - 1) * p.lda * 2) + c * 16;
+  }
+  auto issue_a = [&](int kt, char* sA) {
+    const int soff = (k_begin + kt * 64) * 2;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) dma16(ra, sA + (wave * A_DMA + i) * 1024, a_off[i], soff);
+  };
+
+  const int brg = t % BROWS, bcg = t / BROWS;
+  const int bn = min(n0 + bcg * 8, p.N - 8);
+  __amdgpu_buffer_rsrc_t rb;
+  int b_off;
+  if (BMODE == kV2Int4) {
+    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.K * p.ldb * 4));
+    b_off = (int)(((int64_t)brg * RPT * p.ldb + (bn >> 3)) * 4);
+  } else {
+    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.K * p.ldb * 2));
+    b_off = (int)(((int64_t)brg * RPT * p.ldb + bn) * 2);
+  }
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc(p.scales, has_gs ? (uint32_t)((int64_t)(p.K / p.group) * p.N * 2) : 16u);
+  uint32_t breg[3][RPT][4];
+  pk_u4v sreg[3] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  auto load_b = [&](int kt, auto SLOT) {
+    constexpr int sl = decltype(SLOT)::value;
+    const int k0 = k_begin + kt * 64;
+    if (BMODE == kV2Int4) {
+      const int soff = (int)((int64_t)k0 * p.ldb * 4);
+#pragma unroll
+      for (int r = 0; r < RPT; ++r)
+        breg[sl][r][0] = __builtin_amdgcn_raw_buffer_load_b32(rb, b_off + (int)(r * p.ldb * 4), soff, 0);
+      if constexpr (has_gs) sreg[sl] = __builtin_amdgcn_raw_buffer_load_b128(rs, bn * 2, (k0 / p.group) * p.N * 2, 0);
+    } else {
+      const int soff = (int)((int64_t)k0 * p.ldb * 2);
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        const pk_u4v v = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off + (int)(r * p.ldb * 2), soff, 0);
+        breg[sl][r][0] = v[0]; breg[sl][r][1] = v[1]; breg[sl][r][2] = v[2]; breg[sl][r][3] = v[3];
+      }
+    }
+  };
+  auto store_b = [&](auto SLOT, char* sB) {
+    constexpr int sl = decltype(SLOT)::value;
+    uint32_t col[8][RPT / 2];
+    if (BMODE == kV2Int4) {
+      uint32_t w[RPT];
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) w[r] = breg[sl][r][0] ^ 0x88888888u;
+      const pk_half2 bias = {(pk_half)1032.0f, (pk_half)1032.0f};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
+#pragma unroll
+        for (int r2 = 0; r2 < RPT / 2; ++r2) {
+          const uint32_t pr = __builtin_amdgcn_perm(w[2 * r2 + 1], w[2 * r2], sel);
+#pragma unroll
+          for (int hs = 0; hs < 2; ++hs) {
+            const int cidx = 2 * b + hs;
+            const uint32_t nib = hs ? (pr >> 4) : pr;
+            pk_half2 q = h2v((nib & 0x000f000fu) | 0x64006400u) - bias;  // exact codes
+            if constexpr (has_gs) {
+              const uint32_t sv = sreg[sl][cidx >> 1];
+              const uint32_t s1 = (cidx & 1) ? (sv >> 16) : (sv & 0xffffu);
+              q = q * h2v(s1 | (s1 << 16));
+            }
+            col[cidx][r2] = u32v(q);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+        for (int r2 = 0; r2 < RPT / 2; ++r2)
+          col[c][r2] = __builtin_amdgcn_perm(breg[sl][2 * r2 + 1][c >> 1], breg[sl][2 * r2][c >> 1], sel);
+      }
+    }
+    const int kb = RPT * brg * 2;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int n = bcg * 8 + c;
+      pk_u2v v = {col[c][0], col[c][1]};
+      *reinterpret_cast<pk_u2v*>(sB + swz(n, kb >> 4) + (kb & 15)) = v;
+    }
+  };
+
+  int aoff[FM][4], boff[FN][4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) aoff[i][ks] = swz(wm0 + 32 * i + (lane & 31), 2 * ks + (lane >> 5));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) boff[j][ks] = swz(wn0 + 32 * j + (lane & 31), 2 * ks + (lane >> 5));
+  }
+  pk_f16v acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = (pk_f16v){};
+  // Fragments of k-step ks+1 are read while the MFMAs of k-step ks run (two register sets).
+  auto compute = [&](const char* sA, const char* sB) {
+    pk_half8 af[2][FM], bf[2][FN];
+    auto read = [&](int ks, int bsel) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[bsel][i] = *reinterpret_cast<const pk_half8*>(sA + aoff[i][ks]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[bsel][j] = *reinterpret_cast<const pk_half8*>(sB + boff[j][ks]);
+    };
+    read(0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);  // DS reads of k-step 0
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks < 3) read(ks + 1, (ks + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[ks & 1][j], af[ks & 1][i], acc[i][j], 0, 0, 0);
+      // order: the next k-step's fragment reads, then this k-step's MFMAs
+      if (ks < 3) __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
+    }
+  };
+
+  // Per step this wave issues 5 (int4: 4 words + scales) or 4 (fp16) B loads, then 8 DMAs.
+  // s_waitcnt vmcnt(V) expcnt(7) lgkmcnt(0): everything but the previous step's loads done.
+  constexpr int kStepLoads = (BMODE == kV2Int4 ? (has_gs ? 5 : 4) : 4) + A_DMA;
+  constexpr int kWaitTile = (kStepLoads & 15) | (7 << 4) | ((kStepLoads >> 4) << 14);
+  // prologue: tiles 0 and 1 in flight, tile 0's B in its stage
+  load_b(0, pk_int_c<0>{});
+  issue_a(0, sA0);
+  load_b(min(1, last), pk_int_c<1>{});
+  issue_a(min(1, last), sA1);
+  store_b(pk_int_c<0>{}, sB0);
+  auto step = [&](int kt, auto S, char* sAc, char* sBc, char* sAn, char* sBn1) {
+    constexpr int st = decltype(S)::value;
+    __builtin_amdgcn_s_waitcnt(kWaitTile);
+    asm volatile("s_barrier" ::: "memory");
+    load_b(min(kt + 2, last), pk_int_c<(st + 2) % 3>{});
+    issue_a(min(kt + 2, last), sAn);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sAc, sBc);
+    __builtin_amdgcn_sched_barrier(0);
+    store_b(pk_int_c<(st + 1) % 3>{}, sBn1);
+  };
+  int kt = 0;
+  for (; kt + 2 < ktiles; kt += 3) {
+    step(kt, pk_int_c<0>{}, sA0, sB0, sA2, sB1);
+    step(kt + 1, pk_int_c<1>{}, sA1, sB1, sA0, sB2);
+    step(kt + 2, pk_int_c<2>{}, sA2, sB2, sA1, sB0);
+  }
+  if (kt < ktiles) step(kt, pk_int_c<0>{}, sA0, sB0, sA2, sB1);
+  if (kt + 1 < ktiles) step(kt + 1, pk_int_c<1>{}, sA1, sB1, sA0, sB2);
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): no DMA into LDS outlives the waves
+  mfma_drain();
+
+  float* part = p.split > 1 ? p.partials + (int64_t)blockIdx.y * p.M * p.N : nullptr;
+  const int esz = part ? 4 : (p.c_dtype == PK_F32 ? 4 : 2);
+  const bool vec = part ? true
+                        : (p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & (4 * esz - 1)) == 0);
+  const int em = lane & 31, en = 4 * (lane >> 5);
+  with_dtype(part ? PK_F32 : p.c_dtype, [&](auto DT) {
+    constexpr int dt = decltype(DT)::value;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int gm = m0 + wm0 + 32 * i + em;
+          const int gn = n0 + wn0 + 32 * j + 8 * q + en;
+          if (gm < p.M && gn < p.N) {
+            pk_f4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            if (part) {
+              store4_as<PK_F32>(part, (int64_t)gm * p.N + gn, v, true);
+            } else {
+              v *= p.scale;
+              store4_as<dt>(p.c, (int64_t)gm * p.ldc + gn, v, vec);
+            }
+          }
+        }
+  });
+}
+
+// ---------------------------------------------------------------------------------------
 // fp8 MFMA kernel (A e4m3 (M, K); B e4m3 (K, N) or (N, K)); BK = 128.
 // ---------------------------------------------------------------------------------------
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BLAYOUT>
@@ -525,14 +752,14 @@ int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, 
   const bool gs = scales != nullptr;
   if (bmode == kV2Int4) {
     if (bm == 256) {
-      if (gs) gemm_v2_f16_kernel<256, 128, kV2Int4, true><<<grid, 256, 0, s>>>(p);
-      else gemm_v2_f16_kernel<256, 128, kV2Int4, false><<<grid, 256, 0, s>>>(p);
+      if (gs) gemm_v3_f16_kernel<kV2Int4, true><<<grid, 256, 0, s>>>(p);
+      else gemm_v3_f16_kernel<kV2Int4, false><<<grid, 256, 0, s>>>(p);
     } else {
       if (gs) gemm_v2_f16_kernel<128, 128, kV2Int4, true><<<grid, 256, 0, s>>>(p);
       else gemm_v2_f16_kernel<128, 128, kV2Int4, false><<<grid, 256, 0, s>>>(p);
     }
   } else {
-    if (bm == 256) gemm_v2_f16_kernel<256, 128, kV2F16KN, false><<<grid, 256, 0, s>>>(p);
+    if (bm == 256) gemm_v3_f16_kernel<kV2F16KN, false><<<grid, 256, 0, s>>>(p);
     else gemm_v2_f16_kernel<128, 128, kV2F16KN, false><<<grid, 256, 0, s>>>(p);
   }
   PK_LAUNCH_CHECK("gemm v2 f16");
