@@ -374,6 +374,15 @@ void gemm_v3_f16_kernel(V2Params p) {
       }
     }
   };
+  // row r of tile kt's B words (int4), and the tile's scales with row 0
+  auto load_b_row = [&](int kt, auto SLOT, int r) {
+    constexpr int sl = decltype(SLOT)::value;
+    const int k0 = k_begin + kt * 64;
+    breg[sl][r][0] = __builtin_amdgcn_raw_buffer_load_b32(rb, b_off + (int)(r * p.ldb * 4), (int)((int64_t)k0 * p.ldb * 4), 0);
+    if constexpr (has_gs) {
+      if (r == 0) sreg[sl] = __builtin_amdgcn_raw_buffer_load_b128(rs, bn * 2, (k0 / p.group) * p.N * 2, 0);
+    }
+  };
   auto store_b = [&](auto SLOT, char* sB) {
     constexpr int sl = decltype(SLOT)::value;
     uint32_t col[8][RPT / 2];
@@ -433,8 +442,19 @@ void gemm_v3_f16_kernel(V2Params p) {
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = (pk_f16v){};
-  // Fragments of k-step ks+1 are read while the MFMAs of k-step ks run (two register sets).
-  auto compute = [&](const char* sA, const char* sB) {
+  // int4 B: the dequantisation of tile t+1 is written out in four pieces (one byte position
+  // = two columns each) and woven between the MFMAs of tile t in source order, fenced by
+  // scheduling barriers: a wave issues in order, and with one wave per SIMD its VALU work
+  // only overlaps the matrix pipe when it sits between MFMAs. Fragment reads run one k-step
+  // ahead of the MFMAs that use them.
+  auto issue_a_part = [&](int kt, char* sA, int part) {  // DMAs 2*part, 2*part+1 of a tile
+    const int soff = (k_begin + kt * 64) * 2;
+#pragma unroll
+    for (int i = 2 * part; i < 2 * part + 2; ++i) dma16(ra, sA + (wave * A_DMA + i) * 1024, a_off[i], soff);
+  };
+  auto compute_store = [&](const char* sA, const char* sB, auto SLOT, char* sBn, int kta, char* sAn,
+                           auto LSLOT) {
+    constexpr int sl = decltype(SLOT)::value;
     pk_half8 af[2][FM], bf[2][FN];
     auto read = [&](int ks, int bsel) {
 #pragma unroll
@@ -442,19 +462,76 @@ void gemm_v3_f16_kernel(V2Params p) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) bf[bsel][j] = *reinterpret_cast<const pk_half8*>(sB + boff[j][ks]);
     };
-    read(0, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);  // DS reads of k-step 0
+    auto mfma2 = [&](int ks, int i) {  // fragment row i, both fragment columns
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      if (ks < 3) read(ks + 1, (ks + 1) & 1);
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[ks & 1][j], af[ks & 1][i], acc[i][j], 0, 0, 0);
+    };
+    if constexpr (BMODE == kV2Int4) {
+      uint32_t w[RPT];
+      const pk_half2 bias = {(pk_half)1032.0f, (pk_half)1032.0f};
+      uint32_t col[2][RPT / 2];  // the two columns of the current piece
+      const int kb = RPT * brg * 2;
+      // piece b, row pair r2: columns 2b (low nibbles) and 2b+1 (high nibbles)
+      auto dq = [&](int b, int r2) {
+        const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
+        const uint32_t pr = __builtin_amdgcn_perm(w[2 * r2 + 1], w[2 * r2], sel);
+        pk_half2 lo = h2v((pr & 0x000f000fu) | 0x64006400u) - bias;  // exact codes
+        pk_half2 hi = h2v(((pr >> 4) & 0x000f000fu) | 0x64006400u) - bias;
+        if constexpr (has_gs) {
+          const uint32_t sv = sreg[sl][b];
+          lo = lo * h2v(__builtin_amdgcn_perm(sv, sv, 0x01000100u));  // (s_lo, s_lo)
+          hi = hi * h2v(__builtin_amdgcn_perm(sv, sv, 0x03020302u));  // (s_hi, s_hi)
+        }
+        col[0][r2] = u32v(lo);
+        col[1][r2] = u32v(hi);
+      };
+      auto put = [&](int b) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+        for (int h = 0; h < 2; ++h) {
+          const int n = bcg * 8 + 2 * b + h;
+          pk_u2v v = {col[h][0], col[h][1]};
+          *reinterpret_cast<pk_u2v*>(sBn + swz(n, kb >> 4) + (kb & 15)) = v;
+        }
+      };
+      read(0, 0);
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[ks & 1][j], af[ks & 1][i], acc[i][j], 0, 0, 0);
-      // order: the next k-step's fragment reads, then this k-step's MFMAs
-      if (ks < 3) __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
+      for (int r = 0; r < RPT; ++r) w[r] = breg[sl][r][0] ^ 0x88888888u;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks < 3) read(ks + 1, (ks + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma2(ks, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_a_part(kta, sAn, ks);  // the next-but-one tile's A and B, spread over the k-steps
+        load_b_row(kta, LSLOT, ks);
+        __builtin_amdgcn_sched_barrier(0);
+        dq(ks, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma2(ks, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        dq(ks, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma2(ks, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        put(ks);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma2(ks, 3);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      read(0, 0);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks < 3) read(ks + 1, (ks + 1) & 1);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) mfma2(ks, i);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_a_part(kta, sAn, ks);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      store_b(SLOT, sBn);
     }
   };
 
@@ -472,12 +549,11 @@ void gemm_v3_f16_kernel(V2Params p) {
     constexpr int st = decltype(S)::value;
     __builtin_amdgcn_s_waitcnt(kWaitTile);
     asm volatile("s_barrier" ::: "memory");
-    load_b(min(kt + 2, last), pk_int_c<(st + 2) % 3>{});
-    issue_a(min(kt + 2, last), sAn);
+    if constexpr (BMODE != kV2Int4) load_b(min(kt + 2, last), pk_int_c<(st + 2) % 3>{});
     __builtin_amdgcn_sched_barrier(0);
-    compute(sAc, sBc);
+    compute_store(sAc, sBc, pk_int_c<(st + 1) % 3>{}, sBn1, min(kt + 2, last), sAn,
+                  pk_int_c<(st + 2) % 3>{});
     __builtin_amdgcn_sched_barrier(0);
-    store_b(pk_int_c<(st + 1) % 3>{}, sBn1);
   };
   int kt = 0;
   for (; kt + 2 < ktiles; kt += 3) {
