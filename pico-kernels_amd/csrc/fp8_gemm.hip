@@ -283,9 +283,9 @@ extern "C" int pk_fp8_gemm(const uint8_t* a8, int64_t lda, const uint8_t* b8, in
                      (reinterpret_cast<uintptr_t>(b8) & 15) == 0 &&
                      (int64_t)M * lda < (1ll << 31) &&
                      (b_layout == 1 ? (int64_t)N * ldb : (int64_t)K * ldb) < (1ll << 31);
-  // (K, N) B: the 4-stage kernel with transposing LDS reads. (N, K) B: both kernels DMA B;
-  // the 2-stage 128-deep kernel has half the barriers and measured faster at 4096^3.
-  if (b_layout == 0 && f8_v3_ok(M, N, K, lda, ldb, b_layout, b8))
+  // Large shapes: the 4-stage kernel (both B layouts through LDS DMA; (K, N) B is read with
+  // transposing LDS loads). Smaller ones: the 2-stage kernel with 128 x 128 tiles.
+  if (f8_v3_ok(M, N, K, lda, ldb, b_layout, b8))
     return f8_v3_launch(a8, lda, b8, ldb, b_layout, out_scale, c, c_dtype, ldc, M, N, K, s);
   if (v2_ok) return v2_f8_launch(a8, lda, b8, ldb, b_layout, out_scale, c, c_dtype, ldc, M, N, K, s);
   const bool big = (int64_t)M * N >= (int64_t)2048 * 2048;

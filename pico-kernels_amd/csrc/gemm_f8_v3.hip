@@ -121,12 +121,18 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
       b_off[i] = (int)((int64_t)k * p.ldb) + min(n0 + c * 16, p.N - 16);
     }
   }
+  // DMA `part` (0, 1: A; 2, 3: B) of tile kt
+  auto issue_part = [&](int kt, char* sA, char* sB, int part) {
+    if (part < 2) {
+      f8_dma16(ra, sA + (wave * 2 + part) * 1024, a_off[part], kt * BK);
+    } else {
+      const int bs = BLAYOUT == 1 ? kt * BK : (int)((int64_t)kt * BK * p.ldb);
+      f8_dma16(rb, sB + (wave * 2 + part - 2) * 1024, b_off[part - 2], bs);
+    }
+  };
   auto issue = [&](int kt, char* sA, char* sB) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) f8_dma16(ra, sA + (wave * 2 + i) * 1024, a_off[i], kt * BK);
-    const int bs = BLAYOUT == 1 ? kt * BK : (int)((int64_t)kt * BK * p.ldb);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) f8_dma16(rb, sB + (wave * 2 + i) * 1024, b_off[i], bs);
+    for (int part = 0; part < 4; ++part) issue_part(kt, sA, sB, part);
   };
 
   // ---- fragment offsets inside a stage ----
@@ -159,7 +165,10 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = (pk_f16v){};
 
-  auto compute = [&](const char* sA, const char* sB) {
+  // The fragment reads of the tile, then its MFMAs in pairs with one of the next DMAs after
+  // each pair: issuing the DMAs in one burst fills the TA address FIFO and stalls the wave
+  // before its first MFMA.
+  auto compute_issue = [&](const char* sA, const char* sB, int ktn, char* sAn, char* sBn) {
     pk_i8v bf[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
@@ -175,14 +184,21 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
         bf[j] = (pk_i8v){y0[0], y0[1], y1[0], y1[1], y2[0], y2[1], y3[0], y3[1]};
       }
     }
+    pk_i8v af[FM];
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sA + aoff[i][0]);
       const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sA + aoff[i][1]);
-      const pk_i8v af = {(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+      af[i] = (pk_i8v){(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af, acc[i][j], 0, 0, 0, 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[i][j], 0, 0, 0, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_part(ktn, sAn, sBn, i);
     }
   };
 
@@ -201,9 +217,7 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
   auto step = [&](int kt, char* sAc, char* sBc, char* sAn, char* sBn) {
     __builtin_amdgcn_s_waitcnt(kWaitOldest);
     asm volatile("s_barrier" ::: "memory");
-    issue(min(kt + 3, last), sAn, sBn);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(sAc, sBc);
+    compute_issue(sAc, sBc, min(kt + 3, last), sAn, sBn);
     __builtin_amdgcn_sched_barrier(0);
   };
   int kt = 0;
