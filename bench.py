@@ -35,7 +35,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2516.6  # dense fp16 (256 CU x 2.4 GHz x 4096 FLOP/clk)
 MFMA_F8_PEAK_TFLOPS = 5033.2   # dense fp8
 N_ROTATE = 40
-KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v2_f16_kernel"}
+KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v2_f16_kernel", 3: "w4a16_skinny_kernel"}
 
 
 def _gen(seed: int):
@@ -234,9 +234,15 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
             ms = GraphTimer(lambda i: _pk.w4a16_gemm(a, qws[i % nrot], scs[i % nrot], 128, 1.0,
                                                      torch.float16, out=out), iters, 2).run()
             by = w4a16_bytes(M, K, N)
+            flop = 2.0 * M * N * K
+            # the applicable roof: the slower of streaming the bytes and issuing the MFMAs
+            t_hbm = by / (HBM_PEAK_GBS * 1e9)
+            t_mfma = flop / (MFMA_F16_PEAK_TFLOPS * 1e12)
             rows.append({"layer": name, "M": M, "K": K, "N": N, "us": round(ms * 1e3, 2),
                          "GB/s": round(by / (ms * 1e-3) / 1e9, 1),
-                         "TFLOP/s": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2)})
+                         "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
+                         "bound": "hbm" if t_hbm >= t_mfma else "mfma",
+                         "frac": round(max(t_hbm, t_mfma) / (ms * 1e-3), 4)})
         del qws, scs
     return rows
 

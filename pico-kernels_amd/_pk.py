@@ -25,7 +25,7 @@ _TORCH_TO_PK = {torch.float32: PK_F32, torch.float16: PK_F16, torch.bfloat16: PK
 
 PK_OK, PK_EINVAL, PK_EUNSUPPORTED, PK_EWORKSPACE, PK_EHIP = 0, -1, -2, -3, -4
 
-KERNEL_GEMV, KERNEL_GEMM = 1, 2
+KERNEL_GEMV, KERNEL_GEMM, KERNEL_SKINNY = 1, 2, 3  # pk_w4a16_plan kernel ids
 
 
 class PicoKernelsError(RuntimeError):

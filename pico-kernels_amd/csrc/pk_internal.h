@@ -21,6 +21,21 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
                 int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only = false);
 
+// W4A16 for kSkinnyMinM <= M <= kSkinnyMaxM (w4a16_skinny.hip): weights to registers, MFMA
+// per 16 activation rows, 4-wave LDS reduction, split-K partials.
+constexpr int kSkinnyMinM = 5;
+constexpr int kSkinnyMaxM = 32;
+struct SkinnyPlan {
+  int mb;  // 16-row activation blocks (1 or 2)
+  int split, k_slice, tiles;
+};
+bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out);
+bool skinny_fits(int M, int N, int K, int64_t lda, int64_t ldq, int group, bool has_gs);
+int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
+                  int64_t ldq, const void* scales, int group, float tensor_scale, void* c,
+                  int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
+                  bool partials_only = false);
+
 struct GemmCfg {
   int bm, bn, wm, wn;
 };

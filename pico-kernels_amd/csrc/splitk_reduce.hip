@@ -31,7 +31,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i] * scale);
 }
 
-// Generic slice count: the same fixed order, loads in batches of 8.
+// Generic slice count: the same fixed order. Loads go out in batches of 32 that are all in
+// flight together, so S slices cost ceil(S / 32) memory round trips, not S.
+constexpr int kReduceBatch = 32;
 __global__ __launch_bounds__(256) void splitk_reduce_any_kernel(const float* __restrict__ partials,
                                                                 int S, int M, int N, float scale,
                                                                 void* __restrict__ c, int c_dtype,
@@ -40,8 +42,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_any_kernel(const float* __r
   const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (q >= plane4) return;
   const pk_f4* src = reinterpret_cast<const pk_f4*>(partials) + q;
-  pk_f4 v = __builtin_nontemporal_load(src);
-  for (int s = 1; s < S; ++s) v += __builtin_nontemporal_load(src + s * plane4);
+  pk_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < S; s0 += kReduceBatch) {
+    pk_f4 part[kReduceBatch];
+#pragma unroll
+    for (int i = 0; i < kReduceBatch; ++i)
+      if (s0 + i < S) part[i] = __builtin_nontemporal_load(src + (s0 + i) * plane4);
+    // slice 0 starts the sum (so -0.0 partials stay -0.0, as in the fixed-S kernel)
+    if (s0 == 0) v = part[0];
+#pragma unroll
+    for (int i = 0; i < kReduceBatch; ++i)
+      if (s0 + i < S && s0 + i > 0) v += part[i];
+  }
   const int64_t e = q * 4;
   const int64_t m = e / N, n = e - m * N;
   const int64_t o = m * ldc + n;

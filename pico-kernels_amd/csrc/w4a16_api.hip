@@ -1,15 +1,16 @@
 // C ABI for the W4A16 matmul (gemm_int4.int4_gemm + the group-128 / split-K path) and the
 // dense fp16 split-K matmul (gemm_splitk.triton_gemm_splitk).
 //
-// Dispatch: M <= 4 runs the skinny HBM-bound GEMV (register dequant, v_dot2); larger M runs
-// the MFMA GEMM that dequantises B into LDS. Both honour an explicit split_k.
+// Dispatch: M <= 4 runs the HBM-bound GEMV (w4a16_gemv.hip); 5 <= M <= 32 the register-
+// dequant MFMA kernel (w4a16_skinny.hip); larger M the MFMA GEMM that dequantises B into LDS.
+// All honour an explicit split_k.
 #include "pk_internal.h"
 
 using namespace pk;
 
 namespace {
 
-enum { kKernelGemv = 1, kKernelGemm = 2 };
+enum { kKernelGemv = 1, kKernelGemm = 2, kKernelSkinny = 3 };
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -40,11 +41,19 @@ struct W4Plan {
   int kernel;
   GemvPlan gemv;
   GemmPlan gemm;
+  SkinnyPlan skinny;
 };
 
 bool make_plan(int M, int N, int K, int group_size, bool has_gs, int split_k, W4Plan* pl) {
   if (M <= 4 && gemv_plan(M, N, K, group_size, has_gs, split_k, &pl->gemv)) {
     pl->kernel = kKernelGemv;
+    return true;
+  }
+  // The skinny kernel's split must also be one the GEMM accepts: the GEMM is its fallback
+  // when a buffer exceeds 32-bit offsets, and the workspace size is the same (split*M*N*4).
+  if (skinny_plan(M, N, K, group_size, has_gs, split_k, &pl->skinny) &&
+      gemm_plan(M, N, K, group_size, has_gs, pl->skinny.split, &pl->gemm)) {
+    pl->kernel = kKernelSkinny;
     return true;
   }
   if (gemm_plan(M, N, K, group_size, has_gs, split_k, &pl->gemm)) {
@@ -54,9 +63,30 @@ bool make_plan(int M, int N, int K, int group_size, bool has_gs, int split_k, W4
   return false;
 }
 
+int plan_split(const W4Plan& pl) {
+  return pl.kernel == kKernelGemv ? pl.gemv.split
+         : pl.kernel == kKernelSkinny ? pl.skinny.split
+                                      : pl.gemm.split;
+}
+
 size_t plan_ws(const W4Plan& pl, int M, int N) {
-  return pl.kernel == kKernelGemv ? gemv_workspace_bytes(pl.gemv, M, N)
-                                  : gemm_workspace_bytes(pl.gemm, M, N);
+  if (pl.kernel == kKernelGemv) return gemv_workspace_bytes(pl.gemv, M, N);
+  const int split = plan_split(pl);
+  return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
+}
+
+int plan_launch(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
+                const void* scales, int group, float tensor_scale, void* c, int c_dtype,
+                int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
+                bool partials_only) {
+  if (pl.kernel == kKernelGemv)
+    return gemv_launch(pl.gemv, a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype, ldc,
+                       M, N, K, workspace, s, partials_only);
+  if (pl.kernel == kKernelSkinny && skinny_fits(M, N, K, lda, ldq, group, scales != nullptr))
+    return skinny_launch(pl.skinny, a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype,
+                         ldc, M, N, K, workspace, s, partials_only);
+  return gemm_launch(pl.gemm, 1, a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype, ldc,
+                     M, N, K, workspace, s, partials_only);
 }
 
 }  // namespace
@@ -71,7 +101,7 @@ extern "C" int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, i
     return PK_EUNSUPPORTED;
   }
   if (kernel_id) *kernel_id = pl.kernel;
-  if (split_used) *split_used = pl.kernel == kKernelGemv ? pl.gemv.split : pl.gemm.split;
+  if (split_used) *split_used = plan_split(pl);
   return PK_OK;
 }
 
@@ -102,12 +132,8 @@ extern "C" int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight
     set_error("pk_w4a16_gemm: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
     return PK_EWORKSPACE;
   }
-  hipStream_t s = (hipStream_t)stream;
-  if (pl.kernel == kKernelGemv)
-    return gemv_launch(pl.gemv, a, lda, qweight, ldq, scales, group, tensor_scale, c, c_dtype,
-                       ldc, M, N, K, workspace, s);
-  return gemm_launch(pl.gemm, 1, a, lda, qweight, ldq, scales, group, tensor_scale, c, c_dtype,
-                     ldc, M, N, K, workspace, s);
+  return plan_launch(pl, a, lda, qweight, ldq, scales, group, tensor_scale, c, c_dtype, ldc, M,
+                     N, K, workspace, (hipStream_t)stream, false);
 }
 
 extern "C" size_t pk_gemm_f16_workspace_bytes(int M, int N, int K, int split_k) {
@@ -155,19 +181,15 @@ extern "C" int pk_w4a16_gemm_partials(const void* a, int64_t lda, const uint32_t
     set_error("pk_w4a16_gemm_partials: no plan for split_k=%d, K=%d", split_k, K);
     return PK_EINVAL;
   }
-  const int split = pl.kernel == kKernelGemv ? pl.gemv.split : pl.gemm.split;
+  const int split = plan_split(pl);
   PK_REQUIRE(split >= 2, "pk_w4a16_gemm_partials: the plan has no split (split=%d)", split);
   const size_t need = plan_ws(pl, M, N);
   if (partials_bytes < need) {
     set_error("pk_w4a16_gemm_partials: %zu bytes of partials needed (got %zu)", need, partials_bytes);
     return PK_EWORKSPACE;
   }
-  hipStream_t s = (hipStream_t)stream;
-  if (pl.kernel == kKernelGemv)
-    return gemv_launch(pl.gemv, a, lda, qweight, ldq, scales, group, 1.0f, nullptr, PK_F32, N, M,
-                       N, K, partials, s, true);
-  return gemm_launch(pl.gemm, 1, a, lda, qweight, ldq, scales, group, 1.0f, nullptr, PK_F32, N, M,
-                     N, K, partials, s, true);
+  return plan_launch(pl, a, lda, qweight, ldq, scales, group, 1.0f, nullptr, PK_F32, N, M, N,
+                     K, partials, (hipStream_t)stream, true);
 }
 
 extern "C" int pk_splitk_reduce(const float* partials, int split, int M, int N, float scale,

@@ -260,3 +260,20 @@ def test_partials_then_reduce_equals_fused(M, split, cuda):
         sl = slice(s * ks, (s + 1) * ks)
         ref = oracle.w4a16_ref(a.numpy()[:, sl], codes[sl], s16[s * ks // 128:(s + 1) * ks // 128], 128)
         assert oracle.rel_fro(parts[s].cpu().numpy(), ref) <= W4A16_TOL
+
+
+@pytest.mark.parametrize("S", [3, 33, 56, 70])
+def test_splitk_reduce_any_slice_count(S, cuda):
+    """Slice counts without a dedicated kernel (K = 14336 gives 56 slices of 256 rows) keep the
+    fixed order: bit-equal to a sequential fp32 sum over slices 0..S-1."""
+    M, N = 2, 1032
+    g = _gen(800 + S)
+    parts = torch.randn(S, M, N, generator=g)
+    parts[:, 0, :8] = -0.0  # all slices -0.0: the sum must stay -0.0 (it starts from slice 0)
+    acc = parts[0].numpy().copy()
+    for s in range(1, S):
+        acc = (acc + parts[s].numpy()).astype(np.float32)
+    acc = (acc * np.float32(0.5)).astype(np.float32)
+    out = torch.empty((M, N), dtype=torch.float32, device=cuda)
+    _pk.splitk_reduce(parts.to(cuda), 0.5, out)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), acc.view(np.uint32))

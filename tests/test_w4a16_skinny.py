@@ -1,0 +1,134 @@
+"""W4A16 for 5 <= M <= 32 rows (the register-dequant MFMA kernel between the GEMV and the
+LDS-tiled GEMM): parity with dequantize + fp32 matmul on CPU-seeded inputs, every path the
+kernel has (one or two 16-row activation blocks, group scales or one tensor scale, ragged
+column tiles, k-step counts per wave that are not a multiple of the prefetch depth, split-K
+partials and their ordered reduction)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import _pk
+import gemm_int4
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+W4A16_TOL = 1e-3  # max relative Frobenius error vs dequant + fp32 matmul
+
+
+def _gen(seed: int) -> torch.Generator:
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def _case(M, K, N, seed, cuda, G=128):
+    a = torch.randn(M, K, generator=_gen(seed)).half()
+    w = (torch.randn(K, N, generator=_gen(seed + 1)) * 0.02).half()
+    qw, sc = gemm_int4.quantize_int4_group(w.to(cuda), G)
+    codes, _, s16 = oracle.rtn_group_codes(w.numpy(), 4, G)
+    return a, qw, sc, codes, s16
+
+
+@pytest.mark.parametrize("M", [5, 8, 16, 17, 24, 32])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (384, 528), (1152, 784), (640, 16)])
+def test_skinny_group128(M, K, N, cuda):
+    """N = 528 / 784 / 16 leave a ragged last 256-column tile; K = 384 / 640 / 1152 give 3, 5
+    and 9 k-steps per wave (not multiples of the prefetch depth)."""
+    assert _pk.w4a16_plan(M, N, K, 128, 0)[0] == _pk.KERNEL_SKINNY
+    a, qw, sc, codes, s16 = _case(M, K, N, 10 * M + K % 97 + N % 89, cuda)
+    out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, 128, out_dtype=torch.float32)
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
+    err = oracle.rel_fro(out.cpu().numpy(), ref)
+    assert err <= W4A16_TOL, f"rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("G", [32, 64, 256])
+def test_skinny_group_sizes(G, cuda):
+    M, K, N = 12, 1024, 512
+    a, qw, sc, codes, s16 = _case(M, K, N, 40 + G, cuda, G=G)
+    out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, G, out_dtype=torch.float32)
+    assert oracle.rel_fro(out.cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, G)) <= W4A16_TOL
+
+
+@pytest.mark.parametrize("M", [8, 32])
+def test_skinny_split_k_deterministic(M, cuda):
+    """Every explicit split is bitwise reproducible, and splits agree up to fp32 reassociation."""
+    K, N = 2048, 1024
+    a, qw, sc, codes, s16 = _case(M, K, N, 60 + M, cuda)
+    ag = a.to(cuda)
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
+    base = None
+    for s in (1, 2, 4, 8, 16):
+        assert _pk.w4a16_plan(M, N, K, 128, s) == (_pk.KERNEL_SKINNY, s)
+        o1 = gemm_int4.w4a16_gemm(ag, qw, sc, 128, split_k=s, out_dtype=torch.float32)
+        o2 = gemm_int4.w4a16_gemm(ag, qw, sc, 128, split_k=s, out_dtype=torch.float32)
+        assert torch.equal(o1, o2), f"split {s} not reproducible"
+        assert oracle.rel_fro(o1.cpu().numpy(), ref) <= W4A16_TOL
+        base = o1 if base is None else base
+        assert oracle.rel_fro(o1.cpu().numpy(), base.cpu().numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("M,split", [(8, 4), (20, 8)])
+def test_skinny_partials_then_reduce(M, split, cuda):
+    """The two split-K phases reproduce the one-call result bit for bit, and a slice's partial
+    is that K range's product."""
+    K, N = 2048, 768
+    a, qw, sc, codes, s16 = _case(M, K, N, 80 + M, cuda)
+    ag = a.to(cuda)
+    parts = _pk.w4a16_gemm_partials(ag, qw, sc, 128, split)
+    assert tuple(parts.shape) == (split, M, N)
+    out = torch.empty((M, N), dtype=torch.float32, device=cuda)
+    _pk.splitk_reduce(parts, 1.0, out)
+    fused = gemm_int4.w4a16_gemm(ag, qw, sc, 128, split_k=split, out_dtype=torch.float32)
+    assert torch.equal(out, fused)
+    ks = K // split
+    s = split - 1
+    ref = oracle.w4a16_ref(a.numpy()[:, s * ks:], codes[s * ks:], s16[s * ks // 128:], 128)
+    assert oracle.rel_fro(parts[s].cpu().numpy(), ref) <= W4A16_TOL
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+def test_skinny_output_dtypes(out_dtype, cuda):
+    M, K, N = 16, 1024, 1040
+    a, qw, sc, codes, s16 = _case(M, K, N, 90, cuda)
+    out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, 128, out_dtype=out_dtype)
+    assert out.dtype == out_dtype
+    tol = {torch.float16: 2e-3, torch.bfloat16: 1e-2}[out_dtype]
+    assert oracle.rel_fro(out.float().cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, 128)) <= tol
+
+
+@pytest.mark.parametrize("M", [8, 30])
+def test_skinny_per_tensor_int4_gemm(M, cuda):
+    """The reference's int4_gemm (one tensor scale, gemm_int4.py:75-92) at skinny M: the codes
+    are exact in fp16, so only the fp32 summation order differs from the closed form."""
+    K, N = 1024, 512
+    a = torch.randn(M, K, generator=_gen(95)).half()
+    w = torch.randn(K, N, generator=_gen(96)).half()
+    w_q, scale = gemm_int4.quantize_int4(w.to(cuda))
+    c = gemm_int4.int4_gemm(a.to(cuda), gemm_int4.pack_int4_n(w_q), scale)
+    ref = oracle.int4_gemm_ref(a.numpy(), w_q.cpu().numpy(), scale)
+    assert oracle.rel_fro(c.cpu().numpy(), ref) < 1e-5
+
+
+def test_skinny_strided_activations(cuda):
+    """A row stride larger than K (a view into a wider buffer) is read in place."""
+    M, K, N = 9, 1024, 512
+    a, qw, sc, codes, s16 = _case(M, K, N, 97, cuda)
+    wide = torch.zeros(M, K + 64, dtype=torch.float16)
+    wide[:, :K] = a
+    view = wide.to(cuda)[:, :K]
+    out = gemm_int4.w4a16_gemm(view, qw, sc, 128, out_dtype=torch.float32)
+    assert oracle.rel_fro(out.cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, 128)) <= W4A16_TOL
+
+
+def test_skinny_ineligible_shapes_use_gemm(cuda):
+    """N % 16 != 0 or K % 128 != 0 stay on the LDS-tiled GEMM, still correct."""
+    for M, K, N in ((8, 1024, 520), (8, 1056, 512)):
+        assert _pk.w4a16_plan(M, N, K, 32, 0)[0] == _pk.KERNEL_GEMM
+        a, qw, sc, codes, s16 = _case(M, K, N, 98 + N, cuda, G=32)
+        out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, 32, out_dtype=torch.float32)
+        assert oracle.rel_fro(out.cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, 32)) <= W4A16_TOL
