@@ -9,9 +9,10 @@ buffers rotated (932 MB, more than twice the 256 MB Infinity Cache) so every ste
 its weights from HBM.
 
 Timing: W eager warmup steps, then exactly K steps captured in one HIP graph and replayed
-once between HIP events (bracketed by device synchronisation). The dominant kernel (the
-GEMV slice kernel) is timed the same way on its own through ``pk_w4a16_gemm_partials`` for
-the roofline fraction. The same JSON line carries the split-K sweep of the config, the
+once between HIP events (bracketed by device synchronisation). On MI355X the GEMV's split-K
+slices add up in L2 inside the one kernel, so the op is the dominant kernel and the
+roofline fraction uses its time; where a second (reduce) launch is needed, the slice kernel
+is timed on its own through ``pk_w4a16_gemm_partials``. The same JSON line carries the split-K sweep of the config, the
 W4A16 prefill GEMM (2048x4096x4096) and fp8 GEMM (4096^3) throughputs the metric also
 names, and the reference's CPU path (dequantize + matmul, numpy oracle) on a bounded sample.
 
@@ -138,18 +139,24 @@ def bench_gemv(args, dev) -> dict:
                        split_k=0, out=out)
 
     ms = GraphTimer(step, args.steps, args.warmup).run()
+    launches = _pk.w4a16_launches(M, N, K, 128, 0)
 
-    # dominant kernel alone: the slice kernel writing fp32 partials
-    parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
-
-    def step_partials(i):
-        _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
-
-    # Average launch of the slice kernel: K launches back to back in one graph, HIP events
+    # The dominant kernel's average launch: K launches back to back in one graph, HIP events
     # around the replay on the launch stream (agrees with rocprof's kernel-trace average);
     # single launches bracketed by their own events read ~1.5 us longer (event overhead).
-    ms_kernel = GraphTimer(step_partials, args.steps, args.warmup).run()
-    ms_kernel_events = per_launch_ms(step_partials, min(args.steps, 500))
+    # With the slices added in L2 the op is that one kernel; otherwise time the slice kernel
+    # alone (it writes the fp32 partials that a second launch adds).
+    if launches == 1:
+        ms_kernel = ms
+        ms_kernel_events = per_launch_ms(step, min(args.steps, 500))
+    else:
+        parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
+
+        def step_partials(i):
+            _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
+
+        ms_kernel = GraphTimer(step_partials, args.steps, args.warmup).run()
+        ms_kernel_events = per_launch_ms(step_partials, min(args.steps, 500))
 
     sweep = {}
     for s in (1, 2, 4, 8, 16):
@@ -160,7 +167,8 @@ def bench_gemv(args, dev) -> dict:
         ms_s = GraphTimer(step_s, min(args.steps, 400), 2).run()
         sweep[str(s)] = round(nbytes / (ms_s * 1e-3) / 1e9, 1)
     return {
-        "M": M, "K": K, "N": N, "split": split, "kernel_id": kid, "bytes": nbytes,
+        "M": M, "K": K, "N": N, "split": split, "kernel_id": kid, "launches": launches,
+        "bytes": nbytes,
         "ms_per_step": ms, "ms_kernel": ms_kernel, "ms_kernel_events": ms_kernel_events,
         "split_sweep_GBs": sweep,
         "inputs": (a, w),
@@ -286,9 +294,10 @@ COPY_PROBE_BYTES = 256 << 20
 
 
 def traffic_probe(dev) -> int:
-    """Short run for the rocprofv3 --pmc passes: 50 launches of the GEMV slice kernel on
-    rotating weights, then 10 device copies of COPY_PROBE_BYTES (the calibration kernel:
-    it must read and write exactly that many bytes)."""
+    """Short run for the rocprofv3 --pmc passes: 50 launches of the GEMV's dominant kernel
+    on rotating weights (the whole op when its slices add up in L2, else the slice kernel),
+    then 10 device copies of COPY_PROBE_BYTES (the calibration kernel: it must read and
+    write exactly that many bytes)."""
     import torch
 
     import _pk
@@ -297,9 +306,15 @@ def traffic_probe(dev) -> int:
     a, w, qws, scs = gemv_inputs(M, K, N, N_ROTATE, dev)
     ag = a.to(dev)
     kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
-    parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
-    for i in range(50):
-        _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
+    if _pk.w4a16_launches(M, N, K, 128, 0) == 1:
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        for i in range(50):
+            _pk.w4a16_gemm(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
+                           out=out)
+    else:
+        parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
+        for i in range(50):
+            _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
     torch.cuda.synchronize()
     src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
@@ -377,7 +392,9 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": KERNEL_NAMES.get(g["kernel_id"], "?") + " (split-K slices)",
+                     "kernel": KERNEL_NAMES.get(g["kernel_id"], "?") + (
+                         " (split-K slices added in L2: the whole op)" if g["launches"] == 1
+                         else " (split-K slices)"),
                      "kernel_us": round(g["ms_kernel"] * 1e3, 3),
                      "kernel_us_single_launch_events": round(g["ms_kernel_events"] * 1e3, 3),
                      "bytes_per_launch": g["bytes"]},

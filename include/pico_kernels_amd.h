@@ -13,8 +13,11 @@
  *    hipStream_t passed as void* (NULL = the default stream). All launches are asynchronous
  *    on `stream`; nothing here synchronises the device.
  *  - The library never allocates device memory. Entry points that need scratch space take
- *    a caller-owned `workspace` whose size is given by the matching *_workspace_bytes();
- *    its contents need no initialisation. Calls ordered on one stream may reuse a
+ *    a caller-owned `workspace` whose size is given by the matching *_workspace_bytes().
+ *    The workspace of pk_w4a16_gemm / pk_gemm_f16 starts with 64 KiB of split-K arrival
+ *    counters: zero-fill a workspace once when it is allocated; every call leaves the
+ *    counters zero again, so one workspace serves any sequence of shapes. (pk_absmax's
+ *    workspace needs no initialisation.) Calls ordered on one stream may reuse a
  *    workspace; calls that overlap in time must not share one.
  *  - Matrices are row-major with an explicit leading dimension (elements, or 32-bit words
  *    for packed int4).
@@ -126,7 +129,11 @@ int pk_cast_e4m3(const void* x, int x_dtype, int64_t n, float scale, uint8_t* ou
  * split_k: 0 = choose automatically; s >= 1 = split K into s contiguous slices of K/s rows
  * (K/s a multiple of 8 for M <= 4, of 64 otherwise) whose fp32 partial sums are reduced in a
  * fixed order (results are bitwise reproducible run to run).
- * workspace: pk_w4a16_workspace_bytes() bytes (fp32 partials of the slices).
+ * workspace: pk_w4a16_workspace_bytes() bytes, zero-filled once at allocation (split-K
+ * arrival counters, then fp32 partials of the slices). For M <= 4 on MI355X the slices of a
+ * column tile are placed on one XCD and the last to finish adds them through that XCD's L2,
+ * in the same fixed order as pk_splitk_reduce (bitwise the same result), so no second
+ * launch is needed; larger M adds them with a pk_splitk_reduce launch.
  * Replaces gemm_int4.int4_gemm (gemm_int4.py:75-92, per-tensor mode, the `c * scale`
  * epilogue fused) and provides the group-128 / split-K W4A16 path; the split-K semantics
  * (contiguous K slices of K / split_k) follow gemm_splitk.triton_gemm_splitk
@@ -142,6 +149,12 @@ int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight, int64_t l
  * kernel for 5 <= M <= 32) and the effective split. */
 int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_id,
                   int* split_used);
+
+/* Kernel launches pk_w4a16_gemm makes for this shape on the current device: 1, or 2 when
+ * split-K partials are added by a separate pk_splitk_reduce launch (negative on error).
+ * Assumes aligned operands (the GEMV's MFMA path); for benchmarks and reporting. No
+ * counterpart in the reference (its split-K is one Triton launch plus atomics). */
+int pk_w4a16_launches(int M, int N, int K, int group_size, int split_k);
 
 /* The two phases of a split-K pk_w4a16_gemm, for callers that reduce elsewhere (for example
  * across devices) or time the phases separately. pk_w4a16_gemm_partials writes the fp32

@@ -48,6 +48,7 @@ _SIGNATURES = {
                                  _vp, _i32, _vp]),
     "pk_cast_e4m3": (_i32, [_vp, _i32, _i64, _f32, _vp, _vp]),
     "pk_w4a16_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "pk_w4a16_launches": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "pk_w4a16_plan": (_i32, [_i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32),
                              ctypes.POINTER(_i32)]),
     "pk_w4a16_gemm": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
@@ -117,9 +118,10 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 # ---------------------------------------------------------------------------------------
-# Workspaces: one byte buffer per (device, stream), grown on demand and reused (it holds the
-# fp32 partials of split-K slices; nothing in it needs clearing). Calls on one stream are
-# ordered, so they never overlap on it.
+# Workspaces: one byte buffer per (device, stream), grown on demand and reused. It holds the
+# split-K arrival counters (zero-filled here once, at allocation; every call leaves them zero)
+# and the fp32 partials of split-K slices. Calls on one stream are ordered, so they never
+# overlap on it.
 # ---------------------------------------------------------------------------------------
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
@@ -131,7 +133,7 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         size = max(nbytes, 1 << 20)
-        ws = torch.empty(size, dtype=torch.uint8, device=device)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 
@@ -216,6 +218,13 @@ def w4a16_plan(M: int, N: int, K: int, group_size: int, split_k: int) -> tuple[i
     _check(lib().pk_w4a16_plan(M, N, K, group_size, split_k, ctypes.byref(kid), ctypes.byref(spl)),
            "pk_w4a16_plan")
     return kid.value, spl.value
+
+
+def w4a16_launches(M: int, N: int, K: int, group_size: int, split_k: int) -> int:
+    """Kernel launches one pk_w4a16_gemm call makes (1 when split-K slices add up in L2)."""
+    n = lib().pk_w4a16_launches(M, N, K, group_size, split_k)
+    _check(min(n, 0), "pk_w4a16_launches")
+    return n
 
 
 def _rows_ok(t: torch.Tensor) -> torch.Tensor:

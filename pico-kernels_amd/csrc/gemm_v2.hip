@@ -820,7 +820,7 @@ int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, 
   p.group = group > 0 ? group : K;
   p.scale = scale; p.c = c; p.c_dtype = c_dtype; p.ldc = ldc;
   p.M = M; p.N = N; p.K = K; p.split = split; p.k_slice = K / split;
-  p.partials = split > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
+  p.partials = split > 1 ? split_partials(workspace, partials_only) : nullptr;
   const int bn = 128;
   p.tiles_m = (int)cdiv(M, bm);
   p.tiles_n = (int)cdiv(N, bn);

@@ -185,4 +185,57 @@ __device__ __forceinline__ float clamp_nan(float x, float lo, float hi) {
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// ---------------------------------------------------------------------------------------
+// Split-K reduction inside one XCD's L2.
+//
+// MI355X dispatches the workgroups of a launch round-robin over its XCDs (XCD = linear
+// workgroup id mod the partition's XCC count, 8, 4, 2 or 1), each XCD with its own L2. A
+// 1-D grid in which workgroup b takes column tile (b % 8) + 8 * ((b / 8) / split) and slice
+// (b / 8) % split therefore keeps all slices of a tile on one XCD. There the slices hand off
+// through that L2: each writes its fp32 partials (L1 is write-through) and waits for the
+// stores to be acknowledged, then bumps the tile's arrival counter with an L2 atomic; the
+// workgroup that arrives last adds the partials in slice order 0..split-1 -- the arithmetic
+// of splitk_reduce_kernel, so the result is bitwise the same -- and resets the counter to 0
+// for the next call. Grid slots past the last tile exit at once.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ void xcd_tile_slice(int split, int& tile, int& slice) {
+  const int b = blockIdx.x, jj = b >> 3;
+  tile = (b & 7) + 8 * (jj / split);
+  slice = jj % split;
+}
+
+// True, in every thread, for the last of the `split` workgroups that share *counter.
+__device__ __forceinline__ bool splitk_arrive(unsigned* counter, int split) {
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are in L2
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const bool last = old == (unsigned)(split - 1);
+    if (last) *counter = 0u;  // every slice has arrived: ready for the next call
+    s_last = last;
+  }
+  __syncthreads();
+  return s_last != 0;
+}
+
+// sum over s = 0..split-1 of p[s * stride] in slice order, `own_v` standing in for slice
+// `own` (this workgroup's value); loads go out 16 at a time.
+__device__ __forceinline__ float splitk_sum(const float* p, int64_t stride, int split, int own,
+                                            float own_v) {
+  float acc = 0.0f;
+  for (int s0 = 0; s0 < split; s0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (s0 + i < split) v[i] = (s0 + i == own) ? own_v : p[(int64_t)(s0 + i) * stride];
+    if (s0 == 0) acc = v[0];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (s0 + i < split && s0 + i > 0) acc += v[i];
+  }
+  return acc;
+}
+
 }  // namespace pk

@@ -4,6 +4,24 @@
 
 namespace pk {
 
+// Workspace layout of pk_w4a16_gemm and pk_gemm_f16: the first kWsCounterBytes hold split-K
+// arrival counters (one 128-byte line per column tile; zero before first use, left zero by
+// every call); the fp32 partials of split-K slices follow.
+constexpr size_t kWsCounterBytes = 64 << 10;
+constexpr int kWsMaxTiles = (int)(kWsCounterBytes / 128);
+inline float* ws_partials(void* ws) {
+  return ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsCounterBytes) : nullptr;
+}
+inline unsigned* ws_counters(void* ws) { return reinterpret_cast<unsigned*>(ws); }
+// Where a launcher writes split-K partials: after the counters of a workspace, or at the start
+// of the caller's own partials buffer (the partials-only entry point).
+inline float* split_partials(void* ws, bool partials_only) {
+  return partials_only ? reinterpret_cast<float*>(ws) : ws_partials(ws);
+}
+// Host: split-K slices may hand off through one XCD's L2 on the current device (its XCC count
+// divides 8; the environment variable PK_SPLITK_IN_L2=0 turns it off).
+bool splitk_in_l2_ok();
+
 // C = scale * sum over slices of the (S, M, N) fp32 partials, in slice order.
 int splitk_reduce(const float* partials, int S, int M, int N, float scale, void* c, int c_dtype,
                   int64_t ldc, hipStream_t s);

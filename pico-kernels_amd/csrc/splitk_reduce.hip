@@ -5,7 +5,29 @@
 // (the reference's split-K uses fp32 atomics instead, gemm_splitk.py:64).
 #include "pk_internal.h"
 
+#include <atomic>
+#include <cstdlib>
+
 namespace pk {
+
+// The XCD grouping of xcd_tile_slice holds when the partition's XCC count divides 8 (SPX 8,
+// DPX 4, QPX 2, CPX 1). Queried once per device.
+bool splitk_in_l2_ok() {
+  static std::atomic<int> state[64];  // 0 unknown, 1 on, 2 off
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  int v = state[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    const char* env = std::getenv("PK_SPLITK_IN_L2");
+    int nxcc = 0;
+    const bool on = !(env && env[0] == '0') &&
+                    hipDeviceGetAttribute(&nxcc, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess &&
+                    (nxcc == 1 || nxcc == 2 || nxcc == 4 || nxcc == 8);
+    v = on ? 1 : 2;
+    state[dev].store(v, std::memory_order_relaxed);
+  }
+  return v == 1;
+}
 
 // One thread per 4 consecutive outputs; the S slice loads are unrolled so they are all in
 // flight at once (the kernel is one memory round trip, not S of them).

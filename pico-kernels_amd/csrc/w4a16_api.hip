@@ -71,8 +71,8 @@ int plan_split(const W4Plan& pl) {
 
 size_t plan_ws(const W4Plan& pl, int M, int N) {
   if (pl.kernel == kKernelGemv) return gemv_workspace_bytes(pl.gemv, M, N);
-  const int split = plan_split(pl);
-  return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
+  // the skinny kernel (or its GEMM fallback, planned with the same split) needs the same
+  return gemm_workspace_bytes(pl.gemm, M, N);
 }
 
 int plan_launch(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
@@ -103,6 +103,21 @@ extern "C" int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, i
   if (kernel_id) *kernel_id = pl.kernel;
   if (split_used) *split_used = plan_split(pl);
   return PK_OK;
+}
+
+extern "C" int pk_w4a16_launches(int M, int N, int K, int group_size, int split_k) {
+  W4Plan pl;
+  const bool has_gs = group_size > 0;
+  if (!make_plan(M, N, K, has_gs ? group_size : K, has_gs, split_k, &pl)) {
+    set_error("pk_w4a16_launches: no kernel for M=%d N=%d K=%d group=%d split_k=%d", M, N, K,
+              group_size, split_k);
+    return PK_EUNSUPPORTED;
+  }
+  const int split = plan_split(pl);
+  if (split <= 1) return 1;
+  const bool l2 = splitk_in_l2_ok() && pl.kernel == kKernelGemv && pl.gemv.mfma &&
+                  pl.gemv.tiles <= kWsMaxTiles;
+  return l2 ? 1 : 2;
 }
 
 extern "C" size_t pk_w4a16_workspace_bytes(int M, int N, int K, int group_size, int split_k) {
@@ -183,7 +198,7 @@ extern "C" int pk_w4a16_gemm_partials(const void* a, int64_t lda, const uint32_t
   }
   const int split = plan_split(pl);
   PK_REQUIRE(split >= 2, "pk_w4a16_gemm_partials: the plan has no split (split=%d)", split);
-  const size_t need = plan_ws(pl, M, N);
+  const size_t need = (size_t)split * M * N * sizeof(float);
   if (partials_bytes < need) {
     set_error("pk_w4a16_gemm_partials: %zu bytes of partials needed (got %zu)", need, partials_bytes);
     return PK_EWORKSPACE;

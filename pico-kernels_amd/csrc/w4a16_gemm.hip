@@ -316,7 +316,7 @@ bool gemm_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemmP
 
 size_t gemm_workspace_bytes(const GemmPlan& pl, int M, int N) {
   if (pl.split <= 1) return 0;
-  return (size_t)pl.split * M * N * sizeof(float);
+  return kWsCounterBytes + (size_t)pl.split * M * N * sizeof(float);
 }
 
 template <int BM, int BN, int WMW, int WNW, int BMODE>
@@ -373,7 +373,7 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
   p.k_slice = pl.k_slice;
   p.tiles_m = pl.tiles_m;
   p.tiles_n = pl.tiles_n;
-  p.partials = pl.split > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
+  p.partials = pl.split > 1 ? split_partials(workspace, partials_only) : nullptr;
   int rc = bmode == kBInt4 ? launch_mode<kBInt4>(pl, p, s) : launch_mode<kBF16Dense>(pl, p, s);
   if (rc != PK_OK || pl.split <= 1 || partials_only) return rc;
   return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);

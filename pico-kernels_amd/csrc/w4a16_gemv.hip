@@ -54,7 +54,9 @@ struct GemvParams {
   int M, N, K;
   int split, k_slice;
   int vec_ok;  // N % 32 == 0 and 16-byte aligned rows: whole-uint4 loads everywhere
-  float* partials;  // (split, M, N) fp32 when split > 1
+  float* partials;  // (split, M, N) fp32 when split > 1; (split, M, npad) in the L2 handoff
+  unsigned* counters;  // L2 handoff: arrival counter of tile t at counters[32 t]
+  int tiles, npad;     // column tiles; tiles * 256
 };
 
 __device__ __forceinline__ pk_half2 as_half2(uint32_t v) { return __builtin_bit_cast(pk_half2, v); }
@@ -271,13 +273,17 @@ __global__ __launch_bounds__(kGemvCW* RL) void w4a16_gemv_kernel(GemvParams p) {
 constexpr int kMfmaRows = 256;  // rows per workgroup = slice length
 constexpr int kMfmaSeg = 36;    // LDS floats per 32-column segment (padding spreads banks)
 
-template <int MT, bool HAS_GS>
+template <int MT, bool HAS_GS, bool L2SPLIT>
 __global__ __launch_bounds__(256, MT == 1 ? 4 : 2) void w4a16_gemv_mfma_kernel(GemvParams p) {
   constexpr int NW = 4;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int cl = lane & 7, rl = lane >> 3;
-  const int tile = blockIdx.x, slice = blockIdx.y;
+  int tile = blockIdx.x, slice = blockIdx.y;
+  if constexpr (L2SPLIT) {
+    xcd_tile_slice(p.split, tile, slice);
+    if (tile >= p.tiles) return;
+  }
   const int words_total = p.N >> 3;
   // the ragged last tile re-reads in-bounds words; those columns are never stored
   const int word0 = min(tile * kGemvTileWords + cl * 4, words_total - 4);
@@ -350,7 +356,7 @@ __global__ __launch_bounds__(256, MT == 1 ? 4 : 2) void w4a16_gemv_mfma_kernel(G
     }
   }
   __syncthreads();
-  gemv_finish<MT, 256>(p, tile, slice, t, [&](int m, int col) {
+  auto fold = [&](int m, int col) {
     const int o = (col >> 5) * kMfmaSeg + (col & 31);
     float v = 0.0f;
 #pragma unroll
@@ -360,7 +366,32 @@ __global__ __launch_bounds__(256, MT == 1 ? 4 : 2) void w4a16_gemv_mfma_kernel(G
       else v += part;
     }
     return v * ((col & 1) ? 1048576.0f : 16777216.0f);  // exact: powers of two
-  });
+  };
+  if constexpr (L2SPLIT) gemv_finish_l2<MT>(p, tile, slice, t, fold);
+  else gemv_finish<MT, 256>(p, tile, slice, t, fold);
+}
+
+// Output stage of the split-K GEMV whose slices hand off through one XCD's L2 (the grid
+// layout and protocol of xcd_tile_slice / splitk_arrive): thread t owns tile column t.
+template <int MT, typename Fold>
+__device__ __forceinline__ void gemv_finish_l2(const GemvParams& p, int tile, int slice, int t,
+                                               Fold fold) {
+  const int col = tile * kGemvTileCols + t;
+  float mine[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    mine[m] = m < p.M ? fold(m, t) : 0.0f;
+    if (m < p.M) p.partials[((int64_t)slice * p.M + m) * p.npad + col] = mine[m];
+  }
+  if (!splitk_arrive(p.counters + 32 * tile, p.split)) return;
+  if (col >= p.N) return;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    if (m >= p.M) break;
+    const float v = splitk_sum(p.partials + (int64_t)m * p.npad + col, (int64_t)p.M * p.npad,
+                               p.split, slice, mine[m]);
+    store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + col, v * p.tensor_scale);
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -418,7 +449,8 @@ bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvP
 
 size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N) {
   if (pl.split <= 1) return 0;
-  return (size_t)pl.split * M * N * sizeof(float);
+  // room for the tile-padded partials of the L2 handoff, after the counters
+  return kWsCounterBytes + (size_t)pl.split * M * pl.tiles * kGemvTileCols * sizeof(float);
 }
 
 template <int MT, int RPT, int RL>
@@ -442,10 +474,16 @@ static void launch_gemv_rl(const GemvParams& p, int rl, int tiles, hipStream_t s
 }
 
 template <int MT>
-static void launch_gemv_mfma(const GemvParams& p, int tiles, hipStream_t s) {
+static void launch_gemv_mfma(const GemvParams& p, int tiles, hipStream_t s, bool l2split) {
+  if (l2split) {
+    const unsigned blocks = 8u * (unsigned)cdiv(tiles, 8) * (unsigned)p.split;
+    if (p.scales) w4a16_gemv_mfma_kernel<MT, true, true><<<blocks, 256, 0, s>>>(p);
+    else w4a16_gemv_mfma_kernel<MT, false, true><<<blocks, 256, 0, s>>>(p);
+    return;
+  }
   dim3 grid(tiles, p.split);
-  if (p.scales) w4a16_gemv_mfma_kernel<MT, true><<<grid, 256, 0, s>>>(p);
-  else w4a16_gemv_mfma_kernel<MT, false><<<grid, 256, 0, s>>>(p);
+  if (p.scales) w4a16_gemv_mfma_kernel<MT, true, false><<<grid, 256, 0, s>>>(p);
+  else w4a16_gemv_mfma_kernel<MT, false, false><<<grid, 256, 0, s>>>(p);
 }
 
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
@@ -470,7 +508,10 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
   p.k_slice = pl.k_slice;
   p.vec_ok = ((reinterpret_cast<uintptr_t>(qw) & 15) == 0 && ldq % 4 == 0 && N % 32 == 0 &&
               (scales == nullptr || (reinterpret_cast<uintptr_t>(scales) & 15) == 0)) ? 1 : 0;
-  p.partials = pl.split > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
+  p.partials = pl.split > 1 ? split_partials(workspace, partials_only) : nullptr;
+  p.counters = nullptr;
+  p.tiles = pl.tiles;
+  p.npad = pl.tiles * kGemvTileCols;
   // buffer offsets are 32-bit: the MFMA kernel needs the weights and activations below 2 GiB
   const bool mfma = pl.mfma && pl.k_slice == kMfmaRows && K % kMfmaRows == 0 &&
                     (scales == nullptr || group % 64 == 0) && p.vec_ok &&
@@ -478,12 +519,18 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
                     lda % 8 == 0 && (int64_t)K * ldq * 4 < (1ll << 31) &&
                     (int64_t)M * lda * 2 < (1ll << 31);
   if (mfma) {
+    // Slices hand off through L2 unless the caller wants the partials themselves.
+    const bool l2split = pl.split > 1 && !partials_only && pl.tiles <= kWsMaxTiles &&
+                         splitk_in_l2_ok();
+    if (l2split) p.counters = ws_counters(workspace);
     switch (M) {
-      case 1: launch_gemv_mfma<1>(p, pl.tiles, s); break;
-      case 2: launch_gemv_mfma<2>(p, pl.tiles, s); break;
-      case 3: launch_gemv_mfma<3>(p, pl.tiles, s); break;
-      default: launch_gemv_mfma<4>(p, pl.tiles, s); break;
+      case 1: launch_gemv_mfma<1>(p, pl.tiles, s, l2split); break;
+      case 2: launch_gemv_mfma<2>(p, pl.tiles, s, l2split); break;
+      case 3: launch_gemv_mfma<3>(p, pl.tiles, s, l2split); break;
+      default: launch_gemv_mfma<4>(p, pl.tiles, s, l2split); break;
     }
+    PK_LAUNCH_CHECK("w4a16 gemv");
+    if (l2split) return PK_OK;
   } else {
     switch (M) {
       case 1: launch_gemv_rl<1>(p, pl.rl, pl.tiles, s); break;

@@ -17,16 +17,22 @@
 // weight column 16j + c of lane j, and the 16 x 16 result lands in lane L as rows 4g..4g+3 of
 // column 16j + c. No data crosses lanes.
 //
-// Dequantisation, in registers: XOR 0x88888888 turns each signed nibble v into u = v + 8; a
-// byte permute gathers one byte of rows (2d, 2d+1) into the two halves of a register;
-// OR-ing the masked nibble into 0x6400 gives the fp16 value 1024 + u (1024 + 16u for the high
-// nibble), and a packed subtract (fused multiply-add by 1/16 for the high nibble) yields v
-// exactly; times the fp16 group scale this is the B operand, rounded once to fp16 as in the
-// LDS-tiled GEMM. Accumulation is fp32 in the MFMA.
+// Dequantisation without a conversion per nibble (the arithmetic of the M <= 4 GEMV): XOR
+// 0x88888888 turns each signed nibble v into u = v + 8; a byte permute gathers one byte of rows
+// (2d, 2d+1) into the two 16-bit halves of a register, i.e. the fp16 subnormals
+// (u_lo + 16 u_hi) * 2^-24, and masking with 0x000F000F leaves u_lo * 2^-24. The MFMA keeps
+// fp16 subnormals and forms the products exactly, so per byte two MFMAs give
+//   L = sum x * u_lo * 2^-24   and   R = sum x * (u_lo + 16 u_hi) * 2^-24,
+// and with O = sum x * 8 * 2^-24 (one more MFMA per k-step against a constant operand)
+//   sum x * v_lo = (L - O) * 2^24,   sum x * v_hi = (R - L - 16 O) * 2^20.
+// A wave's rows lie in one quantisation group, so its fp32 result is scaled once per column
+// at the end (exact powers of two folded into the scale).
 //
 // Reduction: the 4 waves' tiles are added in LDS in a fixed order, ((w2 + w0) + (w3 + w1));
 // with split-K every slice writes (split, M, N) fp32 partials and splitk_reduce_kernel adds
-// them in slice order, so results are bitwise reproducible.
+// them in slice order, so results are bitwise reproducible. (Adding the slices through one
+// XCD's L2 inside this kernel, as the M <= 4 GEMV does, was measured slower here for every
+// split: the last workgroup of a tile has M * split partials per thread to gather.)
 #include "pk_internal.h"
 
 namespace pk {
@@ -55,7 +61,6 @@ template <int MB>
 struct SkStep {
   pk_u2v w[8];   // rows 8g..8g+7, words 2j', 2j'+1 of the tile
   pk_u4v x[MB];  // activations: row j of each 16-row block, k = 8g..8g+7
-  pk_u4v s[2];   // fp16 group scales of the lane's 16 columns
 };
 
 template <int MB, bool HAS_GS, int PD>
@@ -81,7 +86,13 @@ __global__ __launch_bounds__(256, 2) void w4a16_skinny_kernel(SkinnyParams p) {
   int a_voff[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) a_voff[mb] = (int)(min(mb * 16 + j, p.M - 1) * p.lda + 8 * g) * 2;
-  const int s_voff = word0 * 16;  // 8 fp16 scales per word
+  // The wave's rows lie in group kb / group: its 16 column scales, requested first.
+  pk_u4v sraw[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  if constexpr (HAS_GS) {
+    const int srow = (kb / p.group) * p.N * 2;
+    sraw[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16, srow, 0);
+    sraw[1] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16 + 16, srow, 0);
+  }
 
   auto load = [&](SkStep<MB>& b, int s) {
     const int k0 = kb + s * kSkStep;
@@ -89,27 +100,25 @@ __global__ __launch_bounds__(256, 2) void w4a16_skinny_kernel(SkinnyParams p) {
     for (int d = 0; d < 8; ++d) b.w[d] = __builtin_amdgcn_raw_buffer_load_b64(rq, q_voff, (k0 + d) * ldq4, 0);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) b.x[mb] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[mb], k0 * 2, 0);
-    if constexpr (HAS_GS) {
-      const int srow = (k0 / p.group) * p.N * 2;
-      b.s[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, s_voff, srow, 0);
-      b.s[1] = __builtin_amdgcn_raw_buffer_load_b128(rs, s_voff + 16, srow, 0);
-    }
   };
 
-  pk_f4 acc[MB][16];
+  // accL / accR: byte b (columns 16j + 2b, 16j + 2b + 1) masked low nibble / both nibbles
+  pk_f4 accL[MB][8], accR[MB][8], off[MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int mb = 0; mb < MB; ++mb) {
+    off[mb] = pk_f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int c = 0; c < 16; ++c) acc[mb][c] = pk_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < 8; ++b) accL[mb][b] = accR[mb][b] = off[mb];
+  }
+  const pk_u4v eight_u = {0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u};
+  const pk_half8 eight = __builtin_bit_cast(pk_half8, eight_u);
 
   auto compute = [&](const SkStep<MB>& b) {
     pk_half8 xa[MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) xa[mb] = __builtin_bit_cast(pk_half8, b.x[mb]);
-    pk_half8 sv[2];
-    if constexpr (HAS_GS) {
-      sv[0] = __builtin_bit_cast(pk_half8, b.s[0]);
-      sv[1] = __builtin_bit_cast(pk_half8, b.s[1]);
+    for (int mb = 0; mb < MB; ++mb) {
+      xa[mb] = __builtin_bit_cast(pk_half8, b.x[mb]);
+      off[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mb], eight, off[mb], 0, 0, 0);
     }
 #pragma unroll
     for (int wi = 0; wi < 2; ++wi) {
@@ -122,25 +131,17 @@ __global__ __launch_bounds__(256, 2) void w4a16_skinny_kernel(SkinnyParams p) {
 #pragma unroll
       for (int bb = 0; bb < 4; ++bb) {
         const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + bb) << 16) | (uint32_t)bb;
-        pk_u4v lo, hi;
+        pk_u4v raw, lo;
 #pragma unroll
         for (int dd = 0; dd < 4; ++dd) {
-          const uint32_t raw = __builtin_amdgcn_perm(wx[2 * dd + 1], wx[2 * dd], sel);
-          lo[dd] = (raw & 0x000f000fu) | 0x64006400u;
-          hi[dd] = (raw & 0x00f000f0u) | 0x64006400u;
+          raw[dd] = __builtin_amdgcn_perm(wx[2 * dd + 1], wx[2 * dd], sel);
+          lo[dd] = raw[dd] & 0x000f000fu;
         }
-        pk_half8 blo = __builtin_bit_cast(pk_half8, lo) - (pk_half)1032.0f;
-        pk_half8 bhi = __builtin_bit_cast(pk_half8, hi) * (pk_half)0.0625f - (pk_half)72.0f;
-        const int clo = 8 * wi + 2 * bb;
-        if constexpr (HAS_GS) {
-          const pk_half s_lo = sv[wi][2 * bb], s_hi = sv[wi][2 * bb + 1];
-          blo = blo * s_lo;
-          bhi = bhi * s_hi;
-        }
+        const int by = 4 * wi + bb;
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-          acc[mb][clo] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mb], blo, acc[mb][clo], 0, 0, 0);
-          acc[mb][clo + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mb], bhi, acc[mb][clo + 1], 0, 0, 0);
+          accL[mb][by] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mb], __builtin_bit_cast(pk_half8, lo), accL[mb][by], 0, 0, 0);
+          accR[mb][by] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mb], __builtin_bit_cast(pk_half8, raw), accR[mb][by], 0, 0, 0);
         }
       }
     }
@@ -162,6 +163,29 @@ __global__ __launch_bounds__(256, 2) void w4a16_skinny_kernel(SkinnyParams p) {
     }
   }
   mfma_drain();
+
+  // ---- per column: remove the +8 offset, apply 2^24 / 2^20 and the group scale ------------
+  // acc[mb][c] holds rows mb*16 + 4g + r of column 16j + c.
+  pk_f4 acc[MB][16];
+  {
+    float sc[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      float sv = 1.0f;
+      if constexpr (HAS_GS) {
+        const uint32_t word = sraw[c >> 3][(c & 7) >> 1];
+        sv = (float)__builtin_bit_cast(pk_half, (uint16_t)((c & 1) ? (word >> 16) : (word & 0xffffu)));
+      }
+      sc[c] = sv * ((c & 1) ? 1048576.0f : 16777216.0f);
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int by = 0; by < 8; ++by) {
+        acc[mb][2 * by] = (accL[mb][by] - off[mb]) * sc[2 * by];
+        acc[mb][2 * by + 1] = (accR[mb][by] - accL[mb][by] - off[mb] * 16.0f) * sc[2 * by + 1];
+      }
+  }
 
   // ---- add the 4 waves' tiles in LDS: ((w2 + w0) + (w3 + w1)) ---------------------------
   __shared__ float red[2][MB * 16][kSkTileCols + kSkPad];
@@ -209,17 +233,27 @@ __global__ __launch_bounds__(256, 2) void w4a16_skinny_kernel(SkinnyParams p) {
 // ---------------------------------------------------------------------------------------
 bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out) {
   if (M < kSkinnyMinM || M > kSkinnyMaxM || N % 16 || K % 128) return false;
-  if (has_gs && group % kSkStep) return false;
-  auto ok = [&](int s) { return s >= 1 && K % s == 0 && (K / s) % 128 == 0; };
-  int split;
+  // A wave takes k_slice / 4 rows, a multiple of the 32-row k-step lying in one group.
+  auto ok = [&](int s) {
+    if (s < 1 || K % s || (K / s) % 128) return false;
+    const int rows_w = K / s / 4;
+    return !has_gs || group % rows_w == 0;
+  };
+  int split = 0;
   if (split_req > 0) {
     if (!ok(split_req)) return false;
     split = split_req;
   } else {
-    // fp32 partials cost 8*S*M*N bytes of traffic against K*N/2 of weights: fewer slices for
-    // more rows.
-    split = M <= 16 ? 16 : 8;
-    while (split > 1 && !ok(split)) split >>= 1;
+    // fp32 partials cost 8*S*M*N bytes of traffic against K*N/2 of weights: 8 slices
+    // (measured fastest on MI355X for M = 8..32 against 16 and 32 on the Llama-3-8B shapes), or
+    // the nearest count that satisfies the group constraint (more slices first, since short
+    // slices are what long K needs).
+    const int base = 8;
+    for (int s = base; s <= K / 128 && !split; ++s)
+      if (ok(s)) split = s;
+    for (int s = min(base - 1, K / 128); s >= 1 && !split; --s)
+      if (ok(s)) split = s;
+    if (!split) return false;
   }
   *out = {M <= 16 ? 1 : 2, split, K / split, (int)cdiv(N, kSkTileCols)};
   return true;
@@ -257,7 +291,7 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
   p.K = K;
   p.split = pl.split;
   p.k_slice = pl.k_slice;
-  p.partials = pl.split > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
+  p.partials = pl.split > 1 ? split_partials(workspace, partials_only) : nullptr;
   const bool gs = scales != nullptr;
   if (pl.mb == 1) {
     if (gs) launch_skinny_t<1, true>(p, pl.tiles, s);
