@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2516.6  # dense fp16 (256 CU x 2.4 GHz x 4096 FLOP/clk)
 MFMA_F8_PEAK_TFLOPS = 5033.2   # dense fp8
 N_ROTATE = 40
-KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v2_f16_kernel", 3: "w4a16_skinny_kernel"}
+KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v3_f16_kernel", 3: "w4a16_skinny_kernel"}
 
 
 def _gen(seed: int):

@@ -1,8 +1,8 @@
 // Large-tile MFMA GEMMs for gfx950: W4A16 / dense fp16 (v_mfma_f32_32x32x16_f16) and
 // e4m3 fp8 (v_mfma_f32_32x32x64_f8f6f4).
 //
-// Design (f16: 4 waves, 2 x 2, each a 128 x 64 block; fp8 256 x 256: 8 waves, 2 x 4, each a
-// 128 x 64 block):
+// Design (f16: 4 waves, 2 x 2, each a 128 x 64 or 64 x 64 block; fp8 256 x 256: 8 waves,
+// 2 x 4, each a 128 x 64 block):
 //  * LDS tiles are rows of 128 bytes (64 fp16 or 128 fp8 values of k) in 8 chunks of 16 B;
 //    chunk c of row r is stored in slot c ^ ((r >> 1) & 7). Sixteen lanes reading 16
 //    consecutive rows at one chunk then touch 16 distinct 16-byte bank groups.
@@ -12,8 +12,8 @@
 //  * int4 B is loaded into registers, dequantised (exact codes via the 0x6400 fp16 exponent
 //    trick, times the fp16 group scale) and written k-contiguous; (K, N) fp16/fp8 B is
 //    transposed with byte permutes on the same path.
-//  * Double buffering: the loads of tile t+1 are issued before the MFMAs of tile t and
-//    consumed after them; one barrier per tile.
+//  * Pipelining: the loads of later tiles are issued before the MFMAs of tile t and
+//    consumed after them (three stages for f16, two for fp8); one barrier per tile.
 //  * Addresses: one buffer resource per operand, per-lane byte offsets computed once, the K
 //    advance folded into the scalar offset. Rows/columns past the matrix are clamped to the
 //    last valid one (never read out of bounds); their results are not stored.
@@ -72,242 +72,27 @@ struct V2Params {
 enum V2B { kV2Int4 = 0, kV2F16KN = 1 };
 
 // ---------------------------------------------------------------------------------------
-// f16 MFMA kernel (A fp16 (M, K); B int4 words or fp16 (K, N)); BK = 64.
-// ---------------------------------------------------------------------------------------
-template <int BM, int BN, int BMODE, bool GS>
-__global__ __launch_bounds__(256) void gemm_v2_f16_kernel(V2Params p) {
-  constexpr int WTM = BM / 2, WTN = BN / 2;  // wave tile
-  constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int A_DMA = BM / 32;             // 1 KB DMA instructions per wave per tile
-  static_assert(BN == 128 || BN == 64, "B loader assumes 16 or 8 word columns");
-  constexpr int BCG = BN / 8;                // 8-column groups
-  constexpr int BROWS = 256 / BCG;           // rows-per-thread groups: BK / rows per thread
-  constexpr int RPT = 64 / BROWS;            // k rows per thread (4 for BN=128, 2 for BN=64)
-
-  __shared__ __align__(16) char sA0[BM * 128];
-  __shared__ __align__(16) char sA1[BM * 128];
-  __shared__ __align__(16) char sB0[BN * 128];
-  __shared__ __align__(16) char sB1[BN * 128];
-
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm0 = (wave >> 1) * WTM, wn0 = (wave & 1) * WTN;
-  int tm, tn;
-  v2_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int k_begin = blockIdx.y * p.k_slice;
-  const int ktiles = p.k_slice / 64;
-
-  // ---- A: per-lane DMA source offsets (bytes), k advance in the scalar offset ----
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda * 2));
-  int a_off[A_DMA];
-#pragma unroll
-  for (int i = 0; i < A_DMA; ++i) {
-    const int r = (wave * A_DMA + i) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ ((r >> 1) & 7);
-    a_off[i] = (int)((int64_t)min(m0 + r, p.M - 1) * p.lda * 2) + c * 16;
-  }
-  auto issue_a = [&](int kt, char* sA) {
-    const int soff = (k_begin + kt * 64) * 2;
-#pragma unroll
-    for (int i = 0; i < A_DMA; ++i)
-      dma16(ra, sA + (wave * A_DMA + i) * 1024, a_off[i], soff);
-  };
-
-  // ---- B: RPT rows x 8 columns per thread ----
-  const int brg = t % BROWS, bcg = t / BROWS;  // row group, 8-column group
-  const int bn = min(n0 + bcg * 8, p.N - 8);   // first column (clamped)
-  __amdgpu_buffer_rsrc_t rb;
-  int b_off;
-  if (BMODE == kV2Int4) {
-    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.K * p.ldb * 4));
-    b_off = (int)(((int64_t)brg * RPT * p.ldb + (bn >> 3)) * 4);
-  } else {
-    rb = make_rsrc(p.b, (uint32_t)((int64_t)p.K * p.ldb * 2));
-    b_off = (int)(((int64_t)brg * RPT * p.ldb + bn) * 2);
-  }
-  constexpr bool has_gs = GS;
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales, has_gs ? (uint32_t)((int64_t)(p.K / p.group) * p.N * 2) : 16u);
-  uint32_t breg[RPT][4];
-  pk_u4v sreg = {0u, 0u, 0u, 0u};
-  auto load_b = [&](int kt) {
-    const int k0 = k_begin + kt * 64;
-    if (BMODE == kV2Int4) {
-      const int soff = (int)((int64_t)k0 * p.ldb * 4);
-#pragma unroll
-      for (int r = 0; r < RPT; ++r)
-        breg[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rb, b_off + (int)(r * p.ldb * 4), soff, 0);
-      if constexpr (has_gs) sreg = __builtin_amdgcn_raw_buffer_load_b128(rs, bn * 2, (k0 / p.group) * p.N * 2, 0);
-    } else {
-      const int soff = (int)((int64_t)k0 * p.ldb * 2);
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        const pk_u4v v = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off + (int)(r * p.ldb * 2), soff, 0);
-        breg[r][0] = v[0]; breg[r][1] = v[1]; breg[r][2] = v[2]; breg[r][3] = v[3];
-      }
-    }
-  };
-  // Columns 8*bcg .. 8*bcg+7 of the tile, k rows RPT*brg .. +RPT-1 -> swizzled [n][k] LDS.
-  auto store_b = [&](char* sB) {
-    uint32_t col[8][RPT / 2];  // (k, k+1) half pairs per column
-    if (BMODE == kV2Int4) {
-      uint32_t w[RPT];
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) w[r] = breg[r][0] ^ 0x88888888u;
-      const pk_half2 bias = {(pk_half)1032.0f, (pk_half)1032.0f};
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
-#pragma unroll
-        for (int r2 = 0; r2 < RPT / 2; ++r2) {
-          const uint32_t pr = __builtin_amdgcn_perm(w[2 * r2 + 1], w[2 * r2], sel);
-#pragma unroll
-          for (int hs = 0; hs < 2; ++hs) {
-            const int cidx = 2 * b + hs;
-            const uint32_t nib = hs ? (pr >> 4) : pr;
-            pk_half2 q = h2v((nib & 0x000f000fu) | 0x64006400u) - bias;  // exact codes
-            if constexpr (has_gs) {
-              const uint32_t sv = sreg[cidx >> 1];
-              const uint32_t s1 = (cidx & 1) ? (sv >> 16) : (sv & 0xffffu);
-              q = q * h2v(s1 | (s1 << 16));
-            }
-            col[cidx][r2] = u32v(q);
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-#pragma unroll
-        for (int r2 = 0; r2 < RPT / 2; ++r2)
-          col[c][r2] = __builtin_amdgcn_perm(breg[2 * r2 + 1][c >> 1], breg[2 * r2][c >> 1], sel);
-      }
-    }
-    // k offset of this thread's rows inside the 128-byte row: RPT*brg halves
-    const int kb = RPT * brg * 2;  // bytes
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int n = bcg * 8 + c;
-      char* dst = sB + swz(n, kb >> 4) + (kb & 15);
-      if (RPT == 4) {
-        pk_u2v v = {col[c][0], col[c][1]};
-        *reinterpret_cast<pk_u2v*>(dst) = v;
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = col[c][0];
-      }
-    }
-  };
-
-  // ---- MFMA operand offsets (bytes within a stage), per fragment and k16 step ----
-  int aoff[FM][4], boff[FN][4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) aoff[i][ks] = swz(wm0 + 32 * i + (lane & 31), 2 * ks + (lane >> 5));
-#pragma unroll
-    for (int j = 0; j < FN; ++j) boff[j][ks] = swz(wn0 + 32 * j + (lane & 31), 2 * ks + (lane >> 5));
-  }
-
-  pk_f16v acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = (pk_f16v){};
-
-  auto compute = [&](const char* sA, const char* sB) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      pk_half8 af[FM], bf[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const pk_half8*>(sA + aoff[i][ks]);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const pk_half8*>(sB + boff[j][ks]);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
-    }
-  };
-
-  // ---- pipeline: tiles in pairs (stage 0, stage 1); an odd last tile sits in stage 0 ----
-  issue_a(0, sA0);
-  load_b(0);
-  store_b(sB0);
-  __syncthreads();
-  int kt = 0;
-  // The scheduling barriers keep the next tile's loads at the top of each step: left to
-  // itself the compiler sinks them next to their first use, which leaves no time to hide
-  // their latency. B goes first so its dequantisation does not wait for the A DMA.
-  for (; kt + 1 < ktiles; kt += 2) {
-    load_b(kt + 1);
-    issue_a(kt + 1, sA1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(sA0, sB0);
-    __builtin_amdgcn_sched_barrier(0);
-    store_b(sB1);
-    __syncthreads();
-    const int n2 = min(kt + 2, ktiles - 1);  // the last pair re-reads a valid tile, unused
-    load_b(n2);
-    issue_a(n2, sA0);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(sA1, sB1);
-    __builtin_amdgcn_sched_barrier(0);
-    store_b(sB0);
-    __syncthreads();
-  }
-  if (kt < ktiles) compute(sA0, sB0);
-  mfma_drain();
-
-  // ---- epilogue. The MFMAs take B as the first operand, so fragment (i, j) holds C^T:
-  // register r of a lane is C[m][n] with m = 32i + lane%32 and n = 32j + 8(r/4) + 4(lane/32)
-  // + r%4, i.e. four consecutive columns per register quad -> one 8- or 16-byte store. ----
-  float* part = p.split > 1 ? p.partials + (int64_t)blockIdx.y * p.M * p.N : nullptr;
-  const int esz = part ? 4 : (p.c_dtype == PK_F32 ? 4 : 2);
-  const bool vec = part ? true
-                        : (p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & (4 * esz - 1)) == 0);
-  const int em = lane & 31, en = 4 * (lane >> 5);
-  auto epilogue = [&](auto DT) {
-    constexpr int dt = decltype(DT)::value;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int gm = m0 + wm0 + 32 * i + em;
-          const int gn = n0 + wn0 + 32 * j + 8 * q + en;  // N % 4 == 0: all four in or out
-          if (gm < p.M && gn < p.N) {
-            pk_f4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-            if (part) {
-              store4_as<PK_F32>(part, (int64_t)gm * p.N + gn, v, true);
-            } else {
-              v *= p.scale;
-              store4_as<dt>(p.c, (int64_t)gm * p.ldc + gn, v, vec);
-            }
-          }
-        }
-  };
-  with_dtype(part ? PK_F32 : p.c_dtype, epilogue);
-}
-
-// ---------------------------------------------------------------------------------------
-// 3-stage f16 MFMA kernel, 256 x 128 tiles (A fp16 (M, K); B int4 words or fp16 (K, N)).
+// 3-stage f16 MFMA kernel, BM x 128 tiles (A fp16 (M, K); B int4 words or fp16 (K, N));
+// BK = 64, 4 waves (2 x 2).
 //
-// Same tile, wave layout, swizzle, B dequantisation and epilogue as gemm_v2_f16_kernel, with
-// a deeper pipeline: three LDS stages of 48 KB, the A DMA of tile t+2 and the B words of
-// tile t+2 issued after the barrier of tile t, and the B words of tile t+1 dequantised into
-// their stage while tile t is multiplied. Per tile one bare s_barrier: __syncthreads() would
+// Swapped MFMA operands (B first) make each accumulator C^T, so a lane holds four consecutive
+// output columns per register quad (8- or 16-byte stores). Three LDS stages: the A DMA of
+// tile t+2 and the B words of tile t+2 issued after the barrier of tile t, and the B words of
+// tile t+1 dequantised into their stage while tile t is multiplied. Per tile one bare
+// s_barrier: __syncthreads() would
 // add a release fence that waits for every outstanding LDS DMA and undo the prefetch; the
 // explicit wait before the barrier (this wave's DMA of tile t and its ds_writes of tile t's
 // B) publishes exactly what the next step reads.
 // ---------------------------------------------------------------------------------------
-template <int BMODE, bool GS>
+// BM = 256 (128 x 64 per wave) serves large M; BM = 128 (64 x 64 per wave) serves M <= 128,
+// where 256-row tiles would leave half the MFMA work on padding rows.
+template <int BMODE, bool GS, int BM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_v3_f16_kernel(V2Params p) {
-  constexpr int BM = 256, BN = 128;
-  constexpr int WTM = 128, WTN = 64, FM = 4, FN = 2;
+  constexpr int BN = 128;
+  constexpr int WTM = BM / 2, WTN = 64, FM = WTM / 32, FN = 2;
   constexpr int A_DMA = BM / 32;  // 1 KB DMA instructions per wave per tile
+  constexpr int A_PART = A_DMA / 4;  // of them per k-step
   constexpr int BCG = BN / 8, BROWS = 256 / BCG, RPT = 64 / BROWS;  // 16, 16, 4
   constexpr bool has_gs = GS;
 
@@ -447,10 +232,11 @@ void gemm_v3_f16_kernel(V2Params p) {
   // scheduling barriers: a wave issues in order, and with one wave per SIMD its VALU work
   // only overlaps the matrix pipe when it sits between MFMAs. Fragment reads run one k-step
   // ahead of the MFMAs that use them.
-  auto issue_a_part = [&](int kt, char* sA, int part) {  // DMAs 2*part, 2*part+1 of a tile
+  auto issue_a_part = [&](int kt, char* sA, int part) {  // a quarter of a tile's DMAs
     const int soff = (k_begin + kt * 64) * 2;
 #pragma unroll
-    for (int i = 2 * part; i < 2 * part + 2; ++i) dma16(ra, sA + (wave * A_DMA + i) * 1024, a_off[i], soff);
+    for (int i = A_PART * part; i < A_PART * (part + 1); ++i)
+      dma16(ra, sA + (wave * A_DMA + i) * 1024, a_off[i], soff);
   };
   auto compute_store = [&](const char* sA, const char* sB, auto SLOT, char* sBn, int kta, char* sAn,
                            auto LSLOT) {
@@ -512,11 +298,15 @@ void gemm_v3_f16_kernel(V2Params p) {
         __builtin_amdgcn_sched_barrier(0);
         dq(ks, 1);
         __builtin_amdgcn_sched_barrier(0);
-        mfma2(ks, 2);
-        __builtin_amdgcn_sched_barrier(0);
-        put(ks);
-        __builtin_amdgcn_sched_barrier(0);
-        mfma2(ks, 3);
+        if constexpr (FM == 4) {
+          mfma2(ks, 2);
+          __builtin_amdgcn_sched_barrier(0);
+          put(ks);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma2(ks, 3);
+        } else {
+          put(ks);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -828,15 +618,15 @@ int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, 
   const bool gs = scales != nullptr;
   if (bmode == kV2Int4) {
     if (bm == 256) {
-      if (gs) gemm_v3_f16_kernel<kV2Int4, true><<<grid, 256, 0, s>>>(p);
-      else gemm_v3_f16_kernel<kV2Int4, false><<<grid, 256, 0, s>>>(p);
+      if (gs) gemm_v3_f16_kernel<kV2Int4, true, 256><<<grid, 256, 0, s>>>(p);
+      else gemm_v3_f16_kernel<kV2Int4, false, 256><<<grid, 256, 0, s>>>(p);
     } else {
-      if (gs) gemm_v2_f16_kernel<128, 128, kV2Int4, true><<<grid, 256, 0, s>>>(p);
-      else gemm_v2_f16_kernel<128, 128, kV2Int4, false><<<grid, 256, 0, s>>>(p);
+      if (gs) gemm_v3_f16_kernel<kV2Int4, true, 128><<<grid, 256, 0, s>>>(p);
+      else gemm_v3_f16_kernel<kV2Int4, false, 128><<<grid, 256, 0, s>>>(p);
     }
   } else {
-    if (bm == 256) gemm_v3_f16_kernel<kV2F16KN, false><<<grid, 256, 0, s>>>(p);
-    else gemm_v2_f16_kernel<128, 128, kV2F16KN, false><<<grid, 256, 0, s>>>(p);
+    if (bm == 256) gemm_v3_f16_kernel<kV2F16KN, false, 256><<<grid, 256, 0, s>>>(p);
+    else gemm_v3_f16_kernel<kV2F16KN, false, 128><<<grid, 256, 0, s>>>(p);
   }
   PK_LAUNCH_CHECK("gemm v2 f16");
   if (split > 1 && !partials_only) return splitk_reduce(p.partials, split, M, N, scale, c, c_dtype, ldc, s);

@@ -280,7 +280,7 @@ static const GemmCfg kCfg256 = {256, 128, 2, 2};  // large-tile kernel: 256 x 12
 static GemmCfg pick_cfg(int M) {
   if (M <= 16) return kCfg16;
   if (M <= 32) return kCfg32;
-  if (M <= 64) return kCfg64;
+  if (M < 64) return kCfg64;
   if (M <= 128) return kCfg128;
   return kCfg256;
 }
@@ -300,6 +300,14 @@ bool gemm_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemmP
   if (split_req > 0) {
     if (!ok(split_req)) return false;
     split = split_req;
+  } else if (cfg.bm >= 128) {
+    // Large tiles run one workgroup per CU: the most slices that still fit the 256 CUs in one
+    // round (measured best on the Llama-3-8B shapes at M = 64..256), each >= 512 rows of K.
+    const int tiles = tiles_m * tiles_n;
+    for (int s = 2; s <= 16; s *= 2) {
+      if (!ok(s) || K / s < 512 || tiles * s > 256) break;
+      split = s;
+    }
   } else {
     // Enough workgroups to cover the 256 CUs, while each slice keeps >= 512 rows of K.
     const int tiles = tiles_m * tiles_n;
