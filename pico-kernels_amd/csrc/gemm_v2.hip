@@ -84,16 +84,18 @@ enum V2B { kV2Int4 = 0, kV2F16KN = 1 };
 // explicit wait before the barrier (this wave's DMA of tile t and its ds_writes of tile t's
 // B) publishes exactly what the next step reads.
 // ---------------------------------------------------------------------------------------
-// BM = 256 (128 x 64 per wave) serves large M; BM = 128 (64 x 64 per wave) serves M <= 128,
-// where 256-row tiles would leave half the MFMA work on padding rows.
-template <int BMODE, bool GS, int BM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// NWM x NWN waves, two per SIMD (measured on MI355X: one wave per SIMD reads LDS at ~96 B/clk
+// per CU, two at ~170): BM = 256 as 4 x 2 waves of 64 x 64; BM = 128 as 2 x 4 waves of 64 x 32
+// for M <= 128, where 256-row tiles would leave half the MFMA work on padding rows.
+template <int BMODE, bool GS, int BM, int NWM, int NWN>
+__global__ __launch_bounds__(64 * NWM * NWN)
+__attribute__((amdgpu_waves_per_eu(NWM * NWN / 4, NWM * NWN / 4)))
 void gemm_v3_f16_kernel(V2Params p) {
-  constexpr int BN = 128;
-  constexpr int WTM = BM / 2, WTN = 64, FM = WTM / 32, FN = 2;
-  constexpr int A_DMA = BM / 32;  // 1 KB DMA instructions per wave per tile
-  constexpr int A_PART = A_DMA / 4;  // of them per k-step
-  constexpr int BCG = BN / 8, BROWS = 256 / BCG, RPT = 64 / BROWS;  // 16, 16, 4
+  constexpr int BN = 128, NT = 64 * NWM * NWN;
+  constexpr int WTM = BM / NWM, WTN = BN / NWN, FM = WTM / 32, FN = WTN / 32;
+  constexpr int A_DMA = BM / (8 * NWM * NWN);  // 1 KB DMA instructions per wave per tile
+  constexpr int BCG = BN / 8, BROWS = NT / BCG, RPT = 64 / BROWS;  // 16 column groups; 4 or 2 rows
+  static_assert(FM >= 2 && FN >= 1 && A_DMA >= 1 && (RPT == 4 || RPT == 2), "tile shape");
   constexpr bool has_gs = GS;
 
   __shared__ __align__(16) char sA0[BM * 128];
@@ -104,7 +106,7 @@ void gemm_v3_f16_kernel(V2Params p) {
   __shared__ __align__(16) char sB2[BN * 128];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm0 = (wave >> 1) * WTM, wn0 = (wave & 1) * WTN;
+  const int wm0 = (wave / NWN) * WTM, wn0 = (wave % NWN) * WTN;
   int tm, tn;
   v2_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -209,8 +211,12 @@ void gemm_v3_f16_kernel(V2Params p) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int n = bcg * 8 + c;
-      pk_u2v v = {col[c][0], col[c][1]};
-      *reinterpret_cast<pk_u2v*>(sB + swz(n, kb >> 4) + (kb & 15)) = v;
+      if constexpr (RPT == 4) {
+        pk_u2v v = {col[c][0], col[c][1]};
+        *reinterpret_cast<pk_u2v*>(sB + swz(n, kb >> 4) + (kb & 15)) = v;
+      } else {
+        *reinterpret_cast<uint32_t*>(sB + swz(n, kb >> 4) + (kb & 15)) = col[c][0];
+      }
     }
   };
 
@@ -229,14 +235,14 @@ void gemm_v3_f16_kernel(V2Params p) {
     for (int j = 0; j < FN; ++j) acc[i][j] = (pk_f16v){};
   // int4 B: the dequantisation of tile t+1 is written out in four pieces (one byte position
   // = two columns each) and woven between the MFMAs of tile t in source order, fenced by
-  // scheduling barriers: a wave issues in order, and with one wave per SIMD its VALU work
-  // only overlaps the matrix pipe when it sits between MFMAs. Fragment reads run one k-step
-  // ahead of the MFMAs that use them.
-  auto issue_a_part = [&](int kt, char* sA, int part) {  // a quarter of a tile's DMAs
+  // scheduling barriers: a wave issues in order, so its VALU work overlaps its own matrix-pipe
+  // work only when it sits between MFMAs. Fragment reads run one k-step ahead of the MFMAs
+  // that use them.
+  auto issue_a_part = [&](int kt, char* sA, int part) {  // the tile's DMAs spread over 4 k-steps
     const int soff = (k_begin + kt * 64) * 2;
 #pragma unroll
-    for (int i = A_PART * part; i < A_PART * (part + 1); ++i)
-      dma16(ra, sA + (wave * A_DMA + i) * 1024, a_off[i], soff);
+    for (int i = 0; i < A_DMA; ++i)
+      if (i * 4 / A_DMA == part) dma16(ra, sA + (wave * A_DMA + i) * 1024, a_off[i], soff);
   };
   auto compute_store = [&](const char* sA, const char* sB, auto SLOT, char* sBn, int kta, char* sAn,
                            auto LSLOT) {
@@ -276,8 +282,12 @@ void gemm_v3_f16_kernel(V2Params p) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int n = bcg * 8 + 2 * b + h;
-          pk_u2v v = {col[h][0], col[h][1]};
-          *reinterpret_cast<pk_u2v*>(sBn + swz(n, kb >> 4) + (kb & 15)) = v;
+          if constexpr (RPT == 4) {
+            pk_u2v v = {col[h][0], col[h][1]};
+            *reinterpret_cast<pk_u2v*>(sBn + swz(n, kb >> 4) + (kb & 15)) = v;
+          } else {
+            *reinterpret_cast<uint32_t*>(sBn + swz(n, kb >> 4) + (kb & 15)) = col[h][0];
+          }
         }
       };
       read(0, 0);
@@ -290,13 +300,13 @@ void gemm_v3_f16_kernel(V2Params p) {
         mfma2(ks, 0);
         __builtin_amdgcn_sched_barrier(0);
         issue_a_part(kta, sAn, ks);  // the next-but-one tile's A and B, spread over the k-steps
-        load_b_row(kta, LSLOT, ks);
+        if (ks < RPT) load_b_row(kta, LSLOT, ks);
         __builtin_amdgcn_sched_barrier(0);
         dq(ks, 0);
         __builtin_amdgcn_sched_barrier(0);
         mfma2(ks, 1);
         __builtin_amdgcn_sched_barrier(0);
-        dq(ks, 1);
+        if constexpr (RPT == 4) dq(ks, 1);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (FM == 4) {
           mfma2(ks, 2);
@@ -327,7 +337,7 @@ void gemm_v3_f16_kernel(V2Params p) {
 
   // Per step this wave issues 5 (int4: 4 words + scales) or 4 (fp16) B loads, then 8 DMAs.
   // s_waitcnt vmcnt(V) expcnt(7) lgkmcnt(0): everything but the previous step's loads done.
-  constexpr int kStepLoads = (BMODE == kV2Int4 ? (has_gs ? 5 : 4) : 4) + A_DMA;
+  constexpr int kStepLoads = (BMODE == kV2Int4 ? RPT + (has_gs ? 1 : 0) : RPT) + A_DMA;
   constexpr int kWaitTile = (kStepLoads & 15) | (7 << 4) | ((kStepLoads >> 4) << 14);
   // prologue: tiles 0 and 1 in flight, tile 0's B in its stage
   load_b(0, pk_int_c<0>{});
@@ -616,17 +626,21 @@ int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, 
   p.tiles_n = (int)cdiv(N, bn);
   dim3 grid(p.tiles_m * p.tiles_n, split);
   const bool gs = scales != nullptr;
+  // 8 waves, two per SIMD: 256-row tiles as 4 x 2 waves of 64 x 64 (measured 7% faster on
+  // the 2048x4096x4096 prefill than 2 x 2 waves of 128 x 64), 128-row tiles as 2 x 4 waves of
+  // 64 x 32 (measured 7-14% faster on the Llama-3-8B layers at M = 64 and 128 than 2 x 2
+  // waves of 64 x 64).
   if (bmode == kV2Int4) {
     if (bm == 256) {
-      if (gs) gemm_v3_f16_kernel<kV2Int4, true, 256><<<grid, 256, 0, s>>>(p);
-      else gemm_v3_f16_kernel<kV2Int4, false, 256><<<grid, 256, 0, s>>>(p);
+      if (gs) gemm_v3_f16_kernel<kV2Int4, true, 256, 4, 2><<<grid, 512, 0, s>>>(p);
+      else gemm_v3_f16_kernel<kV2Int4, false, 256, 4, 2><<<grid, 512, 0, s>>>(p);
     } else {
-      if (gs) gemm_v3_f16_kernel<kV2Int4, true, 128><<<grid, 256, 0, s>>>(p);
-      else gemm_v3_f16_kernel<kV2Int4, false, 128><<<grid, 256, 0, s>>>(p);
+      if (gs) gemm_v3_f16_kernel<kV2Int4, true, 128, 2, 4><<<grid, 512, 0, s>>>(p);
+      else gemm_v3_f16_kernel<kV2Int4, false, 128, 2, 4><<<grid, 512, 0, s>>>(p);
     }
   } else {
-    if (bm == 256) gemm_v3_f16_kernel<kV2F16KN, false, 256><<<grid, 256, 0, s>>>(p);
-    else gemm_v3_f16_kernel<kV2F16KN, false, 128><<<grid, 256, 0, s>>>(p);
+    if (bm == 256) gemm_v3_f16_kernel<kV2F16KN, false, 256, 4, 2><<<grid, 512, 0, s>>>(p);
+    else gemm_v3_f16_kernel<kV2F16KN, false, 128, 2, 4><<<grid, 512, 0, s>>>(p);
   }
   PK_LAUNCH_CHECK("gemm v2 f16");
   if (split > 1 && !partials_only) return splitk_reduce(p.partials, split, M, N, scale, c, c_dtype, ldc, s);
