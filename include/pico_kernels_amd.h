@@ -192,7 +192,8 @@ int pk_gemm_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
  * scale applied once in the epilogue; C is fp32/fp16/bf16.
  * b_layout 0: B8 is (K, N) row-major with row stride ldb (the reference layout);
  * b_layout 1: B8 is stored transposed, (N, K) row-major with row stride ldb.
- * Requires K % 128 == 0, M, N >= 1, 16-byte aligned rows.
+ * Requires K % 16 == 0, M, N >= 1, 16-byte aligned rows (the reference's mask-free kernel
+ * needs K to be a multiple of its autotuned BLOCK_K, 32 or 64).
  * Replaces gemm_fp8.fp8_gemm_precast / fp8_gemm_kernel (gemm_fp8.py:38-86, 98-117). */
 int pk_fp8_gemm(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb, int b_layout,
                 float out_scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,

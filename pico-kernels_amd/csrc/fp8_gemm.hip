@@ -83,7 +83,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(Fp8Par
   int tm, tn;
   f8_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int ktiles = p.K / kF8BK;  // >= 1 (checked on the host)
+  // K % 16 == 0 (checked on the host): the last tile may be partial; its 16-byte k chunks
+  // past K (and, for (K, N) B, its 8-row groups past K) are zeroed like rows past M / N.
+  const int ktiles = (p.K + kF8BK - 1) / kF8BK;
 
   uint4 areg[A_PER_T];
   uint4 btreg[B_LAYOUT == 1 ? BT_PER_T : 1];
@@ -99,29 +101,29 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(Fp8Par
     for (int i = 0; i < A_PER_T; ++i) {
       const int idx = i * T + t;
       const int row = (idx >> 3) % BM, kc = idx & 7;
-      aok[i] = idx < A_ITEMS && m0 + row < p.M;
+      aok[i] = idx < A_ITEMS && m0 + row < p.M && k0 + kc * 16 < p.K;
       const int gm = min(m0 + row, p.M - 1);
-      areg[i] = *reinterpret_cast<const uint4*>(p.a + (int64_t)gm * p.lda + k0 + kc * 16);
+      areg[i] = *reinterpret_cast<const uint4*>(p.a + (int64_t)gm * p.lda + min(k0 + kc * 16, p.K - 16));
     }
     if constexpr (B_LAYOUT == 1) {
 #pragma unroll
       for (int i = 0; i < BT_PER_T; ++i) {
         const int idx = i * T + t;
         const int row = (idx >> 3) % BN, kc = idx & 7;
-        bok[i] = idx < BT_ITEMS && n0 + row < p.N;
+        bok[i] = idx < BT_ITEMS && n0 + row < p.N && k0 + kc * 16 < p.K;
         const int gn = min(n0 + row, p.N - 1);
-        btreg[i] = *reinterpret_cast<const uint4*>(p.b + (int64_t)gn * p.ldb + k0 + kc * 16);
+        btreg[i] = *reinterpret_cast<const uint4*>(p.b + (int64_t)gn * p.ldb + min(k0 + kc * 16, p.K - 16));
       }
     } else {
 #pragma unroll
       for (int i = 0; i < BN_PER_T; ++i) {
         const int idx = i * T + t;
         const int rk = idx & 15, cn = (idx >> 4) % (BN / 8);
-        bok[i] = idx < BN_ITEMS && n0 + cn * 8 < p.N;
+        bok[i] = idx < BN_ITEMS && n0 + cn * 8 < p.N && k0 + rk * 8 < p.K;
         const int gn = min(n0 + cn * 8, p.N - 8);
 #pragma unroll
         for (int r = 0; r < 8; ++r)
-          bnreg[i][r] = *reinterpret_cast<const uint2*>(p.b + (int64_t)(k0 + rk * 8 + r) * p.ldb + gn);
+          bnreg[i][r] = *reinterpret_cast<const uint2*>(p.b + (int64_t)min(k0 + rk * 8 + r, p.K - 1) * p.ldb + gn);
       }
     }
   };
@@ -252,7 +254,7 @@ extern "C" int pk_fp8_gemm(const uint8_t* a8, int64_t lda, const uint8_t* b8, in
                            int M, int N, int K, void* stream) {
   PK_REQUIRE(a8 != nullptr && b8 != nullptr && c != nullptr, "pk_fp8_gemm: null pointer");
   PK_REQUIRE(M >= 1 && N >= 1 && K >= 1, "pk_fp8_gemm: empty shape");
-  PK_REQUIRE(K % kF8BK == 0, "pk_fp8_gemm: K=%d must be a multiple of %d", K, kF8BK);
+  PK_REQUIRE(K % 16 == 0, "pk_fp8_gemm: K=%d must be a multiple of 16", K);
   PK_REQUIRE(b_layout == 0 || b_layout == 1, "pk_fp8_gemm: b_layout must be 0 or 1");
   PK_REQUIRE(c_dtype == PK_F32 || c_dtype == PK_F16 || c_dtype == PK_BF16, "pk_fp8_gemm: out dtype");
   PK_REQUIRE(lda >= K && lda % 16 == 0 && (reinterpret_cast<uintptr_t>(a8) & 15) == 0,
@@ -279,7 +281,8 @@ extern "C" int pk_fp8_gemm(const uint8_t* a8, int64_t lda, const uint8_t* b8, in
   p.K = K;
   hipStream_t s = (hipStream_t)stream;
   // Large-tile 32x32x64 kernel (buffer DMA, swizzled LDS) when its loaders fit the shape.
-  const bool v2_ok = M >= 64 && N >= 64 && N % 16 == 0 && lda % 16 == 0 && ldb % 16 == 0 &&
+  const bool v2_ok = M >= 64 && N >= 64 && K % 128 == 0 && N % 16 == 0 && lda % 16 == 0 &&
+                     ldb % 16 == 0 &&
                      (reinterpret_cast<uintptr_t>(b8) & 15) == 0 &&
                      (int64_t)M * lda < (1ll << 31) &&
                      (b_layout == 1 ? (int64_t)N * ldb : (int64_t)K * ldb) < (1ll << 31);

@@ -88,8 +88,8 @@ def test_w4a16_argument_errors(args, code):
 
 def test_fp8_argument_errors():
     lib = _pk.lib()
-    rc = lib.pk_fp8_gemm(256, 100, 256, 100, 0, 1.0, 256, _pk.PK_F32, 100, 4, 100, 100, None)
-    assert rc == _pk.PK_EINVAL and b"multiple of 128" in lib.pk_last_error()
+    rc = lib.pk_fp8_gemm(256, 104, 256, 104, 0, 1.0, 256, _pk.PK_F32, 104, 4, 104, 100, None)
+    assert rc == _pk.PK_EINVAL and b"multiple of 16" in lib.pk_last_error()
 
 
 def test_product_modules_never_import_the_oracle():

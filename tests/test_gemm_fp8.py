@@ -110,7 +110,11 @@ def _fp8_case(M, K, N, seed, cuda):
                                    # large-tile kernel: ragged M/N tiles, 2-, 6- and 10-tile K loops
                                    (600, 384, 784), (300, 128, 272), (257, 640, 528),
                                    # 128 x 128 kernel, (K, N) B, odd tile count
-                                   (100, 384, 272), (128, 384, 256)])
+                                   (100, 384, 272), (128, 384, 256),
+                                   # K not a multiple of 128: 4-stage kernel (K % 64), fallback
+                                   # kernel with a partial last k-tile (K % 16)
+                                   (512, 320, 512), (300, 64, 272), (100, 208, 264), (64, 16, 64),
+                                   (513, 1040, 520)])
 def test_fp8_gemm_matches_closed_form(M, K, N, cuda):
     a, b, a8, sa, b8, sb = _fp8_case(M, K, N, M + K + N, cuda)
     c = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb)
@@ -139,7 +143,8 @@ def test_fp8_full_size_4096(cuda):
     assert 0.02 < err_gpu < 0.06  # the ~3.7% the reference reports for N(0,1) inputs
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 512, 384), (600, 384, 784), (100, 384, 272)])
+@pytest.mark.parametrize("M,K,N", [(256, 512, 384), (600, 384, 784), (100, 384, 272),
+                                   (512, 320, 512), (100, 208, 264), (300, 64, 272)])
 def test_fp8_transposed_b_layout(M, K, N, cuda):
     a, b, a8, sa, b8, sb = _fp8_case(M, K, N, 77, cuda)
     c0 = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb)
