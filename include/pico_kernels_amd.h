@@ -177,12 +177,21 @@ int pk_splitk_reduce(const float* partials, int split, int M, int N, float scale
 /* C[M,N] (fp32/fp16) = A[M,K] (fp16) @ B[K,N] (fp16, row-major, row stride ldb), fp32
  * accumulate, K split into split_k contiguous slices reduced in fixed order.
  * Requires K % (32 * split_k) == 0 and N % 8 == 0.
- * Replaces gemm_splitk.triton_gemm_splitk (gemm_splitk.py:67-80); the reference reduces the
- * slices with fp32 atomics, this reduction is ordered and reproducible. */
+ * Replaces gemm_splitk.triton_gemm_splitk (gemm_splitk.py:67-80) and, with split_k = 1,
+ * gemm.triton_gemm (gemm.py:103-128); the reference reduces split-K slices with fp32
+ * atomics, this reduction is ordered and reproducible. */
 size_t pk_gemm_f16_workspace_bytes(int M, int N, int K, int split_k);
 int pk_gemm_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int c_dtype,
                 int64_t ldc, int M, int N, int K, int split_k, void* workspace,
                 size_t workspace_bytes, void* stream);
+
+/* pk_gemm_f16 with bf16 A and B (bf16 MFMA, fp32 accumulate); the same constraints and
+ * workspace (pk_gemm_f16_workspace_bytes). Replaces gemm.triton_gemm (gemm.py:103-128) for
+ * bf16 and gemm_splitk.triton_gemm_splitk (gemm_splitk.py:67-80) with bf16 inputs; the
+ * reference serves both dtypes from one tl.dot. */
+int pk_gemm_bf16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c, int c_dtype,
+                 int64_t ldc, int M, int N, int K, int split_k, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------- */
 /* fp8 e4m3 matmul                                                                       */

@@ -59,6 +59,8 @@ _SIGNATURES = {
     "pk_gemm_f16_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "pk_gemm_f16": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp,
                            _sz, _vp]),
+    "pk_gemm_bf16": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp,
+                           _sz, _vp]),
     "pk_fp8_gemm": (_i32, [_vp, _i64, _vp, _i64, _i32, _f32, _vp, _i32, _i64, _i32, _i32, _i32,
                            _vp]),
 }
@@ -284,17 +286,24 @@ def splitk_reduce(partials: torch.Tensor, scale: float, out: torch.Tensor) -> to
     return out
 
 
-def gemm_f16(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, split_k: int) -> torch.Tensor:
+def gemm_dense(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, split_k: int) -> torch.Tensor:
+    """C = A @ B for fp16 or bf16 A and B (same dtype), fp32 accumulate (pk_gemm_f16 /
+    pk_gemm_bf16)."""
     M, K = a.shape
     N = b.shape[1]
     a, b = _rows_ok(a), _rows_ok(b)
     out = torch.empty((M, N), dtype=out_dtype, device=a.device)
     nbytes = lib().pk_gemm_f16_workspace_bytes(M, N, K, int(split_k))
     ws = workspace(a.device, nbytes)
-    _check(lib().pk_gemm_f16(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), out.data_ptr(),
-                             pk_dtype(out_dtype), out.stride(0), M, N, K, int(split_k), ptr(ws),
-                             0 if ws is None else ws.numel(), stream_of(a)), "pk_gemm_f16")
+    name = "pk_gemm_bf16" if a.dtype == torch.bfloat16 else "pk_gemm_f16"
+    _check(getattr(lib(), name)(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
+                                out.data_ptr(), pk_dtype(out_dtype), out.stride(0), M, N, K,
+                                int(split_k), ptr(ws), 0 if ws is None else ws.numel(),
+                                stream_of(a)), name)
     return out
+
+
+gemm_f16 = gemm_dense  # the fp16 name used by earlier callers
 
 
 def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, out_scale: float, out_dtype: torch.dtype,

@@ -69,7 +69,7 @@ struct V2Params {
   float* partials;        // (split, M, N) when split > 1
 };
 
-enum V2B { kV2Int4 = 0, kV2F16KN = 1 };
+enum V2B { kV2Int4 = 0, kV2F16KN = 1, kV2BF16KN = 2 };  // B (K, N): int4 words, fp16, bf16
 
 // ---------------------------------------------------------------------------------------
 // 3-stage f16 MFMA kernel, BM x 128 tiles (A fp16 (M, K); B int4 words or fp16 (K, N));
@@ -254,10 +254,16 @@ void gemm_v3_f16_kernel(V2Params p) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) bf[bsel][j] = *reinterpret_cast<const pk_half8*>(sB + boff[j][ks]);
     };
-    auto mfma2 = [&](int ks, int i) {  // fragment row i, both fragment columns
+    auto mfma2 = [&](int ks, int i) {  // fragment row i, every fragment column
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[ks & 1][j], af[ks & 1][i], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (BMODE == kV2BF16KN)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(pk_bf16x8, bf[ks & 1][j]), __builtin_bit_cast(pk_bf16x8, af[ks & 1][i]),
+              acc[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[ks & 1][j], af[ks & 1][i], acc[i][j], 0, 0, 0);
+      }
     };
     if constexpr (BMODE == kV2Int4) {
       uint32_t w[RPT];
@@ -638,6 +644,9 @@ int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, 
       if (gs) gemm_v3_f16_kernel<kV2Int4, true, 128, 2, 4><<<grid, 512, 0, s>>>(p);
       else gemm_v3_f16_kernel<kV2Int4, false, 128, 2, 4><<<grid, 512, 0, s>>>(p);
     }
+  } else if (bmode == kV2BF16KN) {
+    if (bm == 256) gemm_v3_f16_kernel<kV2BF16KN, false, 256, 4, 2><<<grid, 512, 0, s>>>(p);
+    else gemm_v3_f16_kernel<kV2BF16KN, false, 128, 2, 4><<<grid, 512, 0, s>>>(p);
   } else {
     if (bm == 256) gemm_v3_f16_kernel<kV2F16KN, false, 256, 4, 2><<<grid, 512, 0, s>>>(p);
     else gemm_v3_f16_kernel<kV2F16KN, false, 128, 2, 4><<<grid, 512, 0, s>>>(p);

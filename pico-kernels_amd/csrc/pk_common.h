@@ -15,6 +15,7 @@ typedef _Float16 pk_half;
 typedef _Float16 pk_half2 __attribute__((ext_vector_type(2)));
 typedef _Float16 pk_half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 pk_half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 pk_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pk_f4 __attribute__((ext_vector_type(4)));
 typedef float pk_f16v __attribute__((ext_vector_type(16)));
 typedef int pk_i8v __attribute__((ext_vector_type(8)));

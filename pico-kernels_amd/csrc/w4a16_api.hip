@@ -157,29 +157,44 @@ extern "C" size_t pk_gemm_f16_workspace_bytes(int M, int N, int K, int split_k) 
   return gemm_workspace_bytes(pl, M, N);
 }
 
-extern "C" int pk_gemm_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
-                           int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
-                           void* workspace, size_t workspace_bytes, void* stream) {
-  PK_REQUIRE(a != nullptr && b != nullptr && c != nullptr, "pk_gemm_f16: null pointer");
-  PK_REQUIRE(M >= 1 && N >= 1 && K >= 1, "pk_gemm_f16: empty shape");
-  PK_REQUIRE(N % 8 == 0 && K % 32 == 0, "pk_gemm_f16: needs N %% 8 == 0 and K %% 32 == 0");
-  PK_REQUIRE(lda >= K && lda % 8 == 0 && aligned16(a), "pk_gemm_f16: A rows must be 16-byte aligned");
-  PK_REQUIRE(ldb >= N && ldb % 8 == 0 && aligned16(b), "pk_gemm_f16: B rows must be 16-byte aligned");
-  PK_REQUIRE(c_dtype == PK_F32 || c_dtype == PK_F16 || c_dtype == PK_BF16, "pk_gemm_f16: out dtype");
-  PK_REQUIRE(split_k >= 0, "pk_gemm_f16: split_k must be >= 0");
+// Dense C = A @ B for fp16 (bmode 0) or bf16 (bmode 2) operands.
+static int gemm_dense(const char* name, int bmode, const void* a, int64_t lda, const void* b,
+                      int64_t ldb, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                      int split_k, void* workspace, size_t workspace_bytes, void* stream) {
+  PK_REQUIRE(a != nullptr && b != nullptr && c != nullptr, "%s: null pointer", name);
+  PK_REQUIRE(M >= 1 && N >= 1 && K >= 1, "%s: empty shape", name);
+  PK_REQUIRE(N % 8 == 0 && K % 32 == 0, "%s: needs N %% 8 == 0 and K %% 32 == 0", name);
+  PK_REQUIRE(lda >= K && lda % 8 == 0 && aligned16(a), "%s: A rows must be 16-byte aligned", name);
+  PK_REQUIRE(ldb >= N && ldb % 8 == 0 && aligned16(b), "%s: B rows must be 16-byte aligned", name);
+  PK_REQUIRE(c_dtype == PK_F32 || c_dtype == PK_F16 || c_dtype == PK_BF16, "%s: out dtype", name);
+  PK_REQUIRE(split_k >= 0, "%s: split_k must be >= 0", name);
   GemmPlan pl;
   if (!gemm_plan(M, N, K, K, false, split_k, &pl)) {
-    set_error("pk_gemm_f16: split_k=%d must divide K=%d into slices that are multiples of 64",
+    set_error("%s: split_k=%d must divide K=%d into slices that are multiples of 64", name,
               split_k, K);
     return PK_EINVAL;
   }
   const size_t need = gemm_workspace_bytes(pl, M, N);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
-    set_error("pk_gemm_f16: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
+    set_error("%s: workspace of %zu bytes needed (got %zu)", name, need, workspace_bytes);
     return PK_EWORKSPACE;
   }
-  return gemm_launch(pl, 0, a, lda, b, ldb, nullptr, K, 1.0f, c, c_dtype, ldc, M, N, K, workspace,
-                     (hipStream_t)stream);
+  return gemm_launch(pl, bmode, a, lda, b, ldb, nullptr, K, 1.0f, c, c_dtype, ldc, M, N, K,
+                     workspace, (hipStream_t)stream);
+}
+
+extern "C" int pk_gemm_f16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                           int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  return gemm_dense("pk_gemm_f16", 0, a, lda, b, ldb, c, c_dtype, ldc, M, N, K, split_k,
+                    workspace, workspace_bytes, stream);
+}
+
+extern "C" int pk_gemm_bf16(const void* a, int64_t lda, const void* b, int64_t ldb, void* c,
+                            int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  return gemm_dense("pk_gemm_bf16", 2, a, lda, b, ldb, c, c_dtype, ldc, M, N, K, split_k,
+                    workspace, workspace_bytes, stream);
 }
 
 extern "C" int pk_w4a16_gemm_partials(const void* a, int64_t lda, const uint32_t* qweight,

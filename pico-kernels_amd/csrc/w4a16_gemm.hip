@@ -24,7 +24,7 @@ constexpr int kBK = 64;
 constexpr int kLdsPad = 8;
 constexpr int kLdsRow = kBK + kLdsPad;  // halves per LDS row
 
-enum BMode { kBF16Dense = 0, kBInt4 = 1 };
+enum BMode { kBDenseF16 = 0, kBInt4 = 1, kBDenseBF16 = 2 };  // B operand (A matches dense B)
 
 struct GemmParams {
   const pk_half* a;
@@ -233,7 +233,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmP
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          if constexpr (BMODE == kBDenseBF16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(pk_bf16x8, af[i]), __builtin_bit_cast(pk_bf16x8, bf[j]), acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
     store_tile(buf ^ 1);
     __syncthreads();
@@ -360,7 +364,7 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
   // 128/256-row tiles: the large-tile 32x32-MFMA kernel when its constraints hold.
   if (pl.cfg.bm >= 128 &&
       v2_f16_ok(M, N, K, pl.k_slice, group, scales != nullptr, lda, ldb, bmode == kBInt4))
-    return v2_f16_launch(pl.cfg.bm, bmode == kBInt4 ? 0 : 1, a, lda, b, ldb, scales, group,
+    return v2_f16_launch(pl.cfg.bm, bmode == kBInt4 ? 0 : (bmode == kBDenseBF16 ? 2 : 1), a, lda, b, ldb, scales, group,
                          tensor_scale, c, c_dtype, ldc, M, N, K, pl.split, workspace, s,
                          partials_only);
   GemmParams p;
@@ -382,7 +386,9 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
   p.tiles_m = pl.tiles_m;
   p.tiles_n = pl.tiles_n;
   p.partials = pl.split > 1 ? split_partials(workspace, partials_only) : nullptr;
-  int rc = bmode == kBInt4 ? launch_mode<kBInt4>(pl, p, s) : launch_mode<kBF16Dense>(pl, p, s);
+  int rc = bmode == kBInt4        ? launch_mode<kBInt4>(pl, p, s)
+           : bmode == kBDenseBF16 ? launch_mode<kBDenseBF16>(pl, p, s)
+                                  : launch_mode<kBDenseF16>(pl, p, s);
   if (rc != PK_OK || pl.split <= 1 || partials_only) return rc;
   return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);
 }

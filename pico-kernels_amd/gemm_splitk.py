@@ -4,10 +4,11 @@ Reference entry point kept with its signature (gemm_splitk.py:67-80):
   ``triton_gemm_splitk(a, b, split_k=4, BLOCK_M=128, BLOCK_N=128, BLOCK_K=64) -> (M, N) fp32``
 
 K is split into ``split_k`` contiguous slices of ``K // split_k`` rows (gemm_splitk.py:49-53)
-and the same divisibility contract is asserted (gemm_splitk.py:71). The reference adds the
-slices with fp32 atomics; here each slice writes an fp32 partial tile and the last workgroup
-of the tile adds them in slice order, so the output is reproducible bit for bit. The name
-keeps ``triton_`` only for drop-in compatibility: the kernel is hand-written HIP (MFMA).
+and the same divisibility contract is asserted (gemm_splitk.py:71). fp16 and bf16 inputs are
+served (the reference's ``tl.dot`` takes either). The reference adds the slices with fp32
+atomics; here each slice writes an fp32 partial tile and a second launch adds them in slice
+order, so the output is reproducible bit for bit. The name keeps ``triton_`` only for
+drop-in compatibility: the kernel is hand-written HIP (MFMA).
 """
 
 from __future__ import annotations
@@ -25,5 +26,6 @@ def triton_gemm_splitk(a: torch.Tensor, b: torch.Tensor, split_k: int = 4,
     K2, N = b.shape
     assert K == K2 and K % (split_k * BLOCK_K) == 0, "K must divide split_k * BLOCK_K"
     assert a.is_cuda and b.is_cuda, "triton_gemm_splitk: inputs must be on the GPU"
-    assert a.dtype == torch.float16 and b.dtype == torch.float16, "fp16 inputs expected"
-    return _pk.gemm_f16(a, b, torch.float32, split_k)
+    assert a.dtype == b.dtype and a.dtype in (torch.float16, torch.bfloat16), \
+        "fp16 or bf16 inputs expected"
+    return _pk.gemm_dense(a, b, torch.float32, split_k)
