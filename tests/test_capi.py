@@ -60,12 +60,45 @@ def test_w4a16_plans():
         _pk.w4a16_plan(64, 4096, 4096, 128, 128)
 
 
+def test_w4a16_plans_by_row_count():
+    """The kernel each row count gets, and its split (host planning only)."""
+    G, C = _pk.KERNEL_GEMV, _pk.KERNEL_GEMM
+    S = _pk.KERNEL_SKINNY
+    # M <= 4: the GEMV's 256-row slices (16 for K = 4096, 56 for K = 14336)
+    assert _pk.w4a16_plan(4, 4096, 4096, 128, 0) == (G, 16)
+    assert _pk.w4a16_plan(1, 4096, 14336, 128, 0) == (G, 56)
+    # 5 <= M <= 32: register-dequant kernel, 8 slices (wave rows = 128, one group); for
+    # K = 14336 the nearest count whose wave rows divide the group: 28
+    for M in (5, 8, 16, 17, 32):
+        assert _pk.w4a16_plan(M, 6144, 4096, 128, 0) == (S, 8)
+    assert _pk.w4a16_plan(8, 4096, 14336, 128, 0) == (S, 28)
+    # short K: 384 rows -> 3 slices of one 32-row k-step per wave
+    assert _pk.w4a16_plan(8, 528, 384, 128, 0) == (S, 3)
+    # explicit splits whose wave rows exceed a group go to the GEMM
+    assert _pk.w4a16_plan(8, 1024, 2048, 128, 2)[0] == C
+    # ineligible shapes (N % 16, K % 128) stay on the GEMM
+    assert _pk.w4a16_plan(8, 520, 1024, 32, 0)[0] == C
+    assert _pk.w4a16_plan(8, 512, 1056, 32, 0)[0] == C
+    # M = 33..128: LDS-tiled GEMM; large tiles take the most slices that fit 256 workgroups
+    assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (C, 4)     # 48 tiles x 4
+    assert _pk.w4a16_plan(128, 4096, 4096, 128, 0) == (C, 8)     # 32 tiles x 8
+    assert _pk.w4a16_plan(128, 14336, 4096, 128, 0) == (C, 2)    # 112 tiles x 2
+    assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (C, 8)
+    assert _pk.w4a16_plan(256, 6144, 4096, 128, 0) == (C, 4)
+    assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (C, 1)
+
+
 def test_workspace_sizes():
+    """Workspaces start with 64 KiB of split-K arrival counters, then the fp32 partials
+    (tile-padded for the GEMV's one-launch form)."""
     lib = _pk.lib()
+    counters = 64 << 10
     assert lib.pk_w4a16_workspace_bytes(2048, 4096, 4096, 128, 1) == 0
-    n = lib.pk_w4a16_workspace_bytes(1, 11008, 4096, 128, 8)
-    assert n >= 8 * 11008 * 4
-    assert lib.pk_gemm_f16_workspace_bytes(512, 512, 1024, 4) >= 4 * 512 * 512 * 4
+    assert lib.pk_w4a16_workspace_bytes(1, 11008, 4096, 128, 16) == counters + 16 * 11008 * 4
+    # N = 11000: 43 column tiles of 256, partial rows padded to 11008
+    assert lib.pk_w4a16_workspace_bytes(1, 11000, 4096, 128, 16) == counters + 16 * 11008 * 4
+    assert lib.pk_w4a16_workspace_bytes(8, 6144, 4096, 128, 0) == counters + 8 * 8 * 6144 * 4
+    assert lib.pk_gemm_f16_workspace_bytes(512, 512, 1024, 4) == counters + 4 * 512 * 512 * 4
 
 
 @pytest.mark.parametrize("args,code", [
