@@ -28,7 +28,7 @@ int splitk_reduce(const float* partials, int S, int M, int N, float scale, void*
 
 struct GemvPlan {
   int rpt, rl, split, k_slice, tiles;
-  int mfma;  // 1: MFMA kernel eligible (k_slice and group multiples of 64)
+  int mfma;  // MFMA kernel row blocks per wave (k_slice = 256 * mfma); 0: VALU kernel
 };
 bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvPlan* out);
 size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N);

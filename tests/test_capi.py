@@ -64,9 +64,11 @@ def test_w4a16_plans_by_row_count():
     """The kernel each row count gets, and its split (host planning only)."""
     G, C = _pk.KERNEL_GEMV, _pk.KERNEL_GEMM
     S = _pk.KERNEL_SKINNY
-    # M <= 4: the GEMV's 256-row slices (16 for K = 4096, 56 for K = 14336)
+    # M <= 4: the GEMV's 256-row slices (16 for K = 4096); 512-row slices (two 64-row blocks
+    # per wave) where 256 would make more than 32: 28 for K = 14336
     assert _pk.w4a16_plan(4, 4096, 4096, 128, 0) == (G, 16)
-    assert _pk.w4a16_plan(1, 4096, 14336, 128, 0) == (G, 56)
+    assert _pk.w4a16_plan(1, 4096, 14336, 128, 0) == (G, 28)
+    assert _pk.w4a16_plan(1, 4096, 14336, 128, 56) == (G, 56)
     # 5 <= M <= 32: register-dequant kernel, 8 slices (wave rows = 128, one group); for
     # K = 14336 the nearest count whose wave rows divide the group: 28
     for M in (5, 8, 16, 17, 32):

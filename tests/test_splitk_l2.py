@@ -48,9 +48,11 @@ def _counters_zero(cuda) -> bool:
 
 
 # N: 11008 = 43 tiles of 256 columns (not a multiple of 8), 4096 = 16, 512 = 2 (< 8),
-# 2016 = 8 tiles with a ragged last one; K = 14336 gives 56 slices of 256 rows.
+# 2016 = 8 tiles with a ragged last one; K = 14336 gives 28 slices of 512 rows (two row
+# blocks per wave), K = 8192 32 slices of 256 rows.
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (1, 4096, 4096), (3, 2048, 512),
-                                   (4, 4096, 2016), (1, 14336, 4096), (2, 1024, 11008)])
+                                   (4, 4096, 2016), (1, 14336, 4096), (2, 1024, 11008),
+                                   (2, 14336, 2048), (1, 8192, 4096)])
 def test_gemv_l2_handoff_matches_two_phase(M, K, N, cuda):
     a, qw, sc, codes, s16 = _case(M, K, N, 1000 + M + N % 97, cuda)
     ag = a.to(cuda)
