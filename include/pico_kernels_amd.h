@@ -208,6 +208,32 @@ int pk_fp8_gemm(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb, 
                 float out_scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
                 void* stream);
 
+/* ------------------------------------------------------------------------------------- */
+/* Split-KV decode attention                                                             */
+/* ------------------------------------------------------------------------------------- */
+
+/* Single-query attention per (batch b, head h) over N cached keys/values:
+ *   out[b,h,:] = softmax(q . K^T * sm_scale) @ V   (fp32 out, (B, H, D) contiguous),
+ * computed FlashDecoding-style: K/V split into N/split slices of `split` rows, per-slice
+ * (max, sum, acc) partials in fp32, then one combine in slice order (bitwise reproducible).
+ * q is (B, H, D) fp16 with strides sqb, sqh; k and v are (B, H, N, D) fp16 with strides
+ * (skb, skh, skn) / (svb, svh, svn) and unit stride along D (a KV-cache prefix view is read
+ * in place). D in {16, 32, 64, 128, 256}; any split with N % split == 0 (the reference's
+ * Triton kernel takes powers of two); 16-byte aligned rows.
+ * workspace: pk_flash_decode_workspace_bytes() bytes, zero-filled once before its first use
+ * (its first 64 KiB are the arrival counters, shared with pk_w4a16_gemm: every call leaves
+ * them zero again), so one workspace per stream serves both.
+ * pk_flash_decode_launches: 1 when the slices are combined inside the split kernel (B*H <=
+ * 512 on an XCD count of 1, 2, 4 or 8), else 2 (a combine kernel follows); 0 for a bad shape.
+ * Replaces flash_decoding.flash_decoding (flash_decoding.py:84-115) and its kernel
+ * flash_decoding_kernel (:48-81). */
+size_t pk_flash_decode_workspace_bytes(int B, int H, int N, int D, int split);
+int pk_flash_decode_launches(int B, int H, int N, int D, int split);
+int pk_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int64_t skb,
+                    int64_t skh, int64_t skn, const void* v, int64_t svb, int64_t svh,
+                    int64_t svn, int B, int H, int N, int D, int split, float sm_scale,
+                    float* out, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,8 @@ How each function is pinned (see the tests named in brackets):
 * GEMM references (``w4a16_ref``, ``int4_gemm_ref``, ``fp8_gemm_ref``): the reference tests'
   closed forms (tests/test_gemm_int4.py:26, tests/test_gemm_fp8.py:24), checked against
   float64 integer-exact products and brute force on small shapes.
+* ``decode_attention_ref`` (flash_decoding.eager_decode, flash_decoding.py:126-133): closed
+  forms of the softmax-weighted sum (constant V, identical keys, N = 1, a dominant score).
 """
 
 from .quant import (  # noqa: F401
@@ -44,3 +46,4 @@ from .gemm import (  # noqa: F401
     splitk_ref,
     w4a16_ref,
 )
+from .attention import decode_attention_ref  # noqa: F401

@@ -63,6 +63,10 @@ _SIGNATURES = {
                            _sz, _vp]),
     "pk_fp8_gemm": (_i32, [_vp, _i64, _vp, _i64, _i32, _f32, _vp, _i32, _i64, _i32, _i32, _i32,
                            _vp]),
+    "pk_flash_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "pk_flash_decode_launches": (_i32, [_i32, _i32, _i32, _i32, _i32]),
+    "pk_flash_decode": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+                               _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _sz, _vp]),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
@@ -322,4 +326,32 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, out_scale: float, out_dtype: to
     _check(lib().pk_fp8_gemm(a8.data_ptr(), a8.stride(0), b_buf.data_ptr(), ldb, b_layout,
                              float(out_scale), out.data_ptr(), pk_dtype(out.dtype), out.stride(0),
                              M, N, K, stream_of(a8)), "pk_fp8_gemm")
+    return out
+
+
+def flash_decode_launches(B: int, H: int, N: int, D: int, split: int) -> int:
+    """Kernel launches one pk_flash_decode call makes (1: combined in the split kernel)."""
+    return int(lib().pk_flash_decode_launches(B, H, N, D, int(split)))
+
+
+def flash_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, split: int,
+                 sm_scale: float) -> torch.Tensor:
+    """(B, H, D) fp32 single-query attention of q (B, H, D) over k, v (B, H, N, D), all fp16
+    with unit stride along D (pk_flash_decode)."""
+    B, H, N, D = k.shape
+
+    def _d_unit(t: torch.Tensor) -> torch.Tensor:
+        ok = t.stride(-1) == 1 and all(st % 8 == 0 for st in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+        return t if ok else t.contiguous()
+
+    q, k, v = _d_unit(q), _d_unit(k), _d_unit(v)
+    out = torch.empty((B, H, D), dtype=torch.float32, device=q.device)
+    nbytes = lib().pk_flash_decode_workspace_bytes(B, H, N, D, int(split))
+    ws = workspace(q.device, nbytes)  # zero-filled counters, shared with the GEMMs
+    _check(lib().pk_flash_decode(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+                                 k.stride(1), k.stride(2), v.data_ptr(), v.stride(0), v.stride(1),
+                                 v.stride(2), B, H, N, D, int(split), float(sm_scale),
+                                 out.data_ptr(), 0 if ws is None else ws.data_ptr(),
+                                 0 if ws is None else ws.numel(), stream_of(q)),
+           "pk_flash_decode")
     return out

@@ -127,6 +127,28 @@ def test_fp8_argument_errors():
     assert rc == _pk.PK_EINVAL and b"multiple of 16" in lib.pk_last_error()
 
 
+def test_flash_decode_workspace_and_errors():
+    """Split-KV decode: counters, then per-(b, h) partial regions of S records of 2 + D floats
+    rounded up to 128-byte lines; shape errors are reported before any launch."""
+    lib = _pk.lib()
+    counters = 64 << 10
+    # B=2, H=4, N=1024, D=64, split 256: S = 4 records of 66 floats = 264 -> 288 floats
+    assert lib.pk_flash_decode_workspace_bytes(2, 4, 1024, 64, 256) == counters + 8 * 288 * 4
+    assert lib.pk_flash_decode_workspace_bytes(1, 1, 512, 32, 128) == counters + 160 * 4
+    assert lib.pk_flash_decode_workspace_bytes(1, 1, 1000, 64, 256) == 0
+    assert lib.pk_flash_decode_launches(1, 1, 1000, 64, 256) == 0
+    assert lib.pk_flash_decode_launches(2, 4, 1024, 64, 256) in (1, 2)
+    assert lib.pk_flash_decode_launches(8, 128, 1024, 64, 256) == 2  # B*H > 512 counters
+    fake = 256  # aligned, never dereferenced
+    args = (fake, 64, 64, fake, 64 * 1024, 64 * 1024, 64, fake, 64 * 1024, 64 * 1024, 64)
+    rc = lib.pk_flash_decode(*args, 1, 1, 1000, 64, 256, 0.125, fake, None, 0, None)
+    assert rc == _pk.PK_EINVAL and b"multiple of split" in lib.pk_last_error()
+    rc = lib.pk_flash_decode(*args, 1, 1, 1024, 48, 256, 0.125, fake, None, 0, None)
+    assert rc == _pk.PK_EINVAL and b"D=48" in lib.pk_last_error()
+    rc = lib.pk_flash_decode(*args, 1, 1, 1024, 64, 256, 0.125, fake, None, 0, None)
+    assert rc == _pk.PK_EWORKSPACE
+
+
 def test_product_modules_never_import_the_oracle():
     for f in (ROOT / "pico-kernels_amd").glob("*.py"):
         src = f.read_text()

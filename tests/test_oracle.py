@@ -261,3 +261,33 @@ def test_planted_saturating_cast_is_caught():
     x = np.array([470.0, -470.0], dtype=np.float32)
     assert list(_torch_e4m3(x)) == [0x7F, 0xFF]
     assert list(oracle.e4m3_from_f32(x)) == [0x7F, 0xFF]
+
+
+def test_decode_attention_ref_closed_forms():
+    """Pins decode_attention_ref (flash_decoding.eager_decode, flash_decoding.py:126-133) by
+    what softmax-weighted averaging fixes, so a wrong scale placement, a missing max shift,
+    an unnormalised sum or a transposed operand fails."""
+    rng = np.random.default_rng(0)
+    B, H, N, D = 2, 3, 37, 16
+    q = rng.standard_normal((B, H, 1, D)).astype(np.float16)
+    k = rng.standard_normal((B, H, N, D)).astype(np.float16)
+    # constant V rows: the output is that row whatever the scores
+    row = rng.standard_normal((B, H, 1, D))
+    np.testing.assert_allclose(oracle.decode_attention_ref(q, k, np.repeat(row, N, axis=2)),
+                               row[:, :, 0, :], rtol=1e-12, atol=1e-12)
+    # identical keys: equal weights, the mean of the V rows
+    v = rng.standard_normal((B, H, N, D))
+    kk = np.repeat(k[:, :, :1, :], N, axis=2)
+    np.testing.assert_allclose(oracle.decode_attention_ref(q, kk, v), v.mean(axis=2), rtol=1e-12)
+    # one cached row: that value row
+    np.testing.assert_allclose(oracle.decode_attention_ref(q, k[:, :, :1], v[:, :, :1]),
+                               v[:, :, 0], rtol=1e-12)
+    # one dominant score (huge logits, no overflow thanks to the max shift): its value row
+    k2 = np.zeros((1, 1, 5, 4))
+    k2[0, 0, 3] = 1.0
+    q2 = np.full((1, 1, 1, 4), 400.0)
+    v2 = rng.standard_normal((1, 1, 5, 4))
+    np.testing.assert_allclose(oracle.decode_attention_ref(q2, k2, v2), v2[:, :, 3], rtol=1e-12)
+    # the scale multiplies the logits: scale 0 gives the plain mean of V
+    np.testing.assert_allclose(oracle.decode_attention_ref(q, k, v, sm_scale=0.0),
+                               v.mean(axis=2), rtol=1e-12)
