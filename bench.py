@@ -14,7 +14,9 @@ slices add up in L2 inside the one kernel, so the op is the dominant kernel and 
 roofline fraction uses its time; where a second (reduce) launch is needed, the slice kernel
 is timed on its own through ``pk_w4a16_gemm_partials``. The same JSON line carries the split-K sweep of the config, the
 W4A16 prefill GEMM (2048x4096x4096) and fp8 GEMM (4096^3) throughputs the metric also
-names, and the reference's CPU path (dequantize + matmul, numpy oracle) on a bounded sample.
+names, split-KV decode attention (the reference's benchmark shapes against its eager path,
+and one HBM-bound shape), and the reference's CPU path (dequantize + matmul, numpy oracle) on
+a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--sweep]
 """
@@ -255,6 +257,56 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
     return rows
 
 
+def flash_decode_bytes(B: int, H: int, N: int, D: int) -> int:
+    """Algorithmic HBM bytes of one decode-attention call: fp16 K and V once, fp16 q in,
+    fp32 out (the per-split partials stay in L2)."""
+    return 2 * B * H * N * D * 2 + B * H * D * 2 + B * H * D * 4
+
+
+def bench_flash_decode(dev, iters: int = 50) -> dict:
+    """Split-KV decode attention (flash_decoding.flash_decoding). The reference's own benchmark
+    shapes (flash_decoding.py:141-152: B=2, H=4, D=64, split 256) against its eager_decode on
+    this GPU, plus one HBM-bound shape (B=8, H=32, N=8192, D=128: 1.07 GB of K/V, more than
+    the Infinity Cache) with its roofline fraction."""
+    import math
+
+    import torch
+
+    import _pk
+    import flash_decoding
+
+    def qkv(B, H, N, D, seed):
+        q = torch.randn(B, H, 1, D, generator=_gen(seed)).half().to(dev)
+        k = torch.randn(B, H, N, D, generator=_gen(seed + 1)).half().to(dev)
+        v = torch.randn(B, H, N, D, generator=_gen(seed + 2)).half().to(dev)
+        return q, k, v
+
+    rows = []
+    for N in (1024, 2048, 4096, 8192):
+        q, k, v = qkv(2, 4, N, 64, 20)
+        ms = GraphTimer(lambda i: flash_decoding.flash_decoding(q, k, v, split_size=256), iters, 2).run(reps=3)
+        ms_eager = GraphTimer(lambda i: flash_decoding.eager_decode(q, k, v), iters, 2).run(reps=3)
+        rows.append({"B": 2, "H": 4, "N": N, "D": 64, "split": 256, "us": round(ms * 1e3, 2),
+                     "us_eager": round(ms_eager * 1e3, 2), "vs_eager": round(ms_eager / ms, 2)})
+    B, H, N, D, split = 8, 32, 8192, 128, 256
+    q, k, v = qkv(B, H, N, D, 30)
+    q3 = q[:, :, 0]
+    scale = 1.0 / math.sqrt(D)
+    ms = GraphTimer(lambda i: _pk.flash_decode(q3, k, v, split, scale), 20, 2).run(reps=3)
+    ms_eager = GraphTimer(lambda i: flash_decoding.eager_decode(q, k, v), 10, 2).run(reps=3)
+    by = flash_decode_bytes(B, H, N, D)
+    gbs = by / (ms * 1e-3) / 1e9
+    return {"workload": "split_kv_decode_attention", "B": B, "H": H, "N": N, "D": D,
+            "split": split, "launches": _pk.flash_decode_launches(B, H, N, D, split),
+            "us": round(ms * 1e3, 2), "value": round(gbs, 1), "unit": "GB/s",
+            "us_eager": round(ms_eager * 1e3, 2), "vs_eager": round(ms_eager / ms, 2),
+            "dtype": "fp16 K/V, fp32 softmax and accumulate",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "bytes_per_launch": by},
+            "reference_bench_shapes": rows}
+
+
 def cpu_baseline(a, w, seconds: float) -> dict:
     """The reference's CPU path for the same GEMV (dequantize with the group scales, then an
     fp32 matmul), run through the numpy oracle on the host cores for a bounded sample."""
@@ -400,7 +452,7 @@ def main() -> int:
                      "bytes_per_launch": g["bytes"]},
     }
     if not args.no_secondary:
-        result["secondary"] = [bench_prefill(dev), bench_fp8(dev)]
+        result["secondary"] = [bench_prefill(dev), bench_fp8(dev), bench_flash_decode(dev)]
     if args.sweep:
         result["llama3_8b_sweep"] = bench_llama_sweep(dev)
     if not args.no_cpu_baseline:

@@ -63,15 +63,35 @@ __device__ __forceinline__ float dot8(const pk_u4v a, const pk_u4v b) {
 }
 
 // Head dim d of the combined output of one (b, h) whose S partial records start at `part`.
+// Loads go out kFdBatch records at a time; the sums still run in split order.
+constexpr int kFdBatch = 16;
 __device__ __forceinline__ float fd_combine_dim(const float* part, int S, int rec, int d) {
-  float mg = part[0];
-  for (int s = 1; s < S; ++s) mg = fmaxf(mg, part[s * rec]);
+  float mg = -INFINITY;
+  for (int s0 = 0; s0 < S; s0 += kFdBatch) {
+    float pm[kFdBatch];
+#pragma unroll
+    for (int i = 0; i < kFdBatch; ++i) pm[i] = s0 + i < S ? part[(s0 + i) * rec] : -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kFdBatch; ++i) mg = fmaxf(mg, pm[i]);
+  }
   float lg = 0.0f, o = 0.0f;
-  for (int s = 0; s < S; ++s) {
-    const float* ps = part + s * rec;
-    const float alpha = __expf(ps[0] - mg);
-    lg = __builtin_fmaf(ps[1], alpha, lg);
-    o = __builtin_fmaf(ps[2 + d], alpha, o);
+  for (int s0 = 0; s0 < S; s0 += kFdBatch) {
+    float pm[kFdBatch], pl[kFdBatch], pa[kFdBatch];
+#pragma unroll
+    for (int i = 0; i < kFdBatch; ++i) {
+      const float* ps = part + (s0 + i < S ? s0 + i : 0) * rec;
+      pm[i] = ps[0];
+      pl[i] = ps[1];
+      pa[i] = ps[2 + d];
+    }
+#pragma unroll
+    for (int i = 0; i < kFdBatch; ++i) {
+      if (s0 + i < S) {
+        const float alpha = __expf(pm[i] - mg);
+        lg = __builtin_fmaf(pl[i], alpha, lg);
+        o = __builtin_fmaf(pa[i], alpha, o);
+      }
+    }
   }
   return o / lg;
 }
