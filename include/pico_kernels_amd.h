@@ -209,6 +209,23 @@ int pk_fp8_gemm(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb, 
                 void* stream);
 
 /* ------------------------------------------------------------------------------------- */
+/* GPTQ column sweep                                                                     */
+/* ------------------------------------------------------------------------------------- */
+
+/* Quantizes columns [b0, b0 + nb) of q (fp32 [out, ldq], GPTQ column order) one after another,
+ * in place: column c's value is q[:, c] minus, in column order, err[:, j] * ratio[j][c] for
+ * the block's earlier columns j (each product rounded before its subtraction), then it is
+ * RTN-quantized with `bits` (qmax = 2^(bits-1) - 1) and one scale per `group` consecutive rows
+ * (group 0: one scale per column): s = max|v|.clamp_min(1e-12) / qmax, q = clamp(rint(v/s),
+ * -qmax, qmax) * s. err (fp32 [out, lde]) receives v - q at column c - b0. ratio is fp32
+ * [in, ldr] with ratio[j][c] = Hinv[j, c] / Hinv[j, j]. Updates from columns before b0 must
+ * already be applied to q (the caller's GEMM). nb <= pk_gptq_block_cols(out, group).
+ * Replaces the inner loop of quantize.gptq_layer (quantize.py:104-110). */
+int pk_gptq_block_cols(int out, int group);
+int pk_gptq_block(float* q, int64_t ldq, const float* ratio, int64_t ldr, float* err, int64_t lde,
+                  int out, int in, int b0, int nb, int bits, int group, void* stream);
+
+/* ------------------------------------------------------------------------------------- */
 /* Split-KV decode attention                                                             */
 /* ------------------------------------------------------------------------------------- */
 

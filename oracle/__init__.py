@@ -18,7 +18,8 @@ How each function is pinned (see the tests named in brackets):
   and the golden vectors.
 * ``gptq_layer``: golden vectors (tolerance, fp32 linear algebra), the reference's own
   invariants (act-order permutation consistency, beats RTN) and the closed form that a
-  diagonal Hessian reduces it to RTN.
+  diagonal Hessian reduces it to RTN. Its column loop is ``gptq_sweep``, which the golden
+  vectors therefore pin as well.
 * GEMM references (``w4a16_ref``, ``int4_gemm_ref``, ``fp8_gemm_ref``): the reference tests'
   closed forms (tests/test_gemm_int4.py:26, tests/test_gemm_fp8.py:24), checked against
   float64 integer-exact products and brute force on small shapes.
@@ -32,6 +33,7 @@ from .quant import (  # noqa: F401
     e4m3_to_f32,
     fp8_quantize,
     gptq_layer,
+    gptq_sweep,
     pack_int4_n,
     quantize_col,
     quantize_int4,

@@ -210,6 +210,24 @@ def rtn_group_codes(w_kn: np.ndarray, bits: int = 4, group_size: int = 128):
     return _codes_to_int8(codes), scales, scales.astype(np.float16)
 
 
+def gptq_sweep(wq: np.ndarray, ratio: np.ndarray, bits: int,
+               group_size: int | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """The column loop of quantize.gptq_layer (quantize.py:104-110) in fp32: for each column j
+    in order, quantize it (quantize_col), then subtract outer(err, ratio[j, j+1:]) from every
+    later column. ratio[j, c] = H_inv[j, c] / H_inv[j, j] above the diagonal. Returns the
+    swept matrix and the per-column errors."""
+    wq = np.array(wq, dtype=np.float32)
+    errs = np.zeros_like(wq)
+    for j in range(wq.shape[1]):                                     # :104-110
+        col = wq[:, j].copy()
+        q = quantize_col(col, bits, group_size)
+        err = col - q
+        wq[:, j + 1:] -= np.outer(err, ratio[j, j + 1:]).astype(np.float32)
+        wq[:, j] = q
+        errs[:, j] = err
+    return wq, errs
+
+
 def gptq_layer(w: np.ndarray, x: np.ndarray, bits: int, damp: float = 0.01,
                act_order: bool = True, group_size: int | None = None) -> np.ndarray:
     """quantize.gptq_layer (quantize.py:71-115), sequential column sweep, fp32.
@@ -232,13 +250,10 @@ def gptq_layer(w: np.ndarray, x: np.ndarray, bits: int, damp: float = 0.01,
         order = np.argsort(-act_mag, kind="stable")
         wq = wq[:, order]
         H_inv = H_inv[order][:, order]
-    for j in range(in_dim):                                           # :102-108
-        col = wq[:, j].copy()
-        q = quantize_col(col, bits, group_size)
-        err = col - q
-        ratio = H_inv[j, j + 1:] / H_inv[j, j]
-        wq[:, j + 1:] -= np.outer(err, ratio).astype(np.float32)
-        wq[:, j] = q
+    ratio = np.zeros_like(H_inv)
+    for j in range(in_dim):
+        ratio[j, j + 1:] = H_inv[j, j + 1:] / H_inv[j, j]            # :106
+    wq, _ = gptq_sweep(wq, ratio, bits, group_size)
     if order is not None:                                             # :110-111
         wq = wq[:, np.argsort(order, kind="stable")]
     return wq.astype(w.dtype)

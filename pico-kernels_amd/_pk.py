@@ -63,6 +63,8 @@ _SIGNATURES = {
                            _sz, _vp]),
     "pk_fp8_gemm": (_i32, [_vp, _i64, _vp, _i64, _i32, _f32, _vp, _i32, _i64, _i32, _i32, _i32,
                            _vp]),
+    "pk_gptq_block_cols": (_i32, [_i32, _i32]),
+    "pk_gptq_block": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "pk_flash_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "pk_flash_decode_launches": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "pk_flash_decode": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
@@ -327,6 +329,24 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, out_scale: float, out_dtype: to
                              float(out_scale), out.data_ptr(), pk_dtype(out.dtype), out.stride(0),
                              M, N, K, stream_of(a8)), "pk_fp8_gemm")
     return out
+
+
+def gptq_block_cols(out: int, group: int) -> int:
+    """Columns the GPTQ sweep kernel takes per launch for `out` rows and scale group `group`
+    (0: one scale per column)."""
+    return int(lib().pk_gptq_block_cols(out, group))
+
+
+def gptq_block(q: torch.Tensor, ratio: torch.Tensor, err: torch.Tensor, b0: int, nb: int, bits: int,
+               group: int) -> None:
+    """Sweep columns [b0, b0 + nb) of q (fp32 [out, in], row stride q.stride(0)) in place;
+    err[:, :nb] receives the quantization errors (pk_gptq_block)."""
+    assert q.dtype == ratio.dtype == err.dtype == torch.float32
+    assert q.stride(1) == 1 and ratio.stride(1) == 1 and err.stride(1) == 1
+    out, n_in = q.shape
+    _check(lib().pk_gptq_block(q.data_ptr(), q.stride(0), ratio.data_ptr(), ratio.stride(0),
+                               err.data_ptr(), err.stride(0), out, n_in, int(b0), int(nb), int(bits),
+                               int(group), stream_of(q)), "pk_gptq_block")
 
 
 def flash_decode_launches(B: int, H: int, N: int, D: int, split: int) -> int:

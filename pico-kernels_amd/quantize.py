@@ -86,20 +86,26 @@ def gptq_layer(w: torch.Tensor, x: torch.Tensor, bits: int, damp: float = 0.01,
     # ratios[j, c] = Hinv[j, c] / Hinv[j, j] for c > j (strictly upper triangle).
     ratios = torch.triu(Hinv / torch.diagonal(Hinv).unsqueeze(1), diagonal=1)
 
-    Q = W.clone()
-    for b0 in range(0, in_dim, _GPTQ_BLOCK):
-        b1 = min(b0 + _GPTQ_BLOCK, in_dim)
-        err = torch.empty((out_dim, b1 - b0), dtype=torch.float32, device=dev)
-        for j in range(b0, b1):
-            col = Q[:, j]
-            q = quantize_col(col, bits, group_size)
-            e = col - q
-            err[:, j - b0] = e
-            Q[:, j] = q
-            if j + 1 < b1:
-                Q[:, j + 1:b1].sub_(torch.outer(e, ratios[j, j + 1:b1]))
-        if b1 < in_dim:
-            Q[:, b1:].sub_(err @ ratios[b0:b1, b1:])
+    # Lazy batching on two levels: the HIP kernel sweeps `nb` columns at a time (the error
+    # feedback inside the sweep follows the reference's column order exactly); a small GEMM
+    # carries a sweep's errors to the rest of its 128-column block, and one GEMM per block
+    # carries the block's errors to every later column.
+    Q = W.clone(memory_format=torch.contiguous_format)  # never the caller's tensor
+    ratios = ratios.contiguous()
+    g = 0 if group_size is None else int(group_size)
+    nb = min(_GPTQ_BLOCK, _pk.gptq_block_cols(out_dim, g))
+    assert nb >= 1, f"gptq_layer: a scale group of {out_dim if g == 0 else g} rows is too large"
+    err = torch.empty((out_dim, _GPTQ_BLOCK), dtype=torch.float32, device=dev)
+    for o0 in range(0, in_dim, _GPTQ_BLOCK):
+        o1 = min(o0 + _GPTQ_BLOCK, in_dim)
+        for b0 in range(o0, o1, nb):
+            b1 = min(b0 + nb, o1)
+            e = err[:, b0 - o0:b1 - o0]
+            _pk.gptq_block(Q, ratios, e, b0, b1 - b0, bits, g)
+            if b1 < o1:
+                Q[:, b1:o1].sub_(e @ ratios[b0:b1, b1:o1])
+        if o1 < in_dim:
+            Q[:, o1:].sub_(err[:, :o1 - o0] @ ratios[o0:o1, o1:])
 
     if order is not None:
         Q = Q[:, torch.argsort(order)]
