@@ -307,6 +307,31 @@ def bench_flash_decode(dev, iters: int = 50) -> dict:
             "reference_bench_shapes": rows}
 
 
+def bench_gptq(dev) -> dict:
+    """GPTQ of one 4096 x 4096 layer (quantize.gptq_layer, quantize.py:71-115) from 2048
+    calibration rows, 4-bit, groups of 128 rows: the Hessian GEMM, its inverse, the blocked
+    column sweep (pk_gptq_block) and the GEMM updates between blocks, end to end."""
+    import time
+
+    import torch
+
+    import quantize
+
+    W = (torch.randn(4096, 4096, generator=_gen(40)) * 0.02).to(dev)
+    X = torch.randn(2048, 4096, generator=_gen(41)).to(dev)
+    quantize.gptq_layer(W, X, 4, group_size=128)
+    best = float("inf")
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        quantize.gptq_layer(W, X, 4, group_size=128)
+        torch.cuda.synchronize()
+        best = min(best, time.perf_counter() - t0)
+    return {"workload": "gptq_layer", "out": 4096, "in": 4096, "calib_rows": 2048, "bits": 4,
+            "group_size": 128, "value": round(best * 1e3, 2), "unit": "ms per layer",
+            "higher_is_better": False, "dtype": "fp32"}
+
+
 def cpu_baseline(a, w, seconds: float) -> dict:
     """The reference's CPU path for the same GEMV (dequantize with the group scales, then an
     fp32 matmul), run through the numpy oracle on the host cores for a bounded sample."""
@@ -452,7 +477,8 @@ def main() -> int:
                      "bytes_per_launch": g["bytes"]},
     }
     if not args.no_secondary:
-        result["secondary"] = [bench_prefill(dev), bench_fp8(dev), bench_flash_decode(dev)]
+        result["secondary"] = [bench_prefill(dev), bench_fp8(dev), bench_flash_decode(dev),
+                               bench_gptq(dev)]
     if args.sweep:
         result["llama3_8b_sweep"] = bench_llama_sweep(dev)
     if not args.no_cpu_baseline:
