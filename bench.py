@@ -19,6 +19,7 @@ and one HBM-bound shape), and the reference's CPU path (dequantize + matmul, num
 a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--sweep]
+       python bench.py --only {prefill,gemm4096,fp8,flash_decode,gptq}   (one secondary line)
 """
 
 from __future__ import annotations
@@ -426,6 +427,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true", help="skip the GEMM lines")
     ap.add_argument("--sweep", action="store_true", help="add the Llama-3-8B layer sweep")
+    ap.add_argument("--only", choices=("prefill", "gemm4096", "fp8", "flash_decode", "gptq"),
+                    help="run one secondary workload alone and print its JSON (for profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the short kernel + copy sequence profiled with --pmc")
     args = ap.parse_args()
@@ -448,6 +451,11 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.traffic_probe:
         return traffic_probe(dev)
+    if args.only:
+        fn = {"prefill": bench_prefill, "gemm4096": lambda d: bench_prefill(d, M=4096),
+              "fp8": bench_fp8, "flash_decode": bench_flash_decode, "gptq": bench_gptq}[args.only]
+        print(json.dumps(fn(dev)), flush=True)
+        return 0
 
     g = bench_gemv(args, dev)
     gbs = g["bytes"] / (g["ms_per_step"] * 1e-3) / 1e9

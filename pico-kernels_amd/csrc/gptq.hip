@@ -2,17 +2,21 @@
 // quantize.py:104-110), lazily batched: the caller applies the updates of earlier blocks with
 // a GEMM, this kernel quantizes the block's columns one after another.
 //
-// For column c of the block and every row r, the value to quantize is
-//   v = Q[r, c] - sum_{j < c in the block} e[r, j] * ratio[j, c]
-// with the terms subtracted in j order, each product rounded before its subtraction: the
-// operations of the reference's eager update `wq[:, j+1:] -= outer(err, ratio)` applied to
-// column c, in the same order. Then v is quantized as quantize_col does (quantize.py:42-60):
+// Columns are swept in order. Quantizing column c uses its current value v (all updates from
+// the block's earlier columns already applied), as quantize_col does (quantize.py:42-60):
 // s = max|v over the scale domain|.clamp_min(1e-12) / qmax, q = clamp(rint(v / s), +-qmax) * s,
-// e = v - q. The scale domain is a group of `group` consecutive rows, or the whole column.
+// e = v - q. Then every later column c' of the block takes v[c'] = v[c'] - e * ratio[c][c'],
+// the product rounded before the subtraction: the reference's eager update
+// `wq[:, j+1:] -= outer(err, ratio)` restricted to the block, so each column receives the same
+// operations in the same order and the block's codes and errors equal the reference loop's bit
+// for bit. The scale domain is a group of `group` consecutive rows, or the whole column.
 //
-// One workgroup per scale domain. The block's ratios (transposed, rt[c][j]) and the domain's
-// error history (e[j][row]) live in LDS; a thread owns rows t, t + T, ... of the domain. The
-// only exchange between rows is the max per column (shuffles, then LDS across waves).
+// One workgroup of 1024 threads per scale domain: thread t owns row t % RT (RT = the domain's
+// rows rounded up to a power of two, at most 1024; more rows are taken in strides of RT) and
+// column group t / RT (CG = 1024 / RT groups). Group 0 quantizes and applies each column's
+// errors to the next column; the other groups update the columns after that. The block's
+// values (then, column by column, its errors) and ratios live in LDS; per column the threads
+// meet twice: the max over the domain, the errors.
 #include "pk_internal.h"
 
 namespace pk {
@@ -28,67 +32,113 @@ struct GptqParams {
 };
 
 constexpr int kGptqThreads = 1024;
+
+// |v| as an unsigned bit pattern: for non-negative floats and NaN these order the same way as
+// the values (NaN above infinity), so maxima are branch-free integer maxima and a NaN wins
+// as torch's max lets it.
+__device__ __forceinline__ unsigned abs_bits(float v) { return __builtin_bit_cast(unsigned, v) & 0x7fffffffu; }
+
+// Max over the wave: DPP within rows of 16 lanes, then the four rows.
+__device__ __forceinline__ unsigned wave_max_u32(unsigned x) {
+  int v = (int)x;
+  auto mx = [](int a, int b) { return (unsigned)a > (unsigned)b ? a : b; };
+  v = mx(v, __builtin_amdgcn_mov_dpp(v, 0xb1, 0xf, 0xf, true));   // quad_perm [1,0,3,2]
+  v = mx(v, __builtin_amdgcn_mov_dpp(v, 0x4e, 0xf, 0xf, true));   // quad_perm [2,3,0,1]
+  v = mx(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xf, 0xf, true));  // row_half_mirror
+  v = mx(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xf, 0xf, true));  // row_mirror
+  return (unsigned)mx(mx(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+                      mx(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Workgroup barrier for LDS data only: this wave's LDS operations complete (lgkmcnt(0)), then
+// s_barrier. Global stores stay in flight (__syncthreads() would wait for every one of them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt(63) expcnt(7) lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
 constexpr int kGptqLdsFloats = 38 * 1024;  // 152 KiB of the 160 KiB LDS
 
 __global__ __launch_bounds__(kGptqThreads) void gptq_block_kernel(GptqParams p) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) float lds[];
-  float* rt = lds;                          // [nb][nb]
-  float* eh = lds + p.nb * p.nb;            // [nb][rows of the domain]
-  __shared__ float red[kGptqThreads / 64];
-  const int t = threadIdx.x, T = blockDim.x, lane = t & 63, wave = t >> 6, nw = T >> 6;
+  float* rt = lds;                // [nb][nb]: rt[c][c'] = ratio[b0 + c][b0 + c']
+  float* vh = lds + p.nb * p.nb;  // [nb][rows]: values, column c's errors once it is swept
+  __shared__ __align__(16) unsigned red[kGptqThreads / 64];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r0 = blockIdx.x * p.domain;
   const int rows = min(p.domain, p.out - r0);
   const int nb = p.nb;
+  int RT = 64;
+  while (RT < rows && RT < kGptqThreads) RT <<= 1;
+  const int CG = kGptqThreads / RT, lr0 = t % RT, cg = t / RT;
 
-  for (int i = t; i < nb * nb; i += T) {
-    const int c = i / nb, j = i - c * nb;
-    rt[i] = j < c ? p.ratio[(int64_t)(p.b0 + j) * p.ldr + p.b0 + c] : 0.0f;
+  for (int i = t; i < nb * nb; i += kGptqThreads) {
+    const int c = i / nb, c2 = i - c * nb;
+    rt[i] = p.ratio[(int64_t)(p.b0 + c) * p.ldr + p.b0 + c2];
+  }
+  for (int i = t; i < nb * rows; i += kGptqThreads) {  // row-contiguous global reads
+    const int lr = i / nb, c = i - lr * nb;
+    vh[c * rows + lr] = p.q[(int64_t)(r0 + lr) * p.ldq + p.b0 + c];
   }
   __syncthreads();
 
   const float fq = (float)p.qmax;
   for (int c = 0; c < nb; ++c) {
-    const float* rc = rt + c * nb;
-    float amax = 0.0f;
-    for (int lr = t; lr < rows; lr += T) {
-      float v = p.q[(int64_t)(r0 + lr) * p.ldq + p.b0 + c];
-      int j = 0;
-      for (; j + 4 <= c; j += 4) {
-        const float e0 = eh[(j + 0) * rows + lr], e1 = eh[(j + 1) * rows + lr];
-        const float e2 = eh[(j + 2) * rows + lr], e3 = eh[(j + 3) * rows + lr];
-        v = v - e0 * rc[j + 0];
-        v = v - e1 * rc[j + 1];
-        v = v - e2 * rc[j + 2];
-        v = v - e3 * rc[j + 3];
-      }
-      for (; j < c; ++j) v = v - eh[j * rows + lr] * rc[j];
-      eh[c * rows + lr] = v;  // the value to quantize, until its error replaces it
-      amax = nanmax(amax, __builtin_fabsf(v));
-    }
-    // max over the domain (order-free)
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) amax = nanmax(amax, wave_shfl_xor(amax, m));
+    float* vc = vh + c * rows;
+    unsigned amax = 0u;
+    if (cg == 0)
+      for (int lr = lr0; lr < rows; lr += RT) amax = max(amax, abs_bits(vc[lr]));
+    amax = wave_max_u32(amax);
     if (lane == 0) red[wave] = amax;
-    __syncthreads();
-    float a = red[0];
-    for (int w = 1; w < nw; ++w) a = nanmax(a, red[w]);
-    __syncthreads();  // red is rewritten by the next column
+    lds_barrier();
+    unsigned m4 = 0u;
+#pragma unroll
+    for (int w = 0; w < kGptqThreads / 64; w += 4) {  // all reads issued before any use
+      const pk_u4v r4 = *reinterpret_cast<const pk_u4v*>(red + w);
+      m4 = max(m4, max(max(r4[0], r4[1]), max(r4[2], r4[3])));
+    }
+    const float a = __builtin_bit_cast(float, m4);
     const float s = (a < 1e-12f ? 1e-12f : a) / fq;  // clamp_min: NaN passes through
-    for (int lr = t; lr < rows; lr += T) {
-      const float v = eh[c * rows + lr];
-      const float r = clamp_nan(__builtin_rintf(v / s), -fq, fq);
-      const float qv = r * s;
-      const float e = v - qv;
-      eh[c * rows + lr] = e;
-      p.q[(int64_t)(r0 + lr) * p.ldq + p.b0 + c] = qv;
-      p.err[(int64_t)(r0 + lr) * p.lde + c] = e;
+    if (cg == 0) {
+      for (int lr = lr0; lr < rows; lr += RT) {
+        const float v = vc[lr];
+        const float r = clamp_nan(__builtin_rintf(v / s), -fq, fq);
+        const float qv = r * s;
+        const float e = v - qv;
+        vc[lr] = e;
+        p.q[(int64_t)(r0 + lr) * p.ldq + p.b0 + c] = qv;
+        p.err[(int64_t)(r0 + lr) * p.lde + c] = e;
+      }
+    }
+    lds_barrier();  // column c's errors visible; every read of red done
+    // Group 0 (the rows' quantizers) applies e to column c + 1 itself and goes on to quantize it;
+    // the other groups update columns c + 2 .. and are waited for at the next column's first
+    // barrier, before column c + 2 is read. A column's updates still arrive in column order.
+    const float* rc = rt + c * nb;
+    const int first = cg == 0 ? c + 1 : c + 2 + (cg - 1);
+    const int stride = CG == 1 ? 1 : CG - 1;
+    const int stop = (cg == 0 && CG > 1) ? min(c + 2, nb) : nb;
+    for (int lr = lr0; lr < rows; lr += RT) {
+      const float e = vc[lr];
+      float* vr = vh + lr;
+      int c2 = first;
+      for (; c2 + 3 * stride < stop; c2 += 4 * stride) {  // all loads before any store (the
+        float x[4], r[4];                                  // values and ratios share one array)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          x[u] = vr[(c2 + u * stride) * rows];
+          r[u] = rc[c2 + u * stride];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) vr[(c2 + u * stride) * rows] = x[u] - e * r[u];
+      }
+      for (; c2 < stop; c2 += stride) vr[c2 * rows] = vr[c2 * rows] - e * rc[c2];
     }
   }
 }
 
 // Columns per block for a scale domain of `rows` rows: the largest power of two up to 128
-// whose ratios and error history fit the LDS budget; 0 if not even one column fits.
+// whose ratios and values fit the LDS budget; 0 if not even one column fits.
 inline int gptq_block_cols(int rows) {
   for (int nb = 128; nb >= 1; nb >>= 1)
     if ((int64_t)nb * nb + (int64_t)nb * rows <= kGptqLdsFloats) return nb;
@@ -141,9 +191,8 @@ extern "C" int pk_gptq_block(float* q, int64_t ldq, const float* ratio, int64_t 
     if (e != hipSuccess) return hip_status(e, "gptq: set LDS size");
     attr_done = true;
   }
-  const int threads = domain >= kGptqThreads ? kGptqThreads : ((domain + 63) / 64) * 64;
   const int grid = (out + domain - 1) / domain;
-  gptq_block_kernel<<<grid, threads, lds, (hipStream_t)stream>>>(p);
+  gptq_block_kernel<<<grid, kGptqThreads, lds, (hipStream_t)stream>>>(p);
   PK_LAUNCH_CHECK("gptq block");
   return PK_OK;
 }
