@@ -407,6 +407,34 @@ def traffic_probe(dev) -> int:
     return 0
 
 
+def mfma_probe(dev) -> int:
+    """Eager launches (no graph) of the GEMMs whose MFMA utilisation is read with rocprofv3
+    --pmc: W4A16 prefill 2048x4096x4096 and 4096^3, fp8 4096^3 (fp16 out), 5 calls each."""
+    import torch
+
+    import _pk
+    import gemm_fp8
+    import gemm_int4
+
+    for M in (2048, 4096):
+        a = torch.randn(M, 4096, generator=_gen(2)).half().to(dev)
+        w = (torch.randn(4096, 4096, generator=_gen(3)) * 0.02).half().to(dev)
+        qw, sc = gemm_int4.quantize_int4_group(w, 128)
+        out = torch.empty((M, 4096), dtype=torch.float16, device=dev)
+        for _ in range(5):
+            _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, out=out)
+    a = torch.randn(4096, 4096, generator=_gen(4)).half().to(dev)
+    b = torch.randn(4096, 4096, generator=_gen(5)).half().to(dev)
+    a8, sa = gemm_fp8.quantize(a)
+    b8, sb = gemm_fp8.quantize(b)
+    out = torch.empty((4096, 4096), dtype=torch.float16, device=dev)
+    for _ in range(5):
+        _pk.fp8_gemm(a8, b8, 1.0 / (sa * sb), torch.float16, out=out)
+    torch.cuda.synchronize()
+    print("mfma probe done", flush=True)
+    return 0
+
+
 def measured_traffic():
     """HBM bytes per slice-kernel launch from the committed --pmc summary, or None."""
     import re
@@ -429,6 +457,8 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="add the Llama-3-8B layer sweep")
     ap.add_argument("--only", choices=("prefill", "gemm4096", "fp8", "flash_decode", "gptq"),
                     help="run one secondary workload alone and print its JSON (for profiling)")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="only run eager GEMM calls for rocprofv3 --pmc MFMA utilisation")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the short kernel + copy sequence profiled with --pmc")
     args = ap.parse_args()
@@ -451,6 +481,8 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.traffic_probe:
         return traffic_probe(dev)
+    if args.mfma_probe:
+        return mfma_probe(dev)
     if args.only:
         fn = {"prefill": bench_prefill, "gemm4096": lambda d: bench_prefill(d, M=4096),
               "fp8": bench_fp8, "flash_decode": bench_flash_decode, "gptq": bench_gptq}[args.only]
