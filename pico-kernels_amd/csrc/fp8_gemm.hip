@@ -231,13 +231,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void fp8_gemm_kernel(Fp8Par
 template <int BM, int BN, int WMW, int WNW, int BL>
 static int fp8_launch_cfg(Fp8Params& p, hipStream_t s) {
   constexpr size_t lds = (size_t)2 * (BM + BN) * kF8Row;
-  static bool attr_done = false;
-  if (!attr_done) {
-    hipError_t e = hipFuncSetAttribute((const void*)fp8_gemm_kernel<BM, BN, WMW, WNW, BL>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return hip_status(e, "fp8 gemm: set LDS size");
-    attr_done = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};
+  if (const int rc = set_lds_limit_once((const void*)fp8_gemm_kernel<BM, BN, WMW, WNW, BL>, (int)lds, &lds_done)) return rc;
   p.tiles_m = (int)cdiv(p.M, BM);
   p.tiles_n = (int)cdiv(p.N, BN);
   fp8_gemm_kernel<BM, BN, WMW, WNW, BL><<<p.tiles_m * p.tiles_n, 64 * WMW * WNW, lds, s>>>(p);

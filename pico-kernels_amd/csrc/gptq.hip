@@ -183,14 +183,8 @@ extern "C" int pk_gptq_block(float* q, int64_t ldq, const float* ratio, int64_t 
   p.domain = domain;
   p.qmax = (1 << (bits - 1)) - 1;
   const size_t lds = ((size_t)nb * nb + (size_t)nb * domain) * sizeof(float);
-  static bool attr_done = false;
-  if (!attr_done) {
-    hipError_t e = hipFuncSetAttribute((const void*)gptq_block_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)(kGptqLdsFloats * sizeof(float)));
-    if (e != hipSuccess) return hip_status(e, "gptq: set LDS size");
-    attr_done = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};
+  if (const int rc = set_lds_limit_once((const void*)gptq_block_kernel, (int)(kGptqLdsFloats * sizeof(float)), &lds_done)) return rc;
   const int grid = (out + domain - 1) / domain;
   gptq_block_kernel<<<grid, kGptqThreads, lds, (hipStream_t)stream>>>(p);
   PK_LAUNCH_CHECK("gptq block");

@@ -1,5 +1,7 @@
 // Internal planning/launch interfaces shared between the kernel files and the C-ABI layer.
 #pragma once
+#include <atomic>
+
 #include "pk_common.h"
 
 namespace pk {
@@ -21,6 +23,11 @@ inline float* split_partials(void* ws, bool partials_only) {
 // Host: split-K slices may hand off through one XCD's L2 on the current device (its XCC count
 // divides 8; the environment variable PK_SPLITK_IN_L2=0 turns it off).
 bool splitk_in_l2_ok();
+
+// Host: allow `kernel` up to `bytes` of dynamic LDS on the current device. The attribute is
+// set once per (device, kernel): `done` is a per-kernel bit set of the devices already done
+// (64 at most); concurrent first calls may both set it, which is harmless.
+int set_lds_limit_once(const void* kernel, int bytes, std::atomic<uint64_t>* done);
 
 // C = scale * sum over slices of the (S, M, N) fp32 partials, in slice order.
 int splitk_reduce(const float* partials, int S, int M, int N, float scale, void* c, int c_dtype,

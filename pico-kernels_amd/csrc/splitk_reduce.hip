@@ -12,6 +12,18 @@ namespace pk {
 
 // The XCD grouping of xcd_tile_slice holds when the partition's XCC count divides 8 (SPX 8,
 // DPX 4, QPX 2, CPX 1). Queried once per device.
+int set_lds_limit_once(const void* kernel, int bytes, std::atomic<uint64_t>* done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "set LDS limit: hipGetDevice");
+  const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit && (done->load(std::memory_order_acquire) & bit)) return PK_OK;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) return hip_status(e, "set LDS limit");
+  if (bit) done->fetch_or(bit, std::memory_order_release);
+  return PK_OK;
+}
+
 bool splitk_in_l2_ok() {
   static std::atomic<int> state[64];  // 0 unknown, 1 on, 2 off
   int dev = 0;

@@ -334,13 +334,8 @@ size_t gemm_workspace_bytes(const GemmPlan& pl, int M, int N) {
 template <int BM, int BN, int WMW, int WNW, int BMODE>
 static int launch_cfg(const GemmParams& p, hipStream_t s) {
   constexpr size_t lds = (size_t)2 * (BM + BN) * kLdsRow * sizeof(pk_half);
-  static bool attr_done = false;
-  if (!attr_done) {
-    hipError_t e = hipFuncSetAttribute((const void*)gemm_mfma_kernel<BM, BN, WMW, WNW, BMODE>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return hip_status(e, "gemm: set LDS size");
-    attr_done = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};
+  if (const int rc = set_lds_limit_once((const void*)gemm_mfma_kernel<BM, BN, WMW, WNW, BMODE>, (int)lds, &lds_done)) return rc;
   dim3 grid(p.tiles_m * p.tiles_n, p.split);
   gemm_mfma_kernel<BM, BN, WMW, WNW, BMODE><<<grid, 64 * WMW * WNW, lds, s>>>(p);
   PK_LAUNCH_CHECK("gemm mfma");
