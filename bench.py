@@ -343,13 +343,7 @@ def cpu_baseline(a, w, seconds: float) -> dict:
 
     import oracle
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((p.get("num_threads", 1) for p in threadpool_info()
-                       if p.get("user_api") == "blas"), default=1)
-    except Exception:  # threadpoolctl missing: numpy's BLAS default
-        threads = os.cpu_count() or 1
+    threads = _blas_threads()
     an = a.numpy()
     codes, _, s16 = oracle.rtn_group_codes(w.numpy(), 4, 128)
     packed = oracle.pack_int4_n(codes)
@@ -368,6 +362,56 @@ def cpu_baseline(a, w, seconds: float) -> dict:
             "kind": "port", "sample": f"{reps} full GEMVs (M=1, K=4096, N=11008: unpack + "
             f"group dequant + fp32 matmul) in {el:.1f} s", "ms_per_step": round(el / reps * 1e3, 2),
             "check": float(np.abs(y).sum())}
+
+
+def _blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        return int(max((p.get("num_threads", 1) for p in threadpool_info()
+                        if p.get("user_api") == "blas"), default=1))
+    except Exception:  # threadpoolctl missing: numpy's BLAS default
+        return os.cpu_count() or 1
+
+
+def cpu_baseline_gemm(kind: str, seconds: float) -> dict:
+    """The reference's CPU path for the GEMM lines, full size, through the numpy oracle:
+    W4A16 2048x4096x4096 = unpack + group dequantize + fp32 matmul of the same seeded inputs
+    as bench_prefill; fp8 4096^3 = the e4m3 bytes decoded to fp32, fp32 matmul, out_scale
+    (the test-path oracle, tests/test_gemm_fp8.py:24). Repeated for about `seconds`."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    if kind == "w4a16":
+        M, K, N = 2048, 4096, 4096
+        a = torch.randn(M, K, generator=_gen(2)).half().numpy()
+        w = (torch.randn(K, N, generator=_gen(3)) * 0.02).half().numpy()
+        codes, _, s16 = oracle.rtn_group_codes(w, 4, 128)
+        packed = oracle.pack_int4_n(codes)
+
+        def run():
+            return oracle.w4a16_ref(a, oracle.unpack_int4_n(packed), s16, 128)
+    else:
+        M = N = K = 4096
+        a8, sa = oracle.fp8_quantize(torch.randn(M, K, generator=_gen(4)).half().numpy())
+        b8, sb = oracle.fp8_quantize(torch.randn(K, N, generator=_gen(5)).half().numpy())
+
+        def run():
+            return oracle.fp8_gemm_ref(a8, sa, b8, sb)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        y = run()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    flop = 2.0 * M * N * K
+    return {"value": round(flop * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": _blas_threads(),
+            "kind": "port", "sample": f"{reps} full {M}x{K}x{N} products ({'unpack + group dequant' if kind == 'w4a16' else 'e4m3 decode'} + fp32 matmul) in {el:.1f} s",
+            "ms_per_step": round(el / reps * 1e3, 1), "check": float(np.abs(y).sum())}
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "w4a16_gemv_decode_traffic.md"
@@ -527,6 +571,12 @@ def main() -> int:
     if not args.no_cpu_baseline:
         a, w = g["inputs"]
         result["cpu_baseline"] = cpu_baseline(a, w, args.cpu_seconds)
+        if not args.no_secondary:  # the reference's CPU path beside the GEMM lines too
+            for entry in result["secondary"]:
+                if entry["workload"] == "w4a16_prefill_gemm":
+                    entry["cpu_baseline"] = cpu_baseline_gemm("w4a16", args.cpu_seconds / 3)
+                elif entry["workload"] == "fp8_e4m3_gemm":
+                    entry["cpu_baseline"] = cpu_baseline_gemm("fp8", args.cpu_seconds / 3)
     print(json.dumps(result), flush=True)
     return 0
 
