@@ -414,6 +414,57 @@ def cpu_baseline_gemm(kind: str, seconds: float) -> dict:
             "ms_per_step": round(el / reps * 1e3, 1), "check": float(np.abs(y).sum())}
 
 
+def cpu_baseline_decode(seconds: float) -> dict:
+    """The reference's single-query attention (eager_decode, flash_decoding.py:126-133) on the
+    host through the float64 oracle, on 8 of the 256 (b, h) pairs of the bench shape
+    (N = 8192, D = 128); GB/s of fp16 K/V those pairs hold."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    H, N, D = 8, 8192, 128
+    q = torch.randn(1, H, 1, D, generator=_gen(30)).half().numpy()
+    k = torch.randn(1, H, N, D, generator=_gen(31)).half().numpy()
+    v = torch.randn(1, H, N, D, generator=_gen(32)).half().numpy()
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        y = oracle.decode_attention_ref(q, k, v)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(flash_decode_bytes(1, H, N, D) * reps / el / 1e9, 3), "unit": "GB/s",
+            "cores": _blas_threads(), "kind": "port",
+            "sample": f"{reps} calls of 1x{H}x{N}x{D} (8 of the 256 heads) in {el:.1f} s",
+            "check": float(np.abs(y).sum())}
+
+
+def cpu_baseline_gptq(seconds: float) -> dict:
+    """The reference's gptq_layer column loop on the host through the oracle (fp32, one column
+    at a time, quantize.py:71-115), on a 1024 x 1024 layer (a 4096 x 4096 one is ~64x the
+    work); milliseconds per 1024 x 1024 layer."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    W = (torch.randn(1024, 1024, generator=_gen(42)) * 0.02).numpy()
+    X = torch.randn(512, 1024, generator=_gen(43)).numpy()
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        q = oracle.gptq_layer(W, X, 4, group_size=128)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(el / reps * 1e3, 1), "unit": "ms per 1024x1024 layer", "cores": _blas_threads(),
+            "kind": "port", "sample": f"{reps} layers of 1024x1024 (512 calibration rows, group 128) in {el:.1f} s",
+            "check": float(np.abs(q).sum())}
+
+
 TRAFFIC_PROFILE = ROOT / "profiles" / "w4a16_gemv_decode_traffic.md"
 COPY_PROBE_BYTES = 256 << 20
 
@@ -577,6 +628,10 @@ def main() -> int:
                     entry["cpu_baseline"] = cpu_baseline_gemm("w4a16", args.cpu_seconds / 3)
                 elif entry["workload"] == "fp8_e4m3_gemm":
                     entry["cpu_baseline"] = cpu_baseline_gemm("fp8", args.cpu_seconds / 3)
+                elif entry["workload"] == "split_kv_decode_attention":
+                    entry["cpu_baseline"] = cpu_baseline_decode(args.cpu_seconds / 6)
+                elif entry["workload"] == "gptq_layer":
+                    entry["cpu_baseline"] = cpu_baseline_gptq(args.cpu_seconds / 6)
     print(json.dumps(result), flush=True)
     return 0
 
