@@ -134,12 +134,21 @@ def ptr(t: torch.Tensor | None) -> int | None:
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
+# Workspaces a larger one replaced. A captured HIP graph keeps using the address it recorded,
+# so a replaced workspace is never handed back to the allocator.
+_retired_workspaces: list[torch.Tensor] = []
+
+
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """The zero-initialised workspace of (device, current stream), grown to `nbytes` on demand
+    (the split-K counters at its head are left zero by every call)."""
     if nbytes <= 0:
         return None
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _retired_workspaces.append(ws)
         size = max(nbytes, 1 << 20)
         ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
