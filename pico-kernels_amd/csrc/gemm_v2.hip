@@ -17,6 +17,9 @@
 //  * Addresses: one buffer resource per operand, per-lane byte offsets computed once, the K
 //    advance folded into the scalar offset. Rows/columns past the matrix are clamped to the
 //    last valid one (never read out of bounds); their results are not stored.
+//  * Epilogue (f16 kernel): each wave stages its block of C (or of the split-K partials) in a
+//    free stage array and stores it back row-contiguous, whole 128-byte lines per store
+//    instruction.
 #include "pk_internal.h"
 
 namespace pk {
@@ -374,9 +377,67 @@ void gemm_v3_f16_kernel(V2Params p) {
 
   float* part = p.split > 1 ? p.partials + (int64_t)blockIdx.y * p.M * p.N : nullptr;
   const int esz = part ? 4 : (p.c_dtype == PK_F32 ? 4 : 2);
+  const int em = lane & 31, en = 4 * (lane >> 5);
+  // Through LDS when rows are 16-byte aligned: each wave stages its WTM x WTN block in a free
+  // stage array (rows of WTN values, 16-byte chunks XOR-swizzled by row), then writes it back
+  // row-contiguous, 16 bytes per lane, so a store instruction covers whole lines instead of
+  // 8 or 16 bytes in each of 32 rows (measured on MI355X: the prefill GEMM 5-6% faster).
+  char* const out_base = part ? reinterpret_cast<char*>(part) : reinterpret_cast<char*>(p.c);
+  const int64_t ld_out = part ? p.N : p.ldc;
+  if ((ld_out * esz) % 16 == 0 && (reinterpret_cast<uintptr_t>(out_base) & 15) == 0) {
+    constexpr int STG = WTM * WTN * 4;  // bytes a wave stages (fp32 at most)
+    static_assert(2 * STG <= BM * 128 && (2 * STG <= BN * 128 || STG <= BN * 128), "staging");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS reads are done
+    __syncthreads();                     // and every other wave's: the stages are free
+    char* sW;
+    if (wave < 6) {
+      char* const a2 = wave < 2 ? sA0 : wave < 4 ? sA1 : sA2;
+      sW = a2 + (wave & 1) * STG;
+    } else if constexpr (2 * STG <= BN * 128) {
+      sW = sB0 + (wave - 6) * STG;
+    } else {
+      sW = wave == 6 ? sB0 : sB1;
+    }
+    with_dtype(part ? PK_F32 : p.c_dtype, [&](auto DT) {
+      constexpr int dt = decltype(DT)::value;
+      constexpr int E = dt == PK_F32 ? 4 : 2;
+      constexpr int RB = WTN * E, NCH = RB / 16;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int r = 32 * i + em, col = 32 * j + 8 * q + en;
+            const int byte = col * E;
+            char* dst = sW + r * RB + ((((byte >> 4) ^ (r % NCH)) << 4) | (byte & 15));
+            pk_f4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            if (!part) v *= p.scale;
+            if constexpr (dt == PK_F32) {
+              *reinterpret_cast<pk_f4*>(dst) = v;
+            } else if constexpr (dt == PK_F16) {
+              const pk_half4 hv = {(pk_half)v[0], (pk_half)v[1], (pk_half)v[2], (pk_half)v[3]};
+              *reinterpret_cast<pk_u2v*>(dst) = __builtin_bit_cast(pk_u2v, hv);
+            } else {
+              const pk_u2v bv = {(uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16),
+                                 (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16)};
+              *reinterpret_cast<pk_u2v*>(dst) = bv;
+            }
+          }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // the wave's staging writes are in LDS
+#pragma unroll
+      for (int c0 = 0; c0 < WTM * NCH; c0 += 64) {
+        const int idx = c0 + lane, r = idx / NCH, ch = idx % NCH;
+        const pk_u4v val = *reinterpret_cast<const pk_u4v*>(sW + r * RB + ((ch ^ (r % NCH)) << 4));
+        const int gm = m0 + wm0 + r, gn = n0 + wn0 + ch * (16 / E);
+        if (gm < p.M && gn < p.N)  // N % 8 == 0: a chunk is all in or all out
+          *PK_GLOBAL(pk_u4v, out_base + ((int64_t)gm * ld_out + gn) * E) = val;
+      }
+    });
+    return;
+  }
   const bool vec = part ? true
                         : (p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & (4 * esz - 1)) == 0);
-  const int em = lane & 31, en = 4 * (lane >> 5);
   with_dtype(part ? PK_F32 : p.c_dtype, [&](auto DT) {
     constexpr int dt = decltype(DT)::value;
 #pragma unroll
