@@ -123,8 +123,8 @@ __global__ __launch_bounds__(kGemvCW* RL) void w4a16_gemv_kernel(GemvParams p) {
     if constexpr (VEC) {
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p.qw + (int64_t)(kb + r) * p.ldq + word0);
-        w[r][0] = v.x; w[r][1] = v.y; w[r][2] = v.z; w[r][3] = v.w;
+        const pk_u4v v = __builtin_nontemporal_load(reinterpret_cast<const pk_u4v*>(p.qw + (int64_t)(kb + r) * p.ldq + word0));
+        w[r][0] = v[0]; w[r][1] = v[1]; w[r][2] = v[2]; w[r][3] = v[3];
       }
     } else {
       const int wlast = words_total - 1;
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(kGemvCW* RL) void w4a16_gemv_kernel(GemvParams p) {
       if constexpr (VEC) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const pk_half8 h = *reinterpret_cast<const pk_half8*>(srow + (int64_t)word0 * 8 + 8 * v);
+          const pk_half8 h = __builtin_nontemporal_load(reinterpret_cast<const pk_half8*>(srow + (int64_t)word0 * 8 + 8 * v));
 #pragma unroll
           for (int e = 0; e < 8; ++e) sc[8 * v + e] = (float)h[e];
         }
@@ -302,7 +302,7 @@ void w4a16_gemv_mfma_kernel(GemvParams p) {
     const int scol = min(col_base + t, p.N - 1);
 #pragma unroll
     for (int w = 0; w < NW; ++w)
-      sc[w] = (float)p.scales[(int64_t)((slice * NW * WROWS + w * WROWS) / p.group) * p.N + scol];
+      sc[w] = (float)__builtin_nontemporal_load(p.scales + (int64_t)((slice * NW * WROWS + w * WROWS) / p.group) * p.N + scol);
   }
 
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.qw, (uint32_t)((int64_t)p.K * p.ldq * 4));
@@ -315,7 +315,7 @@ void w4a16_gemv_mfma_kernel(GemvParams p) {
     xq[rb] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(xrow * p.lda + rl * 8) * 2, (kb + 64 * rb) * 2, 0);
 #pragma unroll
     for (int r = 0; r < 8; ++r)
-      w[rb][r] = __builtin_amdgcn_raw_buffer_load_b128(rq, q_voff, (kb + 64 * rb + r) * ldq4, 0);
+      w[rb][r] = __builtin_amdgcn_raw_buffer_load_b128(rq, q_voff, (kb + 64 * rb + r) * ldq4, kPkLoadStream);
   }
 
   const pk_f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
