@@ -24,10 +24,11 @@ typedef unsigned pk_u2v __attribute__((ext_vector_type(2)));
 
 constexpr unsigned kRsrcWord3 = 0x00020000u;  // raw (untyped) buffer, gfx9-family encoding
 
-// Cache policy of a buffer load of data read once (weights, K/V streams): non-temporal, so
-// the stream does not evict what is reused from L2 (split-K partials before their last reader,
-// activations). Measured on MI355X: the M=1 GEMV 10% faster with its weights and scales loaded
-// this way.
+// Cache policy of a buffer load of data read exactly once (weights, K/V streams):
+// non-temporal. Measured on MI355X: the M=1 GEMV 7-10% faster and split-KV decode attention 13%
+// faster with their streams loaded this way (the bytes fetched from memory, FETCH_SIZE, are
+// unchanged); it does not pay for the W4A16 kernel at 5 <= M <= 32 or for GEMM operands that
+// several workgroups share.
 constexpr int kPkLoadStream = 2;
 
 // Raw buffer resource over [p, p + bytes): loads take a per-lane byte offset (VGPR) plus a
