@@ -530,6 +530,71 @@ def mfma_probe(dev) -> int:
     return 0
 
 
+def mfma_ceiling(dev) -> dict:
+    """What the matrix cores sustain with no memory traffic (pk_mfma_probe): 256 workgroups of
+    8 waves issuing independent MFMAs on constant or pseudo-random operands, timed with HIP
+    events on the launch stream, against MI355X's published dense peaks."""
+    import torch
+
+    import _pk
+
+    grid, iters = 256, 4000
+    out = torch.empty(grid * 512, dtype=torch.float32, device=dev)
+    rows = []
+    for fp8, peak in ((True, MFMA_F8_PEAK_TFLOPS), (False, MFMA_F16_PEAK_TFLOPS)):
+        flops = grid * 8 * iters * 8 * (131072 if fp8 else 32768)
+        for random in (False, True):
+            _pk.mfma_probe(fp8, random, grid, iters, out)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(5):
+                _pk.mfma_probe(fp8, random, grid, iters, out)
+            e1.record()
+            e1.synchronize()
+            tf = 5 * flops / (e0.elapsed_time(e1) * 1e-3) / 1e12
+            rows.append({"dtype": "e4m3" if fp8 else "fp16", "operands": "random" if random else "constant",
+                         "TFLOP/s": round(tf, 1), "frac_of_dense_peak": round(tf / peak, 4)})
+    return {"mfma_ceiling": rows, "grid": grid, "waves_per_workgroup": 8, "mfmas_per_wave": iters * 8}
+
+
+def vendor_compare(dev) -> dict:
+    """This library's GEMMs beside the vendor library's (hipBLASLt through torch) on the same
+    GPU and inputs: fp16 GEMMs with B row-major (NN) and transposed (NT) against the W4A16
+    GEMM, torch._scaled_mm against the fp8 GEMM; graph-timed like the bench lines."""
+    import torch
+
+    import _pk
+    import gemm_fp8
+    import gemm_int4
+
+    rows = []
+    for (M, N, K) in ((2048, 4096, 4096), (4096, 4096, 4096), (8192, 8192, 8192)):
+        a = torch.randn(M, K, generator=_gen(4)).half().to(dev)
+        b = torch.randn(K, N, generator=_gen(5)).half().to(dev)
+        bt = b.t().contiguous()
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        w = (torch.randn(K, N, generator=_gen(6)) * 0.02).half().to(dev)
+        qw, sc = gemm_int4.quantize_int4_group(w, 128)
+        a8, sa = gemm_fp8.quantize(a)
+        b8, sb = gemm_fp8.quantize(b)
+        b8t = b8.t().contiguous().t()
+        one = torch.tensor(1.0, device=dev)
+
+        def tf(fn):
+            ms = GraphTimer(fn, 20, 2).run(reps=3)
+            return round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)
+
+        rows.append({"M": M, "N": N, "K": K,
+                     "hipblaslt_f16_nn": tf(lambda i: torch.matmul(a, b, out=out)),
+                     "hipblaslt_f16_nt": tf(lambda i: torch.matmul(a, bt.t(), out=out)),
+                     "pk_w4a16_g128": tf(lambda i: _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, out=out)),
+                     "hipblaslt_fp8_scaled_mm": tf(lambda i: torch._scaled_mm(a8, b8t, one, one, out_dtype=torch.float16)),
+                     "pk_fp8": tf(lambda i: _pk.fp8_gemm(a8, b8, 1.0, torch.float16, out=out)),
+                     "unit": "TFLOP/s"})
+        del a, b, bt, out, w, qw, sc, a8, b8, b8t
+    return {"vendor_compare": rows}
+
+
 def measured_traffic():
     """HBM bytes per slice-kernel launch from the committed --pmc summary, or None."""
     import re
@@ -554,6 +619,10 @@ def main() -> int:
                     help="run one secondary workload alone and print its JSON (for profiling)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only run eager GEMM calls for rocprofv3 --pmc MFMA utilisation")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only measure the matrix cores' sustained rate with no memory traffic")
+    ap.add_argument("--vendor", action="store_true",
+                    help="only time hipBLASLt's fp16 / fp8 GEMMs beside this library's")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the short kernel + copy sequence profiled with --pmc")
     args = ap.parse_args()
@@ -578,6 +647,12 @@ def main() -> int:
         return traffic_probe(dev)
     if args.mfma_probe:
         return mfma_probe(dev)
+    if args.mfma_ceiling:
+        print(json.dumps(mfma_ceiling(dev)), flush=True)
+        return 0
+    if args.vendor:
+        print(json.dumps(vendor_compare(dev)), flush=True)
+        return 0
     if args.only:
         fn = {"prefill": bench_prefill, "gemm4096": lambda d: bench_prefill(d, M=4096),
               "fp8": bench_fp8, "flash_decode": bench_flash_decode, "gptq": bench_gptq}[args.only]

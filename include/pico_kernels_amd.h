@@ -251,6 +251,15 @@ int pk_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int6
                     int64_t svn, int B, int H, int N, int D, int split, float sm_scale,
                     float* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- Measurement ------------------------------------------------------------------------
+ * pk_mfma_probe: no counterpart in the reference; for benchmarks that read the GEMMs'
+ * roofline fractions against what the matrix cores sustain. Launches `grid` workgroups of 8
+ * waves that each issue iters x 8 independent MFMAs (fp8 != 0: v_mfma 32x32x64 e4m3, else
+ * 32x32x16 fp16) on constant (random == 0) or pseudo-random register operands, with no memory
+ * traffic in the loop; out receives grid * 512 floats. FLOPs per launch:
+ * grid * 8 * iters * 8 * (fp8 ? 131072 : 32768). */
+int pk_mfma_probe(int fp8, int random, int grid, int iters, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

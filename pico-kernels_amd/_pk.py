@@ -69,6 +69,7 @@ _SIGNATURES = {
     "pk_flash_decode_launches": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "pk_flash_decode": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
                                _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _sz, _vp]),
+    "pk_mfma_probe": (_i32, [_i32, _i32, _i32, _i32, _vp, _vp]),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
@@ -384,3 +385,11 @@ def flash_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, split: int,
                                  0 if ws is None else ws.numel(), stream_of(q)),
            "pk_flash_decode")
     return out
+
+
+def mfma_probe(fp8: bool, random: bool, grid: int, iters: int, out: torch.Tensor) -> None:
+    """Pure-MFMA throughput probe on the current stream (pk_mfma_probe); ``out`` holds
+    ``grid * 512`` fp32 values."""
+    assert out.dtype == torch.float32 and out.numel() >= grid * 512 and out.is_cuda
+    _check(lib().pk_mfma_probe(int(fp8), int(random), int(grid), int(iters), out.data_ptr(),
+                               stream_of(out)), "pk_mfma_probe")
