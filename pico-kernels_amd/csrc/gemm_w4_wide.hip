@@ -46,9 +46,7 @@ struct W4WideParams {
   int c_dtype;
   int64_t ldc;
   int M, N, K;
-  int k_slice;
   int tiles_m, tiles_n;
-  float* partials;        // (split, M, N) when the grid has more than one k slice
 };
 
 __device__ __forceinline__ void w4w_dma16(__amdgpu_buffer_rsrc_t r, char* lds, int voff, int soff) {
@@ -101,8 +99,7 @@ __global__ __launch_bounds__(512) void gemm_w4_wide_kernel(W4WideParams p) {
   int tm, tn;
   w4w_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * 256;
-  const int k_begin = blockIdx.y * p.k_slice;
-  const int ktiles = p.k_slice / BK;
+  const int ktiles = p.K / BK;
   const int last = ktiles - 1;
 
   // ---- A: two 1 KB DMA instructions per wave per tile (16 rows of 64 bytes each) ----
@@ -115,7 +112,7 @@ __global__ __launch_bounds__(512) void gemm_w4_wide_kernel(W4WideParams p) {
     a_off[i] = (int)((int64_t)min(m0 + r, p.M - 1) * p.lda * 2) + c * 16;
   }
   auto issue_a_part = [&](int kt, char* sA, int part) {
-    w4w_dma16(ra, sA + (wave * 2 + part) * 1024, a_off[part], (k_begin + kt * BK) * 2);
+    w4w_dma16(ra, sA + (wave * 2 + part) * 1024, a_off[part], kt * BK * 2);
   };
 
   // ---- B words and scales of a tile into a register slot ----
@@ -130,7 +127,7 @@ __global__ __launch_bounds__(512) void gemm_w4_wide_kernel(W4WideParams p) {
   pk_u4v bs[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
   auto load_b = [&](int kt, auto SLOT) {
     constexpr int sl = decltype(SLOT)::value;
-    const int k0 = k_begin + kt * BK;
+    const int k0 = kt * BK;
     const int soff = (int)((int64_t)k0 * p.ldb * 4);
     bw[sl][0] = __builtin_amdgcn_raw_buffer_load_b32(rb, b_off0, soff, 0);
     bw[sl][1] = __builtin_amdgcn_raw_buffer_load_b32(rb, b_off1, soff, 0);
@@ -238,12 +235,11 @@ __global__ __launch_bounds__(512) void gemm_w4_wide_kernel(W4WideParams p) {
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): no DMA into LDS outlives the waves
   mfma_drain();
 
-  // ---- epilogue: C (scaled, in the output dtype) or the slice's fp32 partials ----
-  float* part = gridDim.y > 1 ? p.partials + (int64_t)blockIdx.y * p.M * p.N : nullptr;
-  char* const out_base = part ? reinterpret_cast<char*>(part) : reinterpret_cast<char*>(p.c);
-  const int64_t ld_out = part ? p.N : p.ldc;
-  const int out_dtype = part ? PK_F32 : p.c_dtype;
-  const float oscale = part ? 1.0f : p.scale;
+  // ---- epilogue: C, scaled, in the output dtype ----
+  char* const out_base = reinterpret_cast<char*>(p.c);
+  const int64_t ld_out = p.ldc;
+  const int out_dtype = p.c_dtype;
+  const float oscale = p.scale;
   const int esz = out_dtype == PK_F32 ? 4 : 2;
   const int em = lane & 15, en = 4 * (lane >> 4);
   if ((ld_out * esz) % 16 == 0 && (reinterpret_cast<uintptr_t>(out_base) & 15) == 0) {
@@ -306,8 +302,8 @@ __global__ __launch_bounds__(512) void gemm_w4_wide_kernel(W4WideParams p) {
   });
 }
 
-bool w4_wide_ok(int M, int N, int K, int k_slice, int group, bool has_gs, int64_t lda, int64_t ldb) {
-  if (M < 256 || N < 256 || N % 8 || k_slice % 32 || K % k_slice) return false;
+bool w4_wide_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ldb) {
+  if (M < 256 || N < 256 || N % 8 || K % 32 || K < 32) return false;
   if (has_gs && group % 32) return false;
   // 32-bit buffer offsets
   if ((int64_t)M * lda * 2 >= (1ll << 31)) return false;
@@ -317,7 +313,7 @@ bool w4_wide_ok(int M, int N, int K, int k_slice, int group, bool has_gs, int64_
 
 int w4_wide_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
                    int group, float scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
-                   int split, void* workspace, hipStream_t s, bool partials_only) {
+                   hipStream_t s) {
   W4WideParams p;
   p.a = reinterpret_cast<const pk_half*>(a);
   p.lda = lda;
@@ -332,15 +328,12 @@ int w4_wide_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const
   p.M = M;
   p.N = N;
   p.K = K;
-  p.k_slice = K / split;
   p.tiles_m = (int)cdiv(M, 256);
   p.tiles_n = (int)cdiv(N, 256);
-  p.partials = split > 1 ? split_partials(workspace, partials_only) : nullptr;
-  const dim3 grid(p.tiles_m * p.tiles_n, split);
+  const dim3 grid(p.tiles_m * p.tiles_n);
   if (scales) gemm_w4_wide_kernel<true><<<grid, 512, 0, s>>>(p);
   else gemm_w4_wide_kernel<false><<<grid, 512, 0, s>>>(p);
   PK_LAUNCH_CHECK("w4a16 gemm (256 x 256)");
-  if (split > 1 && !partials_only) return splitk_reduce(p.partials, split, M, N, scale, c, c_dtype, ldc, s);
   return PK_OK;
 }
 

@@ -87,10 +87,10 @@ int v2_f8_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb,
                  hipStream_t s);
 
 // 256 x 256 W4A16 GEMM with a 4-stage LDS pipeline, 8 waves of 128 x 64 (gemm_w4_wide.hip).
-bool w4_wide_ok(int M, int N, int K, int k_slice, int group, bool has_gs, int64_t lda, int64_t ldb);
+bool w4_wide_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ldb);
 int w4_wide_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
                    int group, float scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
-                   int split, void* workspace, hipStream_t s, bool partials_only);
+                   hipStream_t s);
 
 // 256 x 256 fp8 GEMM with a 4-stage DMA pipeline and transposing LDS reads for (K, N) B
 // (gemm_f8_v3.hip).
