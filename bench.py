@@ -595,6 +595,31 @@ def vendor_compare(dev) -> dict:
     return {"vendor_compare": rows}
 
 
+def hbm_ceiling(dev) -> dict:
+    """What one launch that only reads achieves (pk_read_probe), timed like the GEMV: a graph of
+    back-to-back launches over rotating buffers (more than the 256 MB Infinity Cache). At the
+    GEMV's 23,279,104 bytes it is the ceiling the headline's fraction is read against; 256 MiB
+    and 1 GiB show the asymptotic rate."""
+    import torch
+
+    import _pk
+
+    rows = []
+    for nbytes, nrot, steps in ((23279104, N_ROTATE, 2000), (256 << 20, 4, 40), (1 << 30, 2, 20)):
+        bufs = [torch.empty(nbytes // 4, dtype=torch.int32, device=dev).fill_(i) for i in range(nrot)]
+        best = None
+        for grid in (256, 512, 768, 1024, 2048, 4096):
+            out = torch.empty(grid, dtype=torch.int32, device=dev)
+            ms = GraphTimer(lambda i: _pk.read_probe(bufs[i % nrot], out, grid), steps, 2).run(reps=3)
+            tbs = nbytes / (ms * 1e-3) / 1e12
+            if best is None or tbs > best["TB/s"]:
+                best = {"bytes": nbytes, "grid": grid, "us": round(ms * 1e3, 3), "TB/s": round(tbs, 3),
+                        "frac_of_8TBs": round(tbs / (HBM_PEAK_GBS / 1000), 4)}
+        rows.append(best)
+        del bufs
+    return {"hbm_read_ceiling": rows}
+
+
 def measured_traffic():
     """HBM bytes per slice-kernel launch from the committed --pmc summary, or None."""
     import re
@@ -621,6 +646,8 @@ def main() -> int:
                     help="only run eager GEMM calls for rocprofv3 --pmc MFMA utilisation")
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="only measure the matrix cores' sustained rate with no memory traffic")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="only measure what a read-only launch of the GEMV's bytes achieves")
     ap.add_argument("--vendor", action="store_true",
                     help="only time hipBLASLt's fp16 / fp8 GEMMs beside this library's")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -652,6 +679,9 @@ def main() -> int:
         return 0
     if args.vendor:
         print(json.dumps(vendor_compare(dev)), flush=True)
+        return 0
+    if args.hbm_ceiling:
+        print(json.dumps(hbm_ceiling(dev)), flush=True)
         return 0
     if args.only:
         fn = {"prefill": bench_prefill, "gemm4096": lambda d: bench_prefill(d, M=4096),

@@ -259,6 +259,11 @@ int pk_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int6
  * traffic in the loop; out receives grid * 512 floats. FLOPs per launch:
  * grid * 8 * iters * 8 * (fp8 ? 131072 : 32768). */
 int pk_mfma_probe(int fp8, int random, int grid, int iters, float* out, void* stream);
+/* pk_read_probe: no counterpart in the reference; for benchmarks that read the memory-bound
+ * kernels' fractions against what one launch reading the same bytes achieves. Reads `bytes`
+ * (a multiple of 16, 16-byte aligned) with `grid` workgroups of 256 threads, writes one
+ * 32-bit word per workgroup to out. */
+int pk_read_probe(const void* src, size_t bytes, uint32_t* out, int grid, void* stream);
 
 #ifdef __cplusplus
 }

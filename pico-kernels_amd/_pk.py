@@ -70,6 +70,7 @@ _SIGNATURES = {
     "pk_flash_decode": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
                                _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _sz, _vp]),
     "pk_mfma_probe": (_i32, [_i32, _i32, _i32, _i32, _vp, _vp]),
+    "pk_read_probe": (_i32, [_vp, _sz, _vp, _i32, _vp]),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
@@ -393,3 +394,11 @@ def mfma_probe(fp8: bool, random: bool, grid: int, iters: int, out: torch.Tensor
     assert out.dtype == torch.float32 and out.numel() >= grid * 512 and out.is_cuda
     _check(lib().pk_mfma_probe(int(fp8), int(random), int(grid), int(iters), out.data_ptr(),
                                stream_of(out)), "pk_mfma_probe")
+
+
+def read_probe(src: torch.Tensor, out: torch.Tensor, grid: int) -> None:
+    """Streaming read of ``src``'s bytes on the current stream (pk_read_probe); ``out`` holds
+    ``grid`` int32 words."""
+    assert out.dtype == torch.int32 and out.numel() >= grid and out.is_cuda and src.is_cuda
+    _check(lib().pk_read_probe(src.data_ptr(), src.numel() * src.element_size(), out.data_ptr(),
+                               int(grid), stream_of(src)), "pk_read_probe")

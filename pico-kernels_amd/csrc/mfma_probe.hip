@@ -1,8 +1,11 @@
-// Matrix-pipe ceiling probe: waves that issue only independent MFMAs (no memory traffic in
-// the loop), 8 waves per workgroup like the GEMMs, on register operands that are either
-// constant or pseudo-random. It measures what the matrix cores sustain on this GPU for the
-// data the GEMMs see, the ceiling their roofline fractions are read against. A measurement
-// entry point of this library; the reference has no counterpart.
+// Ceiling probes, measurement entry points of this library (the reference has no
+// counterpart):
+//  * MFMA: waves that issue only independent MFMAs (no memory traffic in the loop), 8 waves
+//    per workgroup like the GEMMs, on register operands that are either constant or
+//    pseudo-random -- what the matrix cores sustain for the data the GEMMs see.
+//  * HBM read: a streaming read of a buffer (16-byte non-temporal loads, XOR-reduced, one
+//    word written per workgroup) -- what one launch reading a given number of bytes achieves,
+//    the ceiling the memory-bound kernels' fractions are read against.
 #include "pk_internal.h"
 
 namespace pk {
@@ -55,9 +58,45 @@ __global__ __launch_bounds__(512) void mfma_probe_kernel(float* out, int iters) 
   out[(int64_t)blockIdx.x * 512 + t] = x;  // keeps the MFMAs live
 }
 
+// Grid-stride read of n16 16-byte words; each workgroup writes the XOR of what it read.
+__global__ __launch_bounds__(256) void hbm_read_probe_kernel(const pk_u4v* src, int64_t n16,
+                                                             uint32_t* out) {
+  uint32_t x = 0u;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {  // four loads in flight per thread
+    const pk_u4v a = __builtin_nontemporal_load(src + i);
+    const pk_u4v b = __builtin_nontemporal_load(src + i + stride);
+    const pk_u4v c = __builtin_nontemporal_load(src + i + 2 * stride);
+    const pk_u4v d = __builtin_nontemporal_load(src + i + 3 * stride);
+    x ^= a[0] ^ a[1] ^ a[2] ^ a[3] ^ b[0] ^ b[1] ^ b[2] ^ b[3] ^ c[0] ^ c[1] ^ c[2] ^ c[3] ^
+         d[0] ^ d[1] ^ d[2] ^ d[3];
+  }
+  for (; i < n16; i += stride) {
+    const pk_u4v a = __builtin_nontemporal_load(src + i);
+    x ^= a[0] ^ a[1] ^ a[2] ^ a[3];
+  }
+  __shared__ uint32_t red[4];
+  for (int o = 32; o > 0; o >>= 1) x ^= (uint32_t)__shfl_xor((int)x, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 }  // namespace pk
 
 using namespace pk;
+
+extern "C" int pk_read_probe(const void* src, size_t bytes, uint32_t* out, int grid, void* stream) {
+  PK_REQUIRE(src != nullptr && out != nullptr, "pk_read_probe: null pointer");
+  PK_REQUIRE(bytes >= 16 && bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0,
+             "pk_read_probe: bytes must be a positive multiple of 16 on a 16-byte aligned buffer");
+  PK_REQUIRE(grid >= 1, "pk_read_probe: grid must be positive");
+  hbm_read_probe_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(
+      reinterpret_cast<const pk_u4v*>(src), (int64_t)(bytes / 16), out);
+  PK_LAUNCH_CHECK("hbm read probe");
+  return PK_OK;
+}
 
 extern "C" int pk_mfma_probe(int fp8, int random, int grid, int iters, float* out, void* stream) {
   PK_REQUIRE(out != nullptr, "pk_mfma_probe: null output");
