@@ -1,0 +1,46 @@
+"""The measurement probes behind `bench.py --hbm-ceiling` and `--mfma-ceiling`: the read probe
+visits every word of the buffer exactly once (the XOR of its per-workgroup results equals the
+XOR of all words, for several grids and a ragged length), and the MFMA probe's constant-operand
+run gives the closed-form sum."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import _pk
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("grid", [1, 7, 256, 2048])
+@pytest.mark.parametrize("words", [4, 4 * 1000 + 4, 4 * 65536])
+def test_read_probe_reads_every_word_once(grid, words, cuda):
+    g = torch.Generator()
+    g.manual_seed(grid + words)
+    host = torch.randint(-2**31, 2**31 - 1, (words,), generator=g, dtype=torch.int64).to(torch.int32)
+    src = host.to(cuda)
+    out = torch.zeros(grid, dtype=torch.int32, device=cuda)
+    _pk.read_probe(src, out, grid)
+    got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+    want = np.bitwise_xor.reduce(host.numpy().view(np.uint32))
+    assert got == want
+
+
+def test_read_probe_rejects_bad_sizes(cuda):
+    src = torch.zeros(3, dtype=torch.int32, device=cuda)  # 12 bytes: not a multiple of 16
+    out = torch.zeros(4, dtype=torch.int32, device=cuda)
+    with pytest.raises(_pk.PicoKernelsError):
+        _pk.read_probe(src, out, 4)
+
+
+def test_mfma_probe_constant_operands(cuda):
+    """fp16: every product is 0.5 * 0.5 and each accumulator element sums 16 of them per MFMA,
+    so every lane's output is iters * 8 accumulators * 16 elements * 16 * 0.25."""
+    grid, iters = 4, 10
+    out = torch.zeros(grid * 512, dtype=torch.float32, device=cuda)
+    _pk.mfma_probe(False, False, grid, iters, out)
+    assert torch.all(out == iters * 8 * 16 * 16 * 0.25)
+    _pk.mfma_probe(True, True, grid, iters, out)  # random fp8 operands: finite sums
+    assert torch.isfinite(out).all()
