@@ -149,9 +149,12 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        old = 0
         if ws is not None:
             _retired_workspaces.append(ws)
-        size = max(nbytes, 1 << 20)
+            old = ws.numel()
+        # at least double: growing shapes retire O(log) buffers, at most ~2x the final size
+        size = max(nbytes, 1 << 20, 2 * old)
         ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
