@@ -178,7 +178,7 @@ def bench_gemv(args, dev) -> dict:
     }
 
 
-def bench_prefill(dev, iters: int = 20, M: int = 2048) -> dict:
+def bench_prefill(dev, iters: int = 50, M: int = 2048) -> dict:
     """W4A16 GEMM (group 128, fp16 out) at M x 4096 x 4096: M = 2048 is the prefill config,
     M = 4096 the 4096^3 shape the metric also names."""
     import torch
@@ -192,7 +192,7 @@ def bench_prefill(dev, iters: int = 20, M: int = 2048) -> dict:
     qw, sc = gemm_int4.quantize_int4_group(w, 128)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     ms = GraphTimer(lambda i: _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, out=out),
-                    iters, 2).run(reps=3)
+                    iters, 2).run(reps=5)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return {"workload": "w4a16_prefill_gemm" if M == 2048 else "w4a16_gemm_4096^3", "M": M, "K": K,
             "N": N, "ms": round(ms, 4),
@@ -202,7 +202,7 @@ def bench_prefill(dev, iters: int = 20, M: int = 2048) -> dict:
                          "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}}
 
 
-def bench_fp8(dev, iters: int = 20) -> dict:
+def bench_fp8(dev, iters: int = 50) -> dict:
     import torch
 
     import _pk
@@ -215,7 +215,7 @@ def bench_fp8(dev, iters: int = 20) -> dict:
     b8, sb = gemm_fp8.quantize(b)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     scale = 1.0 / (sa * sb)
-    ms = GraphTimer(lambda i: _pk.fp8_gemm(a8, b8, scale, torch.float16, out=out), iters, 2).run(reps=3)
+    ms = GraphTimer(lambda i: _pk.fp8_gemm(a8, b8, scale, torch.float16, out=out), iters, 2).run(reps=5)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     # accuracy of this very output vs fp32 (the reference's own metric)
     ref = a.float() @ b.float()
