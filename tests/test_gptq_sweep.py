@@ -120,3 +120,26 @@ def test_gptq_layer_loss_matches_sequential_oracle(group, cuda):
     assert abs(loss(ours) / loss(ref) - 1) < 5e-3, (loss(ours), loss(ref))
     assert loss(ours) < 0.9 * loss(rtn)
     assert torch.isclose(ours, ref, atol=1e-4, rtol=1e-3).float().mean() > 0.9
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 100, 128, 129, 300, 1000])
+def test_blocked_cholesky_matches_one_call(n, cuda):
+    """gptq_layer's blocked factorisation equals torch.linalg.cholesky to fp32 rounding and
+    reports a matrix that is not positive definite."""
+    import quantize
+
+    g = torch.Generator()
+    g.manual_seed(n)
+    x = torch.randn(max(n // 2, 4), n, generator=g)
+    h = (x.t() @ x) / x.shape[0]
+    h.diagonal().add_(0.01 * torch.diagonal(h).mean())
+    h = h.to(cuda)
+    L, ok = quantize._blocked_cholesky(h)
+    assert ok
+    ref = torch.linalg.cholesky(h.double())
+    assert ((L.double() - ref).norm() / ref.norm()).item() < 1e-5
+    assert torch.equal(L, torch.tril(L))
+    bad = h.clone()
+    bad[n - 1, n - 1] = -1.0
+    assert not quantize._blocked_cholesky(bad)[1]
