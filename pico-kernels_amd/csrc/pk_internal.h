@@ -47,11 +47,13 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
                 bool partials_only = false);
 
 // W4A16 for kSkinnyMinM <= M <= kSkinnyMaxM (w4a16_skinny.hip): weights to registers, MFMA
-// per 16 activation rows, 4-wave LDS reduction, split-K partials.
+// per 16 activation rows, LDS reduction over the workgroup's waves, split-K partials.
 constexpr int kSkinnyMinM = 5;
-constexpr int kSkinnyMaxM = 32;
+constexpr int kSkinnyMaxM = 128;
 struct SkinnyPlan {
-  int mb;  // 16-row activation blocks (1 or 2)
+  int mb;         // 16-row activation blocks per workgroup (1, 2 or 4)
+  int cpl, nw;    // columns per lane (16 or 8), waves per workgroup (4 or 8)
+  int row_parts;  // workgroups along M per (column tile, slice)
   int split, k_slice, tiles;
 };
 bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out);

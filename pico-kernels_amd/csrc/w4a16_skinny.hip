@@ -1,21 +1,24 @@
-// W4A16 matmul for 5 <= M <= 32 activation rows: the HBM-bound middle between the GEMV
+// W4A16 matmul for 5 <= M <= 128 activation rows: the HBM-bound middle between the GEMV
 // (M <= 4) and the LDS-tiled GEMM. C = tensor_scale * A (M, K) fp16 @ deq(W) (K, N), with W in
 // the packed layout of gemm_int4.pack_int4_n (gemm_int4.py:65-72) viewed as int32 words
 // (word j of row k = columns 8j..8j+7, nibble i = column 8j+i) and the group scales of
 // quantize.rtn_layer along K (quantize.py:63-68).
 //
-// Work decomposition: grid.x = column tiles of 256 columns (128 bytes of every row),
-// grid.y = split-K slices of k_slice rows (contiguous, as gemm_splitk.py:49-53). The 4 waves
-// of a workgroup take consecutive quarters of the slice; a wave walks its rows in k-steps of
-// 32 with several k-steps of loads in flight (no LDS staging: weights go straight to
-// registers).
+// Work decomposition: grid.x = column tiles (x row parts), grid.y = split-K slices of k_slice
+// rows (contiguous, as gemm_splitk.py:49-53). The NW waves of a workgroup (4 or 8) take
+// consecutive 1/NW parts of the slice; a wave walks its rows in k-steps of 32 with several
+// k-steps of loads in flight (no LDS staging: weights go straight to registers). A workgroup
+// covers MB 16-row activation blocks (1, 2 or 4); above 64 rows two row parts share each
+// (tile, slice), their workgroups placed on one XCD so the second reads the weights from L2.
 //
-// Per k-step a lane (j = lane % 16, g = lane / 16) loads 8 bytes (16 columns 16j..16j+15) of
-// the 8 rows 8g..8g+7, plus 16 bytes of activations (row j of a 16-row block, the same 8 k).
-// That is exactly the operand layout of v_mfma_f32_16x16x32_f16: lane L supplies A[L%16][8g+d]
-// and B[8g+d][L%16] for d = 0..7, so MFMA number c (c = 0..15) multiplies the activations by
-// weight column 16j + c of lane j, and the 16 x 16 result lands in lane L as rows 4g..4g+3 of
-// column 16j + c. No data crosses lanes.
+// Per k-step a lane (j = lane % 16, g = lane / 16) loads CPL / 2 bytes (CPL = 16 or 8
+// columns: CPL*j .. CPL*j + CPL-1 of the tile) of the 8 rows 8g..8g+7, plus 16 bytes of
+// activations per block (row j of the block, the same 8 k). That is exactly the operand layout
+// of v_mfma_f32_16x16x32_f16: lane L supplies A[L%16][8g+d] and B[8g+d][L%16] for d = 0..7, so
+// MFMA number c (c = 0..CPL-1) multiplies the activations by weight column CPL*j + c of lane j,
+// and the 16 x 16 result lands in lane L as rows 4g..4g+3 of that column. No data crosses
+// lanes. Tiles are 16 * CPL columns: 256 (one 128-byte line per row) or 128 (half the
+// accumulators, so four blocks fit in registers).
 //
 // Dequantisation without a conversion per nibble (the arithmetic of the M <= 4 GEMV): XOR
 // 0x88888888 turns each signed nibble v into u = v + 8; a byte permute gathers one byte of rows
@@ -28,18 +31,21 @@
 // A wave's rows lie in one quantisation group, so its fp32 result is scaled once per column
 // at the end (exact powers of two folded into the scale).
 //
-// Reduction: the 4 waves' tiles are added in LDS in a fixed order, ((w2 + w0) + (w3 + w1));
-// with split-K every slice writes (split, M, N) fp32 partials and splitk_reduce_kernel adds
-// them in slice order, so results are bitwise reproducible. (Adding the slices through one
-// XCD's L2 inside this kernel, as the M <= 4 GEMV does, was measured slower here for every
-// split: the last workgroup of a tile has M * split partials per thread to gather.)
+// Reduction: the waves' tiles are added in LDS in a fixed order; with split-K every slice
+// writes (split, M, N) fp32 partials and splitk_reduce_kernel adds them in slice order, so
+// results are bitwise reproducible, and equal for both tile widths at one wave count.
+// (Adding the slices through one XCD's L2 inside this kernel, as the M <= 4 GEMV does, was
+// measured slower here for every split: the last workgroup of a tile has M * split partials
+// per thread to gather.)
+#include <cstdio>
+#include <cstdlib>
+
 #include "pk_internal.h"
 
 namespace pk {
 
-constexpr int kSkTileCols = 256;  // columns per workgroup tile (16 lanes x 16 columns)
-constexpr int kSkStep = 32;       // rows per k-step (4 lane groups x 8 rows)
-constexpr int kSkPad = 4;         // LDS row padding (floats)
+constexpr int kSkStep = 32;  // rows per k-step (4 lane groups x 8 rows)
+constexpr int kSkPad = 4;    // LDS row padding (floats)
 
 struct SkinnyParams {
   const pk_half* a;
@@ -54,25 +60,38 @@ struct SkinnyParams {
   int64_t ldc;
   int M, N, K;
   int split, k_slice;
+  int tiles, row_parts;
   float* partials;  // (split, M, N) fp32 when split > 1
 };
 
-template <int MB>
+template <int MB, int WPL>
 struct SkStep {
-  pk_u2v w[8];   // rows 8g..8g+7, words 2j', 2j'+1 of the tile
-  pk_u4v x[MB];  // activations: row j of each 16-row block, k = 8g..8g+7
+  uint32_t w[8][WPL];  // rows 8g..8g+7, the lane's WPL words of the tile
+  pk_u4v x[MB];        // activations: row j of each 16-row block, k = 8g..8g+7
 };
 
-template <int MB, bool HAS_GS, int PD, int OCC>
-__global__ __launch_bounds__(256, OCC) void w4a16_skinny_kernel(SkinnyParams p) {
+// MB: 16-row activation blocks per workgroup; CPL: columns per lane (16: 8-byte weight loads,
+// 256-column tiles; 8: 4-byte loads, 128-column tiles, half the accumulators per block);
+// NW: waves per workgroup, each taking 1/NW of the slice's rows.
+template <int MB, int CPL, int NW, bool HAS_GS, int PD, int OCC>
+__global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams p) {
+  constexpr int TC = 16 * CPL;  // tile columns
+  constexpr int WPL = CPL / 8;  // words per lane and row
+  constexpr int NB = NW / 2;    // LDS reduction buffers
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int j = lane & 15, g = lane >> 4;
-  const int tile = blockIdx.x, slice = blockIdx.y;
+  // Row parts of one (tile, slice) are blocks b and b + 8: the same XCD, dispatched close
+  // together, so the second part's weight reads hit that XCD's L2.
+  const int bx = blockIdx.x, slice = blockIdx.y;
+  const int part = (bx >> 3) % p.row_parts;
+  const int tile = (bx / (8 * p.row_parts)) * 8 + (bx & 7);
+  if (tile >= p.tiles) return;
+  const int m0 = part * MB * 16;
   const int words_total = p.N >> 3;
   // The ragged last tile re-reads in-bounds words; those columns are never stored.
-  const int word0 = min(tile * (kSkTileCols / 8) + 2 * j, words_total - 2);
-  const int rows_w = p.k_slice >> 2;
+  const int word0 = min(tile * (TC / 8) + WPL * j, words_total - WPL);
+  const int rows_w = p.k_slice / NW;
   const int nsteps = rows_w / kSkStep;
   const int kb = slice * p.k_slice + wave * rows_w;
 
@@ -85,35 +104,47 @@ __global__ __launch_bounds__(256, OCC) void w4a16_skinny_kernel(SkinnyParams p) 
   const int q_voff = 8 * g * ldq4 + word0 * 4;
   int a_voff[MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) a_voff[mb] = (int)(min(mb * 16 + j, p.M - 1) * p.lda + 8 * g) * 2;
-  // The wave's rows lie in group kb / group: its 16 column scales, requested first.
-  pk_u4v sraw[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  for (int mb = 0; mb < MB; ++mb)
+    a_voff[mb] = (int)(min(m0 + mb * 16 + j, p.M - 1) * p.lda + 8 * g) * 2;
+  // The wave's rows lie in group kb / group: its CPL column scales, requested first.
+  pk_u4v sraw[WPL];
+#pragma unroll
+  for (int i = 0; i < WPL; ++i) sraw[i] = pk_u4v{0u, 0u, 0u, 0u};
   if constexpr (HAS_GS) {
     const int srow = (kb / p.group) * p.N * 2;
-    sraw[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16, srow, 0);
-    sraw[1] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16 + 16, srow, 0);
+#pragma unroll
+    for (int i = 0; i < WPL; ++i)
+      sraw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16 + 16 * i, srow, 0);
   }
 
-  auto load = [&](SkStep<MB>& b, int s) {
+  auto load = [&](SkStep<MB, WPL>& b, int s) {
     const int k0 = kb + s * kSkStep;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) b.w[d] = __builtin_amdgcn_raw_buffer_load_b64(rq, q_voff, (k0 + d) * ldq4, 0);
+    for (int d = 0; d < 8; ++d) {
+      if constexpr (WPL == 2) {
+        const pk_u2v v = __builtin_amdgcn_raw_buffer_load_b64(rq, q_voff, (k0 + d) * ldq4, 0);
+        b.w[d][0] = v[0];
+        b.w[d][1] = v[1];
+      } else {
+        b.w[d][0] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_voff, (k0 + d) * ldq4, 0);
+      }
+    }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) b.x[mb] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[mb], k0 * 2, 0);
   };
 
-  // accL / accR: byte b (columns 16j + 2b, 16j + 2b + 1) masked low nibble / both nibbles
-  pk_f4 accL[MB][8], accR[MB][8], off[MB];
+  // accL / accR: byte b (columns 2b, 2b + 1 of the lane) masked low nibble / both nibbles
+  pk_f4 accL[MB][CPL / 2], accR[MB][CPL / 2], off[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     off[mb] = pk_f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int b = 0; b < 8; ++b) accL[mb][b] = accR[mb][b] = off[mb];
+    for (int b = 0; b < CPL / 2; ++b) accL[mb][b] = accR[mb][b] = off[mb];
   }
   const pk_u4v eight_u = {0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u};
   const pk_half8 eight = __builtin_bit_cast(pk_half8, eight_u);
 
-  auto compute = [&](const SkStep<MB>& b) {
+  auto compute = [&](const SkStep<MB, WPL>& b) {
     pk_half8 xa[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -121,13 +152,10 @@ __global__ __launch_bounds__(256, OCC) void w4a16_skinny_kernel(SkinnyParams p) 
       off[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mb], eight, off[mb], 0, 0, 0);
     }
 #pragma unroll
-    for (int wi = 0; wi < 2; ++wi) {
+    for (int wi = 0; wi < WPL; ++wi) {
       uint32_t wx[8];
 #pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        const pk_u2v wd = b.w[d];
-        wx[d] = wd[wi] ^ 0x88888888u;
-      }
+      for (int d = 0; d < 8; ++d) wx[d] = b.w[d][wi] ^ 0x88888888u;
 #pragma unroll
       for (int bb = 0; bb < 4; ++bb) {
         const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + bb) << 16) | (uint32_t)bb;
@@ -148,7 +176,7 @@ __global__ __launch_bounds__(256, OCC) void w4a16_skinny_kernel(SkinnyParams p) 
   };
 
   // ---- k-steps: a ring of PD buffers, each refilled PD steps ahead -----------------------
-  SkStep<MB> ring[PD];
+  SkStep<MB, WPL> ring[PD];
 #pragma unroll
   for (int i = 0; i < PD; ++i)
     if (i < nsteps) load(ring[i], i);
@@ -165,12 +193,12 @@ __global__ __launch_bounds__(256, OCC) void w4a16_skinny_kernel(SkinnyParams p) 
   mfma_drain();
 
   // ---- per column: remove the +8 offset, apply 2^24 / 2^20 and the group scale ------------
-  // acc[mb][c] holds rows mb*16 + 4g + r of column 16j + c.
-  pk_f4 acc[MB][16];
+  // acc[mb][c] holds rows m0 + mb*16 + 4g + r of the lane's column c.
+  pk_f4 acc[MB][CPL];
   {
-    float sc[16];
+    float sc[CPL];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
+    for (int c = 0; c < CPL; ++c) {
       float sv = 1.0f;
       if constexpr (HAS_GS) {
         const uint32_t word = sraw[c >> 3][(c & 7) >> 1];
@@ -181,82 +209,132 @@ __global__ __launch_bounds__(256, OCC) void w4a16_skinny_kernel(SkinnyParams p) 
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int by = 0; by < 8; ++by) {
+      for (int by = 0; by < CPL / 2; ++by) {
         acc[mb][2 * by] = (accL[mb][by] - off[mb]) * sc[2 * by];
         acc[mb][2 * by + 1] = (accR[mb][by] - accL[mb][by] - off[mb] * 16.0f) * sc[2 * by + 1];
       }
   }
 
-  // ---- add the 4 waves' tiles in LDS: ((w2 + w0) + (w3 + w1)) ---------------------------
-  __shared__ float red[2][MB * 16][kSkTileCols + kSkPad];
-  if (wave >= 2) {
+  // ---- add the waves' tiles in LDS: waves NB.. store, waves 0..NB-1 add their own, and the
+  // buffers are summed in a fixed order: 4 waves ((w2 + w0) + (w3 + w1)); 8 waves
+  // ((w4 + w0) + (w6 + w2)) + ((w5 + w1) + (w7 + w3)) ----------------------------------
+  __shared__ float red[NB][MB * 16][TC + kSkPad];
+  auto tile_vec = [&](int mb, int r, int c4) {
+    return pk_f4{acc[mb][4 * c4][r], acc[mb][4 * c4 + 1][r], acc[mb][4 * c4 + 2][r],
+                 acc[mb][4 * c4 + 3][r]};
+  };
+  if (wave >= NB) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) {
-          const pk_f4 v = {acc[mb][4 * c4][r], acc[mb][4 * c4 + 1][r], acc[mb][4 * c4 + 2][r],
-                           acc[mb][4 * c4 + 3][r]};
-          *reinterpret_cast<pk_f4*>(&red[wave - 2][mb * 16 + 4 * g + r][16 * j + 4 * c4]) = v;
-        }
+        for (int c4 = 0; c4 < CPL / 4; ++c4)
+          *reinterpret_cast<pk_f4*>(&red[wave - NB][mb * 16 + 4 * g + r][CPL * j + 4 * c4]) =
+              tile_vec(mb, r, c4);
   }
   __syncthreads();
-  if (wave < 2) {
+  if (wave < NB) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) {
-          pk_f4* q = reinterpret_cast<pk_f4*>(&red[wave][mb * 16 + 4 * g + r][16 * j + 4 * c4]);
-          const pk_f4 v = {acc[mb][4 * c4][r], acc[mb][4 * c4 + 1][r], acc[mb][4 * c4 + 2][r],
-                           acc[mb][4 * c4 + 3][r]};
-          *q = *q + v;
+        for (int c4 = 0; c4 < CPL / 4; ++c4) {
+          pk_f4* q = reinterpret_cast<pk_f4*>(&red[wave][mb * 16 + 4 * g + r][CPL * j + 4 * c4]);
+          *q = *q + tile_vec(mb, r, c4);
         }
   }
   __syncthreads();
-  const int col = tile * kSkTileCols + t;
-  if (col < p.N) {
-    for (int m = 0; m < p.M; ++m) {
-      const float v = red[0][m][t] + red[1][m][t];
-      if (p.split == 1)
-        store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + col, v * p.tensor_scale);
-      else
-        p.partials[((int64_t)slice * p.M + m) * p.N + col] = v;
-    }
+  const int rows = min(MB * 16, p.M - m0);
+  for (int idx = t; idx < rows * TC; idx += 64 * NW) {
+    const int m = idx / TC, cl = idx % TC;
+    const int col = tile * TC + cl;
+    if (col >= p.N) continue;
+    float v;
+    if constexpr (NB == 2) v = red[0][m][cl] + red[1][m][cl];
+    else v = (red[0][m][cl] + red[2][m][cl]) + (red[1][m][cl] + red[3][m][cl]);
+    if (p.split == 1)
+      store_from_f32(p.c, p.c_dtype, (int64_t)(m0 + m) * p.ldc + col, v * p.tensor_scale);
+    else
+      p.partials[((int64_t)slice * p.M + m0 + m) * p.N + col] = v;
   }
 }
 
 // ---------------------------------------------------------------------------------------
 // Planning and launch.
 // ---------------------------------------------------------------------------------------
-bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out) {
-  if (M < kSkinnyMinM || M > kSkinnyMaxM || N % 16 || K % 128) return false;
-  // A wave takes k_slice / 4 rows, a multiple of the 32-row k-step lying in one group.
+// Waves the automatic plan aims for: the fewest slices whose workgroups reach this many waves
+// (about 1.5 per SIMD) won on every Llama-3-8B layer at M = 8..64 (MI355X): fewer waves
+// leave HBM requests short, more slices add fp32 partials.
+constexpr int kSkWaveTarget = 1536;
+
+// The plan for nw waves per workgroup, cpl_fixed columns per lane (0: chosen here).
+static bool skinny_plan_nw(int M, int N, int K, int group, bool has_gs, int split_req, int nw,
+                           int cpl_fixed, SkinnyPlan* out) {
+  // A wave takes k_slice / nw rows, a multiple of the 32-row k-step lying in one group.
   auto ok = [&](int s) {
-    if (s < 1 || K % s || (K / s) % 128) return false;
-    const int rows_w = K / s / 4;
+    if (s < 1 || K % s || (K / s) % (nw * kSkStep)) return false;
+    const int rows_w = K / s / nw;
     return !has_gs || group % rows_w == 0;
   };
-  int split = 0;
+  // 16 columns per lane (256-column tiles) hold at most two 16-row blocks; 8 columns per lane
+  // (128-column tiles) up to four, with two row parts above 64 rows.
+  const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  const int rp = (int)cdiv(M, mb * 16);
+  auto waves = [&](int cpl, int s) {
+    return (int64_t)cdiv(N, 16 * cpl) * rp * s * nw;
+  };
+  auto pick = [&](int cpl) {  // fewest slices reaching the wave target, else the most
+    int last = 0;
+    for (int s = 1; s <= K / (nw * kSkStep); ++s)
+      if (ok(s)) {
+        last = s;
+        if (waves(cpl, s) >= kSkWaveTarget) return s;
+      }
+    return last;
+  };
+  int cpl = 8, split = 0;
   if (split_req > 0) {
     if (!ok(split_req)) return false;
     split = split_req;
+    if (cpl_fixed) cpl = cpl_fixed;
+    else if (M <= 32 && waves(16, split) >= kSkWaveTarget) cpl = 16;
+  } else if (cpl_fixed) {
+    cpl = cpl_fixed;
+    split = pick(cpl);
   } else {
-    // fp32 partials cost 8*S*M*N bytes of traffic against K*N/2 of weights: 8 slices
-    // (measured fastest on MI355X for M = 8..32 against 16 and 32 on the Llama-3-8B shapes), or
-    // the nearest count that satisfies the group constraint (more slices first, since short
-    // slices are what long K needs).
-    const int base = 8;
-    for (int s = base; s <= K / 128 && !split; ++s)
-      if (ok(s)) split = s;
-    for (int s = min(base - 1, K / 128); s >= 1 && !split; --s)
-      if (ok(s)) split = s;
-    if (!split) return false;
+    // 256-column tiles when they reach the wave target without extra slices
+    int first = 0;
+    for (int s = 1; s <= K / (nw * kSkStep) && !first; ++s)
+      if (ok(s)) first = s;
+    if (first && M <= 32 && waves(16, first) >= kSkWaveTarget) {
+      cpl = 16;
+      split = first;
+    } else {
+      split = pick(8);
+    }
   }
-  *out = {M <= 16 ? 1 : 2, split, K / split, (int)cdiv(N, kSkTileCols)};
+  if (!split) return false;
+  *out = {mb, cpl, nw, rp, split, K / split, (int)cdiv(N, 16 * cpl)};
   return true;
+}
+
+bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out) {
+  if (M < kSkinnyMinM || M > kSkinnyMaxM || N % 16 || K % 128) return false;
+  // Above 64 rows every weight is read by two row parts; that beat the LDS-tiled GEMM only
+  // on layers of at most 4096 x 4096 weights (measured at M = 96 and 128).
+  if (M > 64 && (int64_t)K * N > 4096ll * 4096) return false;
+  // PK_SKINNY_CFG="cpl,nw" fixes columns per lane and waves per workgroup (read per plan).
+  if (const char* e = getenv("PK_SKINNY_CFG")) {
+    int c = 0, w = 0;
+    if (sscanf(e, "%d,%d", &c, &w) == 2 && (c == 8 || c == 16) && (w == 4 || w == 8))
+      return skinny_plan_nw(M, N, K, group, has_gs, split_req, w, M > 32 ? 8 : c, out);
+  }
+  // 8 waves (half the slices for the same waves in flight); 4 where slices of 8 k-steps do
+  // not fit K, the group or the requested split.
+  return skinny_plan_nw(M, N, K, group, has_gs, split_req, 8, 0, out) ||
+         skinny_plan_nw(M, N, K, group, has_gs, split_req, 4, 0, out);
 }
 
 // Buffer offsets are 32-bit: weights, scales and activations must each stay below 2 GiB.
@@ -265,12 +343,34 @@ bool skinny_fits(int M, int N, int K, int64_t lda, int64_t ldq, int group, bool 
          (!has_gs || (int64_t)(K / group) * N * 2 < (1ll << 31));
 }
 
-template <int MB, bool GS>
-static void launch_skinny_t(const SkinnyParams& p, int tiles, hipStream_t s) {
-  // k-steps in flight per wave, measured on the Llama-3-8B shapes: 3 for one 16-row block
-  // (162 VGPRs, three waves per SIMD; 2-3% faster than 4 at two waves), 2 for two blocks.
-  constexpr int PD = MB == 1 ? 3 : 2;
-  w4a16_skinny_kernel<MB, GS, PD, 2><<<dim3(tiles, p.split), 256, 0, s>>>(p);
+template <int MB, int CPL, int NW, bool GS>
+static void launch_skinny_t(const SkinnyParams& p, hipStream_t s) {
+  // k-steps in flight per wave, measured on the Llama-3-8B shapes: 3 for one 16-row block of
+  // 16 columns per lane (162 VGPRs, three waves per SIMD; 2-3% faster than 4 at two waves),
+  // 2 for two blocks; 8 columns per lane halve the weight registers.
+  constexpr int PD = CPL == 16 ? (MB == 1 ? 3 : 2) : (MB == 1 ? 4 : MB == 2 ? 3 : 2);
+  constexpr int OCC = NW == 4 ? 2 : 1;
+  const unsigned gx = p.row_parts == 1 ? (unsigned)p.tiles
+                                       : (unsigned)(cdiv(p.tiles, 8) * 8 * p.row_parts);
+  w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC><<<dim3(gx, p.split), 64 * NW, 0, s>>>(p);
+}
+
+template <int MB, int CPL, bool GS>
+static void launch_skinny_nw(const SkinnyParams& p, int nw, hipStream_t s) {
+  if (nw == 8) launch_skinny_t<MB, CPL, 8, GS>(p, s);
+  else launch_skinny_t<MB, CPL, 4, GS>(p, s);
+}
+
+template <bool GS>
+static void launch_skinny_cfg(const SkinnyPlan& pl, const SkinnyParams& p, hipStream_t s) {
+  if (pl.cpl == 16) {
+    if (pl.mb == 1) launch_skinny_nw<1, 16, GS>(p, pl.nw, s);
+    else launch_skinny_nw<2, 16, GS>(p, pl.nw, s);
+  } else {
+    if (pl.mb == 1) launch_skinny_nw<1, 8, GS>(p, pl.nw, s);
+    else if (pl.mb == 2) launch_skinny_nw<2, 8, GS>(p, pl.nw, s);
+    else launch_skinny_nw<4, 8, GS>(p, pl.nw, s);
+  }
 }
 
 int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
@@ -293,15 +393,11 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
   p.K = K;
   p.split = pl.split;
   p.k_slice = pl.k_slice;
+  p.tiles = pl.tiles;
+  p.row_parts = pl.row_parts;
   p.partials = pl.split > 1 ? split_partials(workspace, partials_only) : nullptr;
-  const bool gs = scales != nullptr;
-  if (pl.mb == 1) {
-    if (gs) launch_skinny_t<1, true>(p, pl.tiles, s);
-    else launch_skinny_t<1, false>(p, pl.tiles, s);
-  } else {
-    if (gs) launch_skinny_t<2, true>(p, pl.tiles, s);
-    else launch_skinny_t<2, false>(p, pl.tiles, s);
-  }
+  if (scales) launch_skinny_cfg<true>(pl, p, s);
+  else launch_skinny_cfg<false>(pl, p, s);
   PK_LAUNCH_CHECK("w4a16 skinny");
   if (pl.split > 1 && !partials_only)
     return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);

@@ -48,9 +48,10 @@ def test_w4a16_plans():
         assert _pk.w4a16_plan(1, 11008, 4096, 128, s) == (_pk.KERNEL_GEMV, s)
     # prefill: MFMA GEMM, no split needed at 2048 rows
     assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (_pk.KERNEL_GEMM, 1)
-    assert _pk.w4a16_plan(128, 4096, 4096, 128, 0)[0] == _pk.KERNEL_GEMM
+    assert _pk.w4a16_plan(128, 6144, 4096, 128, 0)[0] == _pk.KERNEL_GEMM
     # per-tensor mode (group_size 0) for the drop-in int4_gemm
-    assert _pk.w4a16_plan(128, 512, 256, 0, 0)[0] == _pk.KERNEL_GEMM
+    assert _pk.w4a16_plan(256, 512, 256, 0, 0)[0] == _pk.KERNEL_GEMM
+    assert _pk.w4a16_plan(128, 512, 256, 0, 0)[0] == _pk.KERNEL_SKINNY
     # slices may cut a group (scales are applied per 16-row chunk) ...
     assert _pk.w4a16_plan(1, 4096, 4096, 128, 64) == (_pk.KERNEL_GEMV, 64)
     # ... but a split must divide K into multiples of the row chunk
@@ -69,21 +70,28 @@ def test_w4a16_plans_by_row_count():
     assert _pk.w4a16_plan(4, 4096, 4096, 128, 0) == (G, 16)
     assert _pk.w4a16_plan(1, 4096, 14336, 128, 0) == (G, 28)
     assert _pk.w4a16_plan(1, 4096, 14336, 128, 56) == (G, 56)
-    # 5 <= M <= 32: register-dequant kernel, 8 slices (wave rows = 128, one group); for
-    # K = 14336 the nearest count whose wave rows divide the group: 28
-    for M in (5, 8, 16, 17, 32):
-        assert _pk.w4a16_plan(M, 6144, 4096, 128, 0) == (S, 8)
-    assert _pk.w4a16_plan(8, 4096, 14336, 128, 0) == (S, 28)
-    # short K: 384 rows -> 3 slices of one 32-row k-step per wave
+    # 5 <= M <= 64: register-dequant kernel, 8 waves per workgroup (wave rows of at most one
+    # group: slices of at most 1024 rows), the fewest slices reaching 1536 waves: 256-column
+    # tiles where they reach it without extra slices, else 128-column tiles
+    for M in (5, 8, 16, 17, 32, 33, 64):
+        assert _pk.w4a16_plan(M, 6144, 4096, 128, 0) == (S, 4)       # 48 tiles x 4 x 8 waves
+    assert _pk.w4a16_plan(8, 4096, 4096, 128, 0) == (S, 8)           # 32 tiles x 8 x 8
+    assert _pk.w4a16_plan(8, 4096, 14336, 128, 0) == (S, 14)         # 16 wide tiles x 14 x 8
+    assert _pk.w4a16_plan(48, 4096, 14336, 128, 0) == (S, 14)
+    # short K: 384 rows fit no 8-wave slice -> 4 waves, 3 slices of one 32-row k-step each
     assert _pk.w4a16_plan(8, 528, 384, 128, 0) == (S, 3)
     # explicit splits whose wave rows exceed a group go to the GEMM
-    assert _pk.w4a16_plan(8, 1024, 2048, 128, 2)[0] == C
+    assert _pk.w4a16_plan(8, 1024, 2048, 128, 1)[0] == C
+    assert _pk.w4a16_plan(8, 1024, 2048, 128, 2) == (S, 2)
     # ineligible shapes (N % 16, K % 128) stay on the GEMM
     assert _pk.w4a16_plan(8, 520, 1024, 32, 0)[0] == C
     assert _pk.w4a16_plan(8, 512, 1056, 32, 0)[0] == C
-    # M = 33..128: LDS-tiled GEMM; large tiles take the most slices that fit 256 workgroups
+    # M = 65..128: two row parts of the register-dequant kernel on layers of at most
+    # 4096 x 4096 weights; otherwise the LDS-tiled GEMM, whose large tiles take the most slices
+    # that fit 256 workgroups
+    assert _pk.w4a16_plan(128, 4096, 4096, 128, 0) == (S, 4)     # 32 tiles x 2 parts x 4
+    assert _pk.w4a16_plan(96, 4096, 4096, 128, 0) == (S, 4)
     assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (C, 4)     # 48 tiles x 4
-    assert _pk.w4a16_plan(128, 4096, 4096, 128, 0) == (C, 8)     # 32 tiles x 8
     assert _pk.w4a16_plan(128, 14336, 4096, 128, 0) == (C, 2)    # 112 tiles x 2
     assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (C, 8)
     assert _pk.w4a16_plan(256, 6144, 4096, 128, 0) == (C, 4)
@@ -99,7 +107,7 @@ def test_workspace_sizes():
     assert lib.pk_w4a16_workspace_bytes(1, 11008, 4096, 128, 16) == counters + 16 * 11008 * 4
     # N = 11000: 43 column tiles of 256, partial rows padded to 11008
     assert lib.pk_w4a16_workspace_bytes(1, 11000, 4096, 128, 16) == counters + 16 * 11008 * 4
-    assert lib.pk_w4a16_workspace_bytes(8, 6144, 4096, 128, 0) == counters + 8 * 8 * 6144 * 4
+    assert lib.pk_w4a16_workspace_bytes(8, 6144, 4096, 128, 0) == counters + 4 * 8 * 6144 * 4
     assert lib.pk_gemm_f16_workspace_bytes(512, 512, 1024, 4) == counters + 4 * 512 * 512 * 4
 
 

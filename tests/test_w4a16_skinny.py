@@ -1,8 +1,9 @@
-"""W4A16 for 5 <= M <= 32 rows (the register-dequant MFMA kernel between the GEMV and the
+"""W4A16 for 5 <= M <= 128 rows (the register-dequant MFMA kernel between the GEMV and the
 LDS-tiled GEMM): parity with dequantize + fp32 matmul on CPU-seeded inputs, every path the
-kernel has (one or two 16-row activation blocks, group scales or one tensor scale, ragged
-column tiles, k-step counts per wave that are not a multiple of the prefetch depth, split-K
-partials and their ordered reduction)."""
+kernel has (one, two or four 16-row activation blocks, one or two row parts, 16 or 8 columns
+per lane, 4 or 8 waves per workgroup, group scales or one tensor scale, ragged column tiles,
+k-step counts per wave that are not a multiple of the prefetch depth, split-K partials and
+their ordered reduction)."""
 
 from __future__ import annotations
 
@@ -36,8 +37,8 @@ def _case(M, K, N, seed, cuda, G=128):
 @pytest.mark.parametrize("M", [5, 8, 16, 17, 24, 32])
 @pytest.mark.parametrize("K,N", [(4096, 4096), (384, 528), (1152, 784), (640, 16)])
 def test_skinny_group128(M, K, N, cuda):
-    """N = 528 / 784 / 16 leave a ragged last 256-column tile; K = 384 / 640 / 1152 need 3, 5
-    and 9 slices (one 32-row k-step per wave), K = 4096 four k-steps per wave."""
+    """N = 528 / 784 / 16 leave a ragged last column tile; K = 384 / 640 / 1152 need 3, 5 and
+    9 slices of 4 waves (one 32-row k-step per wave), K = 4096 four k-steps per wave."""
     assert _pk.w4a16_plan(M, N, K, 128, 0)[0] == _pk.KERNEL_SKINNY
     a, qw, sc, codes, s16 = _case(M, K, N, 10 * M + K % 97 + N % 89, cuda)
     out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, 128, out_dtype=torch.float32)
@@ -56,13 +57,14 @@ def test_skinny_group_sizes(G, cuda):
 
 @pytest.mark.parametrize("M", [8, 32])
 def test_skinny_split_k_deterministic(M, cuda):
-    """Every explicit split whose wave rows (K / split / 4) fit in one group is bitwise
-    reproducible, and splits agree up to fp32 reassociation; other splits go to the GEMM."""
+    """Every explicit split whose wave rows (K / split / waves) fit in one group is bitwise
+    reproducible, and splits agree up to fp32 reassociation; other splits go to the GEMM.
+    Splits 4 and 8 run 8 waves per workgroup, 16 (128-row slices) 4 waves."""
     K, N = 2048, 1024
     a, qw, sc, codes, s16 = _case(M, K, N, 60 + M, cuda)
     ag = a.to(cuda)
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
-    assert _pk.w4a16_plan(M, N, K, 128, 2)[0] == _pk.KERNEL_GEMM
+    assert _pk.w4a16_plan(M, N, K, 128, 1)[0] == _pk.KERNEL_GEMM
     base = None
     for s in (4, 8, 16):
         assert _pk.w4a16_plan(M, N, K, 128, s) == (_pk.KERNEL_SKINNY, s)
@@ -139,8 +141,8 @@ def test_skinny_ineligible_shapes_use_gemm(cuda):
 
 @pytest.mark.parametrize("M,K,split", [(8, 3200, 5), (8, 4096, 2), (24, 3200, 5), (24, 4096, 1)])
 def test_skinny_per_tensor_long_wave_rows(M, K, split, cuda):
-    """One tensor scale puts no group limit on a wave's rows: 5, 16 and 32 k-steps per wave run
-    the prefetch ring through refills and a partial last round."""
+    """One tensor scale puts no group limit on a wave's rows: 5 (4 waves), 8 and 16 k-steps
+    (8 waves) per wave run the prefetch ring through refills and a partial last round."""
     N = 528
     assert _pk.w4a16_plan(M, N, K, 0, split) == (_pk.KERNEL_SKINNY, split)
     a = torch.randn(M, K, generator=_gen(110 + K)).half()
@@ -150,3 +152,61 @@ def test_skinny_per_tensor_long_wave_rows(M, K, split, cuda):
     out = _pk.w4a16_gemm(a.to(cuda), qw, None, 0, scale, torch.float32, split_k=split)
     ref = oracle.int4_gemm_ref(a.numpy(), q.numpy(), scale)
     assert oracle.rel_fro(out.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("M", [33, 48, 64, 65, 100, 128])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (1152, 784), (640, 16)])
+def test_skinny_four_blocks(M, K, N, cuda):
+    """33 <= M <= 128: four 16-row blocks and 128-column tiles; above 64 rows two row parts
+    per tile (their workgroups paired on one XCD), the second part ragged unless M = 128."""
+    assert _pk.w4a16_plan(M, N, K, 128, 0)[0] == _pk.KERNEL_SKINNY
+    a, qw, sc, codes, s16 = _case(M, K, N, 7 * M + K % 89 + N % 83, cuda)
+    out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, 128, out_dtype=torch.float32)
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
+    err = oracle.rel_fro(out.cpu().numpy(), ref)
+    assert err <= W4A16_TOL, f"rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("M", [8, 24, 64, 128])
+def test_skinny_layouts_agree(M, cuda, monkeypatch):
+    """The tile layouts (PK_SKINNY_CFG = columns per lane, waves): at one wave count the
+    column width changes only which lane holds a column, so 16 and 8 columns per lane give the
+    same bits; 8 waves split a slice's rows differently (fp32 reassociation only)."""
+    K, N, split = 4096, 1040, 8
+    a, qw, sc, codes, s16 = _case(M, K, N, 120 + M, cuda)
+    ag = a.to(cuda)
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
+    outs = {}
+    for cfg in ("16,4", "8,4", "16,8", "8,8"):
+        monkeypatch.setenv("PK_SKINNY_CFG", cfg)
+        if M > 32 and cfg.startswith("16"):
+            continue  # four blocks always use 8 columns per lane
+        sp = split if cfg.endswith(",4") else 4
+        assert _pk.w4a16_plan(M, N, K, 128, sp) == (_pk.KERNEL_SKINNY, sp)
+        o = gemm_int4.w4a16_gemm(ag, qw, sc, 128, split_k=sp, out_dtype=torch.float32)
+        assert oracle.rel_fro(o.cpu().numpy(), ref) <= W4A16_TOL, cfg
+        outs[cfg] = o
+    if "16,4" in outs:
+        assert torch.equal(outs["16,4"], outs["8,4"])
+        assert torch.equal(outs["16,8"], outs["8,8"])
+    assert oracle.rel_fro(outs["8,8"].cpu().numpy(), outs["8,4"].cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("cfg", ["8,4", "8,8", "16,8"])
+@pytest.mark.parametrize("M", [5, 20, 40, 97])
+def test_skinny_layouts_edges(cfg, M, cuda, monkeypatch):
+    """Every layout on ragged tiles, ragged row blocks and parts, per-tensor and group scales,
+    and the automatic split (8 waves need slices of 8 * 32 rows)."""
+    monkeypatch.setenv("PK_SKINNY_CFG", cfg)
+    for K, N, G in ((2048, 528, 128), (1024, 784, 64), (2560, 272, 32)):
+        assert _pk.w4a16_plan(M, N, K, G, 0)[0] == _pk.KERNEL_SKINNY
+        a, qw, sc, codes, s16 = _case(M, K, N, 130 + M + N, cuda, G=G)
+        out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, G, out_dtype=torch.float32)
+        err = oracle.rel_fro(out.cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, G))
+        assert err <= W4A16_TOL, (K, N, G, err)
+    K, N = 3072, 400
+    a = torch.randn(M, K, generator=_gen(140 + M)).half()
+    q = torch.randint(-8, 8, (K, N), generator=_gen(141), dtype=torch.int8)
+    qw = gemm_int4.pack_int4_n(q.to(cuda)).view(torch.int32)
+    out = _pk.w4a16_gemm(a.to(cuda), qw, None, 0, 0.02, torch.float32)
+    assert oracle.rel_fro(out.cpu().numpy(), oracle.int4_gemm_ref(a.numpy(), q.numpy(), 0.02)) < 1e-5
