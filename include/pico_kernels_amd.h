@@ -146,7 +146,8 @@ int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight, int64_t l
 
 /* Which kernel pk_w4a16_gemm would run and its split factor (for reporting/benchmarks):
  * writes kernel id (1 = GEMV for M <= 4, 2 = LDS-tiled MFMA GEMM, 3 = register-dequant MFMA
- * kernel for 5 <= M <= 32) and the effective split. */
+ * kernel for 5 <= M <= 64, and M <= 128 on layers of at most 4096 x 4096 weights) and the
+ * effective split. */
 int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_id,
                   int* split_used);
 

@@ -1,9 +1,9 @@
 // C ABI for the W4A16 matmul (gemm_int4.int4_gemm + the group-128 / split-K path) and the
 // dense fp16 split-K matmul (gemm_splitk.triton_gemm_splitk).
 //
-// Dispatch: M <= 4 runs the HBM-bound GEMV (w4a16_gemv.hip); 5 <= M <= 32 the register-
-// dequant MFMA kernel (w4a16_skinny.hip); larger M the MFMA GEMM that dequantises B into LDS.
-// All honour an explicit split_k.
+// Dispatch: M <= 4 runs the HBM-bound GEMV (w4a16_gemv.hip); 5 <= M <= 64 (<= 128 for layers
+// of at most 4096 x 4096 weights) the register-dequant MFMA kernel (w4a16_skinny.hip); larger
+// M the MFMA GEMM that dequantises B into LDS. All honour an explicit split_k.
 #include "pk_internal.h"
 
 using namespace pk;
