@@ -531,12 +531,12 @@ def mfma_probe(dev) -> int:
 
 
 def mfma_ceiling(dev) -> dict:
-    """What the matrix cores sustain with no memory traffic (pk_mfma_probe): 256 workgroups of
+    """What the matrix cores sustain with no memory traffic (pkb_mfma_probe): 256 workgroups of
     8 waves issuing independent MFMAs on constant or pseudo-random operands, timed with HIP
     events on the launch stream, against MI355X's published dense peaks."""
     import torch
 
-    import _pk
+    import _probes
 
     grid, iters = 256, 4000
     out = torch.empty(grid * 512, dtype=torch.float32, device=dev)
@@ -544,11 +544,11 @@ def mfma_ceiling(dev) -> dict:
     for fp8, peak in ((True, MFMA_F8_PEAK_TFLOPS), (False, MFMA_F16_PEAK_TFLOPS)):
         flops = grid * 8 * iters * 8 * (131072 if fp8 else 32768)
         for random in (False, True):
-            _pk.mfma_probe(fp8, random, grid, iters, out)
+            _probes.mfma_probe(fp8, random, grid, iters, out)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             for _ in range(5):
-                _pk.mfma_probe(fp8, random, grid, iters, out)
+                _probes.mfma_probe(fp8, random, grid, iters, out)
             e1.record()
             e1.synchronize()
             tf = 5 * flops / (e0.elapsed_time(e1) * 1e-3) / 1e12
@@ -596,13 +596,13 @@ def vendor_compare(dev) -> dict:
 
 
 def hbm_ceiling(dev) -> dict:
-    """What one launch that only reads achieves (pk_read_probe), timed like the GEMV: a graph of
+    """What one launch that only reads achieves (pkb_read_probe), timed like the GEMV: a graph of
     back-to-back launches over rotating buffers (more than the 256 MB Infinity Cache). At the
     GEMV's 23,279,104 bytes it is the ceiling the headline's fraction is read against; 256 MiB
     and 1 GiB show the asymptotic rate."""
     import torch
 
-    import _pk
+    import _probes
 
     rows = []
     for nbytes, nrot, steps in ((23279104, N_ROTATE, 2000), (256 << 20, 4, 40), (1 << 30, 2, 20)):
@@ -610,7 +610,7 @@ def hbm_ceiling(dev) -> dict:
         best = None
         for grid in (256, 512, 768, 1024, 2048, 4096):
             out = torch.empty(grid, dtype=torch.int32, device=dev)
-            ms = GraphTimer(lambda i: _pk.read_probe(bufs[i % nrot], out, grid), steps, 2).run(reps=3)
+            ms = GraphTimer(lambda i: _probes.read_probe(bufs[i % nrot], out, grid), steps, 2).run(reps=3)
             tbs = nbytes / (ms * 1e-3) / 1e12
             if best is None or tbs > best["TB/s"]:
                 best = {"bytes": nbytes, "grid": grid, "us": round(ms * 1e3, 3), "TB/s": round(tbs, 3),

@@ -145,8 +145,10 @@ int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight, int64_t l
                   size_t workspace_bytes, void* stream);
 
 /* Which kernel pk_w4a16_gemm would run and its split factor (for reporting/benchmarks):
- * writes kernel id (1 = GEMV for M <= 4, 2 = LDS-tiled MFMA GEMM, 3 = register-dequant MFMA
- * kernel for 5 <= M <= 64, and M <= 128 on layers of at most 4096 x 4096 weights) and the
+ * writes kernel id (1 = GEMV for M <= 4, 2 = LDS-tiled MFMA GEMM that dequantises B into LDS,
+ * 3 = register-dequant MFMA kernel for 5 <= M <= 64, and M <= 128 on layers of at most
+ * 4096 x 4096 weights, 4 = MFMA GEMM that keeps B packed in LDS, for unsplit M >= 256,
+ * N % 256 == 0, K % 128 == 0, group % 64 == 0, assuming 16-byte aligned operands) and the
  * effective split. */
 int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_id,
                   int* split_used);
@@ -251,20 +253,6 @@ int pk_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int6
                     int64_t skh, int64_t skn, const void* v, int64_t svb, int64_t svh,
                     int64_t svn, int B, int H, int N, int D, int split, float sm_scale,
                     float* out, void* workspace, size_t workspace_bytes, void* stream);
-
-/* ---- Measurement ------------------------------------------------------------------------
- * pk_mfma_probe: no counterpart in the reference; for benchmarks that read the GEMMs'
- * roofline fractions against what the matrix cores sustain. Launches `grid` workgroups of 8
- * waves that each issue iters x 8 independent MFMAs (fp8 != 0: v_mfma 32x32x64 e4m3, else
- * 32x32x16 fp16) on constant (random == 0) or pseudo-random register operands, with no memory
- * traffic in the loop; out receives grid * 512 floats. FLOPs per launch:
- * grid * 8 * iters * 8 * (fp8 ? 131072 : 32768). */
-int pk_mfma_probe(int fp8, int random, int grid, int iters, float* out, void* stream);
-/* pk_read_probe: no counterpart in the reference; for benchmarks that read the memory-bound
- * kernels' fractions against what one launch reading the same bytes achieves. Reads `bytes`
- * (a multiple of 16, 16-byte aligned) with `grid` workgroups of 256 threads, writes one
- * 32-bit word per workgroup to out. */
-int pk_read_probe(const void* src, size_t bytes, uint32_t* out, int grid, void* stream);
 
 #ifdef __cplusplus
 }

@@ -25,7 +25,7 @@ _TORCH_TO_PK = {torch.float32: PK_F32, torch.float16: PK_F16, torch.bfloat16: PK
 
 PK_OK, PK_EINVAL, PK_EUNSUPPORTED, PK_EWORKSPACE, PK_EHIP = 0, -1, -2, -3, -4
 
-KERNEL_GEMV, KERNEL_GEMM, KERNEL_SKINNY = 1, 2, 3  # pk_w4a16_plan kernel ids
+KERNEL_GEMV, KERNEL_GEMM, KERNEL_SKINNY, KERNEL_GEMM_TR4 = 1, 2, 3, 4  # pk_w4a16_plan kernel ids
 
 
 class PicoKernelsError(RuntimeError):
@@ -69,8 +69,6 @@ _SIGNATURES = {
     "pk_flash_decode_launches": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "pk_flash_decode": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
                                _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _sz, _vp]),
-    "pk_mfma_probe": (_i32, [_i32, _i32, _i32, _i32, _vp, _vp]),
-    "pk_read_probe": (_i32, [_vp, _sz, _vp, _i32, _vp]),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
@@ -389,19 +387,3 @@ def flash_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, split: int,
                                  0 if ws is None else ws.numel(), stream_of(q)),
            "pk_flash_decode")
     return out
-
-
-def mfma_probe(fp8: bool, random: bool, grid: int, iters: int, out: torch.Tensor) -> None:
-    """Pure-MFMA throughput probe on the current stream (pk_mfma_probe); ``out`` holds
-    ``grid * 512`` fp32 values."""
-    assert out.dtype == torch.float32 and out.numel() >= grid * 512 and out.is_cuda
-    _check(lib().pk_mfma_probe(int(fp8), int(random), int(grid), int(iters), out.data_ptr(),
-                               stream_of(out)), "pk_mfma_probe")
-
-
-def read_probe(src: torch.Tensor, out: torch.Tensor, grid: int) -> None:
-    """Streaming read of ``src``'s bytes on the current stream (pk_read_probe); ``out`` holds
-    ``grid`` int32 words."""
-    assert out.dtype == torch.int32 and out.numel() >= grid and out.is_cuda and src.is_cuda
-    _check(lib().pk_read_probe(src.data_ptr(), src.numel() * src.element_size(), out.data_ptr(),
-                               int(grid), stream_of(src)), "pk_read_probe")

@@ -5,6 +5,8 @@ Usage: ``python pico-kernels_amd/build.py [-j N] [--verbose]``.
 Every ``csrc/*.hip`` file is compiled with hipcc for gfx950 only and linked into one shared
 library next to this file. The library exposes the C ABI declared in
 ``include/pico_kernels_amd.h``; the Python modules in this directory load it with ctypes.
+The measurement probes bench.py uses (``csrc/bench/*.hip``) go into a second library,
+``libpk_bench_probes.so``, so they stay outside the product library and its header.
 """
 
 from __future__ import annotations
@@ -21,6 +23,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 INCLUDE = HERE.parent / "include"
 LIB_NAME = "libpico_kernels_amd.so"
+PROBES_LIB_NAME = "libpk_bench_probes.so"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -58,21 +61,8 @@ def _compile(src: Path, obj: Path, verbose: bool) -> None:
         print(err)
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile all HIP sources and link the shared library; returns its path."""
-    objdir = HERE / "_build"
-    objdir.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
-    if not sources:
-        raise RuntimeError(f"no HIP sources under {CSRC}")
-    objs = [objdir / (s.stem + ".o") for s in sources]
-    jobs = jobs or min(len(sources), os.cpu_count() or 4, 16)
-    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_compile, s, o, verbose) for s, o in zip(sources, objs)]
-        for f in futs:
-            f.result()
-    out = HERE / LIB_NAME
-    tmp = HERE / (LIB_NAME + ".tmp")
+def _link(objs: list[Path], out: Path, verbose: bool) -> None:
+    tmp = out.with_name(out.name + ".tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -86,8 +76,31 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     try:
         ctypes.CDLL(str(tmp), mode=os.RTLD_NOW)
     except OSError as e:
-        raise RuntimeError(f"built library does not load: {e}") from None
+        raise RuntimeError(f"built library {out.name} does not load: {e}") from None
     os.replace(tmp, out)
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile all HIP sources and link the product library and the bench probes library;
+    returns the product library's path."""
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    probe_sources = sorted((CSRC / "bench").glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    objs = [objdir / (s.stem + ".o") for s in sources]
+    probe_objs = [objdir / ("bench_" + s.stem + ".o") for s in probe_sources]
+    jobs = jobs or min(len(sources) + len(probe_sources), os.cpu_count() or 4, 16)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [ex.submit(_compile, s, o, verbose)
+                for s, o in zip(sources + probe_sources, objs + probe_objs)]
+        for f in futs:
+            f.result()
+    out = HERE / LIB_NAME
+    _link(objs, out, verbose)
+    if probe_objs:
+        _link(probe_objs, HERE / PROBES_LIB_NAME, verbose)
     return out
 
 

@@ -1,0 +1,30 @@
+/*
+ * pk_bench_probes.h -- measurement probes for bench.py (libpk_bench_probes.so). Not part of
+ * the product library or its C ABI (include/pico_kernels_amd.h); no counterpart in the
+ * reference. Both return 0, -1 for a bad argument, or the HIP error code of the launch.
+ */
+#ifndef PK_BENCH_PROBES_H
+#define PK_BENCH_PROBES_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Launches `grid` workgroups of 8 waves that each issue iters x 8 independent MFMAs (fp8 != 0:
+ * v_mfma 32x32x64 e4m3, else 32x32x16 fp16) on constant (random == 0) or pseudo-random register
+ * operands, with no memory traffic in the loop; out receives grid * 512 floats. FLOPs per
+ * launch: grid * 8 * iters * 8 * (fp8 ? 131072 : 32768). */
+int pkb_mfma_probe(int fp8, int random, int grid, int iters, float* out, void* stream);
+
+/* Reads `bytes` (a multiple of 16, 16-byte aligned) with `grid` workgroups of 256 threads and
+ * writes one 32-bit word per workgroup (the XOR of the words it read) to out. */
+int pkb_read_probe(const void* src, size_t bytes, uint32_t* out, int grid, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PK_BENCH_PROBES_H */

@@ -1,12 +1,14 @@
-// Ceiling probes, measurement entry points of this library (the reference has no
-// counterpart):
+// Ceiling probes for bench.py, built into their own library (libpk_bench_probes.so), outside
+// the product library and its header; the reference has no counterpart:
 //  * MFMA: waves that issue only independent MFMAs (no memory traffic in the loop), 8 waves
 //    per workgroup like the GEMMs, on register operands that are either constant or
 //    pseudo-random -- what the matrix cores sustain for the data the GEMMs see.
 //  * HBM read: a streaming read of a buffer (16-byte non-temporal loads, XOR-reduced, one
 //    word written per workgroup) -- what one launch reading a given number of bytes achieves,
 //    the ceiling the memory-bound kernels' fractions are read against.
-#include "pk_internal.h"
+#include "../pk_common.h"
+
+#include "pk_bench_probes.h"
 
 namespace pk {
 
@@ -87,20 +89,17 @@ __global__ __launch_bounds__(256) void hbm_read_probe_kernel(const pk_u4v* src, 
 
 using namespace pk;
 
-extern "C" int pk_read_probe(const void* src, size_t bytes, uint32_t* out, int grid, void* stream) {
-  PK_REQUIRE(src != nullptr && out != nullptr, "pk_read_probe: null pointer");
-  PK_REQUIRE(bytes >= 16 && bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0,
-             "pk_read_probe: bytes must be a positive multiple of 16 on a 16-byte aligned buffer");
-  PK_REQUIRE(grid >= 1, "pk_read_probe: grid must be positive");
+// Status: 0, or -1 for a bad argument, or the HIP error of the launch.
+extern "C" int pkb_read_probe(const void* src, size_t bytes, uint32_t* out, int grid, void* stream) {
+  if (src == nullptr || out == nullptr || grid < 1) return -1;
+  if (bytes < 16 || bytes % 16 || (reinterpret_cast<uintptr_t>(src) & 15)) return -1;
   hbm_read_probe_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(
       reinterpret_cast<const pk_u4v*>(src), (int64_t)(bytes / 16), out);
-  PK_LAUNCH_CHECK("hbm read probe");
-  return PK_OK;
+  return (int)hipGetLastError();
 }
 
-extern "C" int pk_mfma_probe(int fp8, int random, int grid, int iters, float* out, void* stream) {
-  PK_REQUIRE(out != nullptr, "pk_mfma_probe: null output");
-  PK_REQUIRE(grid >= 1 && iters >= 1, "pk_mfma_probe: grid and iters must be positive");
+extern "C" int pkb_mfma_probe(int fp8, int random, int grid, int iters, float* out, void* stream) {
+  if (out == nullptr || grid < 1 || iters < 1) return -1;
   const hipStream_t s = (hipStream_t)stream;
   if (fp8) {
     if (random) mfma_probe_kernel<true, true><<<grid, 512, 0, s>>>(out, iters);
@@ -109,6 +108,5 @@ extern "C" int pk_mfma_probe(int fp8, int random, int grid, int iters, float* ou
     if (random) mfma_probe_kernel<false, true><<<grid, 512, 0, s>>>(out, iters);
     else mfma_probe_kernel<false, false><<<grid, 512, 0, s>>>(out, iters);
   }
-  PK_LAUNCH_CHECK("mfma probe");
-  return PK_OK;
+  return (int)hipGetLastError();
 }

@@ -1,8 +1,8 @@
 // Large-tile MFMA GEMMs for gfx950: W4A16 / dense fp16 (v_mfma_f32_32x32x16_f16) and
 // e4m3 fp8 (v_mfma_f32_32x32x64_f8f6f4).
 //
-// Design (f16: 4 waves, 2 x 2, each a 128 x 64 or 64 x 64 block; fp8 256 x 256: 8 waves,
-// 2 x 4, each a 128 x 64 block):
+// Design (f16: 8 waves, two per SIMD: 256 x 128 tiles as 4 x 2 waves of 64 x 64, 128 x 128
+// tiles as 2 x 4 waves of 64 x 32; fp8 256 x 256: 8 waves, 2 x 4, each a 128 x 64 block):
 //  * LDS tiles are rows of 128 bytes (64 fp16 or 128 fp8 values of k) in 8 chunks of 16 B;
 //    chunk c of row r is stored in slot c ^ ((r >> 1) & 7). Sixteen lanes reading 16
 //    consecutive rows at one chunk then touch 16 distinct 16-byte bank groups.

@@ -88,11 +88,15 @@ int v2_f8_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb,
                  float out_scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
                  hipStream_t s);
 
-// 256 x 256 W4A16 GEMM with a 4-stage LDS pipeline, 8 waves of 128 x 64 (gemm_w4_wide.hip).
-bool w4_wide_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ldb);
-int w4_wide_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
-                   int group, float scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
-                   hipStream_t s);
+// W4A16 GEMM with the int4 B tile kept packed in LDS and read with transposing 4-bit reads,
+// 128 x 256 tiles, eight waves splitting each k-tile in halves (w4a16_tr4.hip); split 1,
+// N % 256 == 0, K % 128 == 0.
+bool tr4_shape_ok(int M, int N, int K, int group, bool has_gs);
+bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ldb, int64_t ldc,
+            int c_dtype, const void* c);
+int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
+               int group, float scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+               hipStream_t s);
 
 // 256 x 256 fp8 GEMM with a 4-stage DMA pipeline and transposing LDS reads for (K, N) B
 // (gemm_f8_v3.hip).

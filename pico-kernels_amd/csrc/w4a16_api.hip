@@ -10,7 +10,7 @@ using namespace pk;
 
 namespace {
 
-enum { kKernelGemv = 1, kKernelGemm = 2, kKernelSkinny = 3 };
+enum { kKernelGemv = 1, kKernelGemm = 2, kKernelSkinny = 3, kKernelGemmTr4 = 4 };
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -100,7 +100,12 @@ extern "C" int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, i
               group_size, split_k);
     return PK_EUNSUPPORTED;
   }
-  if (kernel_id) *kernel_id = pl.kernel;
+  int kid = pl.kernel;
+  // the unsplit GEMM runs the kernel that keeps B packed in LDS where its shape rules hold
+  // (and its operands are aligned, which this report assumes)
+  if (kid == kKernelGemm && pl.gemm.split == 1 && tr4_shape_ok(M, N, K, has_gs ? group_size : K, has_gs))
+    kid = kKernelGemmTr4;
+  if (kernel_id) *kernel_id = kid;
   if (split_used) *split_used = plan_split(pl);
   return PK_OK;
 }

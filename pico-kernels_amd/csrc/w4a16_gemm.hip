@@ -354,32 +354,14 @@ static int launch_mode(const GemmPlan& pl, const GemmParams& p, hipStream_t s) {
   return launch_cfg<256, 128, 2, 2, BMODE>(p, s);
 }
 
-// The 256 x 256 int4 kernel (gemm_w4_wide.hip) or the 256 x 128 one for a large output.
-// Measured on MI355X: the 256 x 256 kernel is ~6% faster per tile (8192^3: 1105 against
-// 1044 TFLOP/s) but its tiles come in rounds of 256 workgroups four times as large: at
-// 4096^3 (one round) it is 1-2% slower, at 4096 x 14336 (3.5 rounds) 4% slower. So it runs
-// when it has at least two rounds of tiles and fills its last round at least as well as the
-// 256 x 128 tiles fill theirs. PK_W4_WIDE=1 forces it (where its constraints hold), =0 turns
-// it off; read at each call.
-static bool w4_wide_pick(int M, int N) {
-  if (const char* env = std::getenv("PK_W4_WIDE")) {
-    if (env[0] == '0') return false;
-    if (env[0] == '1') return true;
-  }
-  const int64_t tw = cdiv(M, 256) * cdiv(N, 256), to = cdiv(M, 256) * cdiv(N, 128);
-  if (tw < 512) return false;
-  // fill of the last round: tiles / (256 * rounds), compared without division
-  const int64_t rw = cdiv(tw, 256), ro = cdiv(to, 256);
-  return tw * ro >= to * rw;
-}
-
 int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const void* b,
                 int64_t ldb, const void* scales, int group, float tensor_scale, void* c,
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only) {
-  if (bmode == kBInt4 && pl.split == 1 && !partials_only && w4_wide_pick(M, N) &&
-      w4_wide_ok(M, N, K, group, scales != nullptr, lda, ldb))
-    return w4_wide_launch(a, lda, b, ldb, scales, group, tensor_scale, c, c_dtype, ldc, M, N, K, s);
+  // Unsplit int4 GEMMs of at least 256 rows: the kernel that keeps B packed in LDS.
+  if (bmode == kBInt4 && pl.split == 1 && !partials_only &&
+      tr4_ok(M, N, K, group, scales != nullptr, lda, ldb, ldc, c_dtype, c))
+    return tr4_launch(a, lda, b, ldb, scales, group, tensor_scale, c, c_dtype, ldc, M, N, K, s);
   // 128/256-row tiles: the large-tile 32x32-MFMA kernel when its constraints hold.
   if (pl.cfg.bm >= 128 &&
       v2_f16_ok(M, N, K, pl.k_slice, group, scales != nullptr, lda, ldb, bmode == kBInt4))

@@ -23,15 +23,11 @@
 //     -8 * sum(x) and the group scale is applied in fp32.
 //
 // Reduction: row-lanes inside a wave are folded with a reduce-scatter over lane masks
-// 32/16/8, waves through LDS. With split-K each slice writes an fp32 partial row and a
-// second small kernel (splitk_reduce_kernel) adds the slices in order 0..S-1, so the result
-// is bitwise reproducible (no floating-point atomics). A kernel boundary is the cheapest
-// point where writes from every XCD's L2 become visible to all; measured on MI355X, a
-// last-workgroup handoff inside the kernel costs more: with agent-scope release/acquire
-// fences (an L2 writeback per releasing workgroup) it is 2.6x slower at 16 slices, and with
-// device-coherent relaxed atomics it still adds a ~2.3 us chain of dependent memory round
-// trips (store acknowledgement, arrival counter, partial loads) to the kernel, no faster
-// end to end than the second kernel.
+// 32/16/8, waves through LDS. With split-K each slice writes an fp32 partial row; the slices
+// are then added in order 0..S-1 (bitwise reproducible, no floating-point atomics), either
+// inside the same launch by the last slice of a column tile to arrive (the MFMA kernel below,
+// when all slices of a tile share one XCD: gemv_finish_l2) or by a second small kernel
+// (splitk_reduce_kernel) for this VALU kernel and the partials-only entry point.
 #include "pk_internal.h"
 
 namespace pk {

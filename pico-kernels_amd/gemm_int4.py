@@ -77,7 +77,7 @@ def int4_gemm(a: torch.Tensor, w_packed: torch.Tensor, scale: float,
     assert a.is_cuda and a.dtype in (torch.float16, torch.bfloat16)
     M, K = a.shape
     K2, N_half = w_packed.shape
-    assert K2 == K and N_half % 1 == 0
+    assert K2 == K, "int4_gemm: w_packed must be (K, N//2) for a of shape (M, K)"
     if a.dtype != torch.float16:
         raise NotImplementedError("int4_gemm: the MI355X kernels take fp16 activations")
     N = N_half * 2

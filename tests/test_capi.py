@@ -46,11 +46,13 @@ def test_w4a16_plans():
     assert kid == _pk.KERNEL_GEMV and split >= 4
     for s in (1, 2, 4, 8, 16):
         assert _pk.w4a16_plan(1, 11008, 4096, 128, s) == (_pk.KERNEL_GEMV, s)
-    # prefill: MFMA GEMM, no split needed at 2048 rows
-    assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (_pk.KERNEL_GEMM, 1)
+    # prefill: the MFMA GEMM that keeps B packed in LDS, no split needed at 2048 rows
+    assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (_pk.KERNEL_GEMM_TR4, 1)
     assert _pk.w4a16_plan(128, 6144, 4096, 128, 0)[0] == _pk.KERNEL_GEMM
     # per-tensor mode (group_size 0) for the drop-in int4_gemm
-    assert _pk.w4a16_plan(256, 512, 256, 0, 0)[0] == _pk.KERNEL_GEMM
+    assert _pk.w4a16_plan(256, 512, 256, 0, 0)[0] == _pk.KERNEL_GEMM_TR4
+    assert _pk.w4a16_plan(256, 520, 256, 0, 0)[0] == _pk.KERNEL_GEMM   # N % 256 != 0
+    assert _pk.w4a16_plan(256, 512, 192, 0, 0)[0] == _pk.KERNEL_GEMM   # K % 128 != 0
     assert _pk.w4a16_plan(128, 512, 256, 0, 0)[0] == _pk.KERNEL_SKINNY
     # slices may cut a group (scales are applied per 16-row chunk) ...
     assert _pk.w4a16_plan(1, 4096, 4096, 128, 64) == (_pk.KERNEL_GEMV, 64)
@@ -95,7 +97,11 @@ def test_w4a16_plans_by_row_count():
     assert _pk.w4a16_plan(128, 14336, 4096, 128, 0) == (C, 2)    # 112 tiles x 2
     assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (C, 8)
     assert _pk.w4a16_plan(256, 6144, 4096, 128, 0) == (C, 4)
-    assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (C, 1)
+    # unsplit from 256 rows on: the GEMM that keeps B packed in LDS (N % 256, K % 128, group % 64)
+    T = _pk.KERNEL_GEMM_TR4
+    assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (T, 1)
+    assert _pk.w4a16_plan(4096, 4096, 4096, 128, 0) == (T, 1)
+    assert _pk.w4a16_plan(2048, 4096, 4096, 32, 0) == (C, 1)      # group % 64 != 0
 
 
 def test_workspace_sizes():

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-import _pk
+import _probes
 
 pytestmark = pytest.mark.gpu
 
@@ -22,7 +22,7 @@ def test_read_probe_reads_every_word_once(grid, words, cuda):
     host = torch.randint(-2**31, 2**31 - 1, (words,), generator=g, dtype=torch.int64).to(torch.int32)
     src = host.to(cuda)
     out = torch.zeros(grid, dtype=torch.int32, device=cuda)
-    _pk.read_probe(src, out, grid)
+    _probes.read_probe(src, out, grid)
     got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
     want = np.bitwise_xor.reduce(host.numpy().view(np.uint32))
     assert got == want
@@ -31,8 +31,8 @@ def test_read_probe_reads_every_word_once(grid, words, cuda):
 def test_read_probe_rejects_bad_sizes(cuda):
     src = torch.zeros(3, dtype=torch.int32, device=cuda)  # 12 bytes: not a multiple of 16
     out = torch.zeros(4, dtype=torch.int32, device=cuda)
-    with pytest.raises(_pk.PicoKernelsError):
-        _pk.read_probe(src, out, 4)
+    with pytest.raises(_probes.ProbeError):
+        _probes.read_probe(src, out, 4)
 
 
 def test_mfma_probe_constant_operands(cuda):
@@ -40,7 +40,7 @@ def test_mfma_probe_constant_operands(cuda):
     so every lane's output is iters * 8 accumulators * 16 elements * 16 * 0.25."""
     grid, iters = 4, 10
     out = torch.zeros(grid * 512, dtype=torch.float32, device=cuda)
-    _pk.mfma_probe(False, False, grid, iters, out)
+    _probes.mfma_probe(False, False, grid, iters, out)
     assert torch.all(out == iters * 8 * 16 * 16 * 0.25)
-    _pk.mfma_probe(True, True, grid, iters, out)  # random fp8 operands: finite sums
+    _probes.mfma_probe(True, True, grid, iters, out)  # random fp8 operands: finite sums
     assert torch.isfinite(out).all()

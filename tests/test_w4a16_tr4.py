@@ -1,0 +1,90 @@
+"""The W4A16 GEMM that keeps the int4 weights packed in LDS (w4a16_tr4.hip, plan kernel id 4):
+against the float64 dequantise-and-matmul oracle, through the C ABI, on every k-tile remainder
+its unrolled loop has (1 to 7 tiles of 128 k), ragged M, group sizes 64 / 128 / 256 and the
+per-tensor mode, strided activations, an output view wider than N, every output dtype; results
+bitwise reproducible run to run."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import _pk
+import gemm_int4
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(M, K, N, G, seed, cuda):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    a = torch.randn(M, K, generator=g).half()
+    w = (torch.randn(K, N, generator=g) * 0.02).half()
+    codes, _, s16 = oracle.rtn_group_codes(w.numpy(), 4, G)
+    qw = torch.from_numpy(oracle.pack_int4_n(codes).view(np.int32).copy()).to(cuda)
+    sc = torch.from_numpy(s16).to(cuda)
+    return a, codes, s16, qw, sc
+
+
+@pytest.mark.parametrize("M,K,N,G", [
+    (256, 128, 256, 128),    # one k-tile
+    (256, 256, 512, 64),     # two, group 64 (each k half its own scale row)
+    (300, 384, 256, 128),    # three, ragged M
+    (256, 512, 768, 256),    # four, group 256
+    (384, 640, 256, 128),    # five
+    (512, 768, 512, 128),    # six (one pass of the unrolled loop)
+    (257, 896, 256, 64),     # seven (loop + one), one row past a tile
+    (2048, 4096, 4096, 128), # the prefill shape
+])
+def test_tr4_matches_oracle(M, K, N, G, cuda):
+    a, codes, s16, qw, sc = _case(M, K, N, G, M + K + N, cuda)
+    assert _pk.w4a16_plan(M, N, K, G, 0) == (_pk.KERNEL_GEMM_TR4, 1)
+    out = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float32)
+    again = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float32)
+    assert torch.equal(out, again), "not bitwise reproducible"
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, G)
+    err = oracle.rel_fro(out.cpu().numpy(), ref)
+    assert err < 1e-3, err  # dequantised weights rounded to fp16 (as the other GEMMs): ~2.7e-4
+
+
+def test_tr4_per_tensor_mode(cuda):
+    """int4_gemm's per-tensor path (codes in [-8, 7], the scale in the epilogue)."""
+    g = torch.Generator()
+    g.manual_seed(11)
+    M, K, N = 2048, 512, 2048  # unsplit (smaller outputs take split-K kernels)
+    a = torch.randn(M, K, generator=g).half()
+    q = torch.randint(-8, 8, (K, N), generator=g, dtype=torch.int8)
+    packed = torch.from_numpy(oracle.pack_int4_n(q.numpy()))
+    assert _pk.w4a16_plan(M, N, K, 0, 0) == (_pk.KERNEL_GEMM_TR4, 1)
+    out = gemm_int4.int4_gemm(a.to(cuda), packed.to(cuda), 0.037)
+    ref = (a.double().numpy() @ q.double().numpy()) * 0.037
+    assert oracle.rel_fro(out.cpu().numpy(), ref) < 1e-5  # codes are exact in fp16
+
+
+@pytest.mark.parametrize("out_dtype,tol", [(torch.float16, 2e-3), (torch.bfloat16, 1e-2),
+                                           (torch.float32, 1e-3)])
+def test_tr4_output_dtypes(out_dtype, tol, cuda):
+    M, K, N, G = 384, 512, 512, 128
+    a, codes, s16, qw, sc = _case(M, K, N, G, 5, cuda)
+    out = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, out_dtype)
+    assert out.dtype == out_dtype
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, G)
+    assert oracle.rel_fro(out.float().cpu().numpy(), ref) < tol
+
+
+def test_tr4_strided_operands(cuda):
+    """A with lda > K and an output view into a wider buffer (ldc > N): the same bits as
+    contiguous operands."""
+    M, K, N, G = 320, 512, 512, 128
+    a, codes, s16, qw, sc = _case(M, K, N, G, 9, cuda)
+    a_wide = torch.zeros(M, K + 64, dtype=torch.float16)
+    a_wide[:, :K] = a
+    a_view = a_wide.to(cuda)[:, :K]
+    big = torch.full((M, N + 256), 7.0, dtype=torch.float16, device=cuda)
+    out_view = big[:, 128:128 + N]
+    _pk.w4a16_gemm(a_view, qw, sc, G, 1.0, torch.float16, out=out_view)
+    ref = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float16)
+    assert torch.equal(out_view, ref)
+    assert torch.all(big[:, :128] == 7.0) and torch.all(big[:, 128 + N:] == 7.0)
