@@ -159,6 +159,21 @@ int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_
  * counterpart in the reference (its split-K is one Triton launch plus atomics). */
 int pk_w4a16_launches(int M, int N, int K, int group_size, int split_k);
 
+/* pk_w4a16_gemm for callers that cannot allocate (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc): no workspace argument, and the call allocates nothing. No
+ * counterpart in the reference. The split-K workspace is a fixed device array inside the
+ * library, pk_w4a16_noalloc_scratch_bytes() bytes (16 MiB) per GPU, held until the process
+ * ends; shapes whose plan needs more return PK_EWORKSPACE (pk_w4a16_workspace_bytes() gives
+ * the need). The first call on a device looks the array up and clears its counters on
+ * `stream`; every call leaves them zero. Every call on a GPU shares that GPU's array: calls
+ * that overlap in time on one GPU (different streams, threads) race and must not be made.
+ * Results are bitwise those of pk_w4a16_gemm with the same arguments. */
+size_t pk_w4a16_noalloc_scratch_bytes(void);
+int pk_w4a16_gemm_noalloc(const void* a, int64_t lda, const uint32_t* qweight, int64_t ldq,
+                          const void* scales, int group_size, float tensor_scale, void* c,
+                          int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
+                          void* stream);
+
 /* The two phases of a split-K pk_w4a16_gemm, for callers that reduce elsewhere (for example
  * across devices) or time the phases separately. pk_w4a16_gemm_partials writes the fp32
  * partial sums of every slice to `partials`, laid out (split, M, N) -- the per-slice products

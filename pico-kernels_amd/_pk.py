@@ -53,6 +53,9 @@ _SIGNATURES = {
                              ctypes.POINTER(_i32)]),
     "pk_w4a16_gemm": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
                              _i32, _i32, _vp, _sz, _vp]),
+    "pk_w4a16_noalloc_scratch_bytes": (_sz, []),
+    "pk_w4a16_gemm_noalloc": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
+                                     _i32, _i32, _vp]),
     "pk_w4a16_gemm_partials": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _vp, _sz, _i32, _i32, _i32,
                                       _i32, _vp]),
     "pk_splitk_reduce": (_i32, [_vp, _i32, _i32, _i32, _f32, _vp, _i32, _i64, _vp]),

@@ -6,6 +6,8 @@
 // M the MFMA GEMM that dequantises B into LDS. All honour an explicit split_k.
 #include "pk_internal.h"
 
+#include <atomic>
+
 using namespace pk;
 
 namespace {
@@ -154,6 +156,88 @@ extern "C" int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight
   }
   return plan_launch(pl, a, lda, qweight, ldq, scales, group, tensor_scale, c, c_dtype, ldc, M,
                      N, K, workspace, (hipStream_t)stream, false);
+}
+
+// ---------------------------------------------------------------------------------------
+// pk_w4a16_gemm without a caller workspace, for callers that cannot allocate: the split-K
+// workspace (arrival counters, then fp32 partials) is this file-scope device array. Each GPU
+// holds its own copy, zero at load; every call leaves the counters zero again. Calls that
+// overlap in time on one GPU share it and race.
+// ---------------------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = 16u << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// Clears the split-K arrival counters at the head of the scratch array (a kernel, not a
+// memset node, so the call can sit in a captured graph).
+__global__ void noalloc_zero_counters(unsigned* counters, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) counters[i] = 0u;
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on the current device, looked up once per device (the
+// symbol's host-side name is not a device address); the first lookup also clears the
+// counters on `stream`, ahead of the call that needs them.
+int scratch_on_current_device(void** out, hipStream_t stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return pk::hip_status(e, "pk_w4a16_gemm_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("pk_w4a16_gemm_noalloc: device %d beyond the %d this library tracks", dev, kMaxDevices);
+    return PK_EUNSUPPORTED;
+  }
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return pk::hip_status(e, "pk_w4a16_gemm_noalloc: hipGetSymbolAddress");
+    if (ptr == nullptr) {
+      set_error("pk_w4a16_gemm_noalloc: no device address for the scratch array");
+      return PK_EHIP;
+    }
+    noalloc_zero_counters<<<16, 256, 0, stream>>>(static_cast<unsigned*>(ptr),
+                                                   (int)(kWsCounterBytes / sizeof(unsigned)));
+    e = hipGetLastError();
+    if (e != hipSuccess) return pk::hip_status(e, "pk_w4a16_gemm_noalloc: counter clear");
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return PK_OK;
+}
+}  // namespace
+
+extern "C" size_t pk_w4a16_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int pk_w4a16_gemm_noalloc(const void* a, int64_t lda, const uint32_t* qweight,
+                                     int64_t ldq, const void* scales, int group_size,
+                                     float tensor_scale, void* c, int c_dtype, int64_t ldc, int M,
+                                     int N, int K, int split_k, void* stream) {
+  int rc = check_w4a16(a, lda, qweight, ldq, scales, group_size, c, c_dtype, ldc, M, N, K,
+                       split_k);
+  if (rc != PK_OK) return rc;
+  const bool has_gs = scales != nullptr;
+  const int group = has_gs ? group_size : K;
+  W4Plan pl;
+  if (!make_plan(M, N, K, group, has_gs, split_k, &pl)) {
+    set_error("pk_w4a16_gemm_noalloc: split_k=%d does not divide K=%d into slices of whole "
+              "groups (group %d, multiple of 32 rows)", split_k, K, group);
+    return PK_EINVAL;
+  }
+  const size_t need = plan_ws(pl, M, N);
+  if (need > kNoAllocScratchBytes) {
+    set_error("pk_w4a16_gemm_noalloc: this shape and split need %zu bytes of split-K scratch, "
+              "above the library's fixed %zu (use pk_w4a16_gemm with a workspace, or a smaller "
+              "split)", need, kNoAllocScratchBytes);
+    return PK_EWORKSPACE;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    rc = scratch_on_current_device(&ws, (hipStream_t)stream);
+    if (rc != PK_OK) return rc;
+  }
+  return plan_launch(pl, a, lda, qweight, ldq, scales, group, tensor_scale, c, c_dtype, ldc, M,
+                     N, K, ws, (hipStream_t)stream, false);
 }
 
 extern "C" size_t pk_gemm_f16_workspace_bytes(int M, int N, int K, int split_k) {
