@@ -4,22 +4,32 @@
 Headline workload: W4A16 decode GEMV, M=1, K=4096, N=11008, int4 group
 128 with fp16 scales, fp16 activations N(0,1), weights N(0, 0.02), seeded CPU generator.
 A "step" is one ``w4a16_gemm`` call over one activation row. ``value`` is the whole-op HBM
-throughput (algorithmic bytes / step time), inputs resident in HBM, with 40 distinct weight
-buffers rotated (932 MB, more than twice the 256 MB Infinity Cache) so every step streams
-its weights from HBM.
+throughput (algorithmic bytes / step time), inputs resident in HBM. 40 distinct copies of the
+packed weights and scales (932 MB, more than twice the 256 MB Infinity Cache) are rotated:
+the W warm-up calls read copies 0..W-1, the timed graph starts at copy W and holds
+max(K, 80) calls, so it reads every copy at least twice and never starts on a copy the
+warm-up has just read.
 
-Timing: W eager warmup steps, then exactly K steps captured in one HIP graph and replayed
-once between HIP events (bracketed by device synchronisation). On MI355X the GEMV's split-K
-slices add up in L2 inside the one kernel, so the op is the dominant kernel and the
-roofline fraction uses its time; where a second (reduce) launch is needed, the slice kernel
-is timed on its own through ``pk_w4a16_gemm_partials``. The same JSON line carries the split-K sweep of the config, the
-W4A16 GEMM (prefill 2048x4096x4096 and 4096^3) and fp8 GEMM (4096^3) throughputs the
-metric also names, split-KV decode attention (the reference's benchmark shapes against its eager path,
-and one HBM-bound shape), and the reference's CPU path (dequantize + matmul, numpy oracle) on
-a bounded sample.
+Timing: W eager warm-up steps, then max(K, 80) steps captured in one HIP graph, replayed 3
+times between HIP events on the graph's stream (device synchronisation around each replay);
+the best replay gives ``ms_per_step``. On MI355X the GEMV's split-K slices add up in L2 inside
+the one kernel, so the op is the dominant kernel and the roofline fraction uses its time;
+where a second (reduce) launch is needed, the slice kernel is timed on its own through
+``pk_w4a16_gemm_partials``.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--sweep]
-       python bench.py --only {prefill,gemm4096,fp8,flash_decode,gptq}   (one secondary line)
+Correctness comes first: before any timing each GPU line checks its own output against the
+reference's test-path expression in fp32 torch on the GPU (unpack, multiply by the repeated
+group scales, ``a.float() @ deq``; for fp8 ``(a8.float() @ b8.float()) * out_scale`` and the
+fp32 product) and runs the call twice to check that the two outputs are bitwise equal.
+
+The same JSON line carries the split-K sweep of the config, the Llama-3-8B layer sweep
+(config 5), the W4A16 GEMM (prefill 2048x4096x4096 and 4096^3) and fp8 GEMM (4096^3) lines the
+metric also names, split-KV decode attention, GPTQ of one layer, the eager host time of one
+``w4a16_gemm`` call, and the reference's CPU path (the torch expression above on the host
+cores: dequantize, then matmul, each the median of 5 runs after a warm-up).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-sweep]
+       python bench.py --only {prefill,gemm4096,fp8,flash_decode,gptq,sweep}   (one line)
 """
 
 from __future__ import annotations
@@ -57,7 +67,9 @@ def w4a16_bytes(M: int, K: int, N: int, group: int = 128) -> int:
 
 
 class GraphTimer:
-    """Capture `steps` calls of fn(i) in one HIP graph on a private stream; time a replay."""
+    """Capture `steps` calls fn(warmup + i) in one HIP graph on a private stream, after the
+    eager warm-up calls fn(0 .. warmup-1); time replays. With fn rotating over buffer copies
+    by index, the graph starts on the copy after the last one the warm-up read."""
 
     def __init__(self, fn, steps: int, warmup: int):
         import torch
@@ -69,9 +81,10 @@ class GraphTimer:
                 fn(i)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
+        start = max(warmup, 1)
         with torch.cuda.graph(self.graph, stream=self.stream):
             for i in range(steps):
-                fn(i)
+                fn(start + i)
         torch.cuda.synchronize()
 
     def run(self, reps: int = 1) -> float:
@@ -125,6 +138,76 @@ def gemv_inputs(M: int, K: int, N: int, nrot: int, dev):
     return a, w, qws, scs
 
 
+def unpack_codes(qw):
+    """``(K, N//8)`` int32 words holding pack_int4_n bytes -> ``(K, N)`` int8 codes in [-8, 7],
+    with plain torch ops (the reference's unpack, tests/test_gemm_int4.py:36-41)."""
+    import torch
+
+    b = qw.contiguous().view(torch.uint8)
+    lo = (b & 0x0F).to(torch.int8)
+    hi = (b >> 4).to(torch.int8)
+    q = torch.stack((lo, hi), dim=2).reshape(b.shape[0], -1)
+    return torch.where(q >= 8, q - 16, q)
+
+
+def dequant_expr(qw, sc, group: int = 128):
+    """fp32 weights of the group format: codes times the scales repeated over each group."""
+    return unpack_codes(qw).float() * sc.float().repeat_interleave(group, 0)[: qw.shape[0]]
+
+
+def rel_fro(x, ref) -> float:
+    import torch
+
+    return (torch.linalg.norm(x.float() - ref) / torch.linalg.norm(ref)).item()
+
+
+def check_w4a16(call, a, qw, sc, group: int = 128) -> dict:
+    """Correctness of a W4A16 call before it is timed: relative Frobenius error against the
+    reference's test-path expression in fp32 torch on the GPU (``a.float() @ deq``,
+    tests/test_gemm_int4.py:26), and a bitwise repeat of the call."""
+    import torch
+
+    y1 = call().clone()
+    y2 = call().clone()
+    torch.cuda.synchronize()
+    ref = a.float() @ dequant_expr(qw, sc, group)
+    rel = rel_fro(y1, ref)
+    ok = bool(torch.equal(y1, y2))
+    if not (rel <= 1e-3 and ok):
+        raise RuntimeError(f"W4A16 output check failed before timing: rel_fro={rel:.3e} "
+                           f"bitwise_repeat={ok}")
+    return {"rel_fro_vs_fp32_expr": float(f"{rel:.3e}"), "tolerance": 1e-3,
+            "bitwise_repeat": ok}
+
+
+def host_overhead(step, n: int = 1000) -> dict:
+    """Eager cost of one call from Python: ``wall`` = n back-to-back calls then one device
+    synchronisation, per call; ``enqueue`` = median host time inside one call (argument
+    checks, plan, ctypes marshalling, launch)."""
+    import statistics
+
+    import torch
+
+    for i in range(20):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(n):
+        step(i)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / n
+    ts = []
+    for i in range(200):
+        t = time.perf_counter()
+        step(i)
+        ts.append(time.perf_counter() - t)
+        if i % 16 == 15:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return {"eager_wall_us_per_call": round(wall * 1e6, 2),
+            "host_enqueue_us_median": round(statistics.median(ts) * 1e6, 2)}
+
+
 def bench_gemv(args, dev) -> dict:
     import torch
 
@@ -141,25 +224,31 @@ def bench_gemv(args, dev) -> dict:
         _pk.w4a16_gemm(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
                        split_k=0, out=out)
 
-    ms = GraphTimer(step, args.steps, args.warmup).run()
+    def once():
+        step(0)
+        return out
+
+    check = check_w4a16(once, ag, qws[0], scs[0])
+    timed = max(args.steps, 2 * N_ROTATE)
+    ms = GraphTimer(step, timed, args.warmup).run(reps=3)
     launches = _pk.w4a16_launches(M, N, K, 128, 0)
 
-    # The dominant kernel's average launch: K launches back to back in one graph, HIP events
+    # The dominant kernel's average launch: back-to-back launches in one graph, HIP events
     # around the replay on the launch stream (agrees with rocprof's kernel-trace average);
     # single launches bracketed by their own events read ~1.5 us longer (event overhead).
     # With the slices added in L2 the op is that one kernel; otherwise time the slice kernel
     # alone (it writes the fp32 partials that a second launch adds).
     if launches == 1:
         ms_kernel = ms
-        ms_kernel_events = per_launch_ms(step, min(args.steps, 500))
+        ms_kernel_events = per_launch_ms(step, min(timed, 500))
     else:
         parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
 
         def step_partials(i):
             _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
 
-        ms_kernel = GraphTimer(step_partials, args.steps, args.warmup).run()
-        ms_kernel_events = per_launch_ms(step_partials, min(args.steps, 500))
+        ms_kernel = GraphTimer(step_partials, timed, args.warmup).run(reps=3)
+        ms_kernel_events = per_launch_ms(step_partials, min(timed, 500))
 
     sweep = {}
     for s in (1, 2, 4, 8, 16):
@@ -167,20 +256,26 @@ def bench_gemv(args, dev) -> dict:
             _pk.w4a16_gemm(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
                            split_k=s, out=out)
 
-        ms_s = GraphTimer(step_s, min(args.steps, 400), 2).run()
+        def once_s(s=s):
+            step_s(0)
+            return out
+
+        check_w4a16(once_s, ag, qws[0], scs[0])
+        ms_s = GraphTimer(step_s, max(min(args.steps, 400), 2 * N_ROTATE), 2).run(reps=3)
         sweep[str(s)] = round(nbytes / (ms_s * 1e-3) / 1e9, 1)
     return {
         "M": M, "K": K, "N": N, "split": split, "kernel_id": kid, "launches": launches,
-        "bytes": nbytes,
+        "bytes": nbytes, "steps_timed": timed, "check": check,
         "ms_per_step": ms, "ms_kernel": ms_kernel, "ms_kernel_events": ms_kernel_events,
-        "split_sweep_GBs": sweep,
-        "inputs": (a, w),
+        "split_sweep_GBs": sweep, "host": host_overhead(step),
+        "inputs": (ag, qws[0], scs[0]),
     }
 
 
 def bench_prefill(dev, iters: int = 50, M: int = 2048) -> dict:
     """W4A16 GEMM (group 128, fp16 out) at M x 4096 x 4096: M = 2048 is the prefill config,
-    M = 4096 the 4096^3 shape the metric also names."""
+    M = 4096 the 4096^3 shape the metric also names. Checked, then a graph of `iters` calls
+    replayed 5 times (best replay)."""
     import torch
 
     import _pk
@@ -191,72 +286,121 @@ def bench_prefill(dev, iters: int = 50, M: int = 2048) -> dict:
     w = (torch.randn(K, N, generator=_gen(3)) * 0.02).half().to(dev)
     qw, sc = gemm_int4.quantize_int4_group(w, 128)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
-    ms = GraphTimer(lambda i: _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, out=out),
-                    iters, 2).run(reps=5)
+
+    def once():
+        _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, out=out)
+        return out
+
+    check = check_w4a16(once, a, qw, sc)
+    kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
+    ms = GraphTimer(lambda i: once(), iters, 2).run(reps=5)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return {"workload": "w4a16_prefill_gemm" if M == 2048 else "w4a16_gemm_4096^3", "M": M, "K": K,
-            "N": N, "ms": round(ms, 4),
+            "N": N, "ms": round(ms, 4), "kernel_id": kid, "split": split,
             "value": round(tflops, 1), "unit": "TFLOP/s", "dtype": "fp16 MFMA, fp32 acc",
+            "check": check,
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}}
 
 
-def bench_fp8(dev, iters: int = 50) -> dict:
+def bench_fp8(dev, iters: int = 50, M: int = 4096) -> dict:
+    """fp8 e4m3 GEMM at M x 4096 x 4096 (fp16 out). Checked first: relative Frobenius error of
+    this output against the fp32 product, beside the same error of the reference's own fp8
+    expression ``(a8.float() @ b8.float()) * out_scale`` (tests/test_gemm_fp8.py:24), and a
+    bitwise repeat."""
     import torch
 
     import _pk
     import gemm_fp8
 
-    M = N = K = 4096
+    N = K = 4096
     a = torch.randn(M, K, generator=_gen(4)).half().to(dev)
     b = torch.randn(K, N, generator=_gen(5)).half().to(dev)
     a8, sa = gemm_fp8.quantize(a)
     b8, sb = gemm_fp8.quantize(b)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     scale = 1.0 / (sa * sb)
-    ms = GraphTimer(lambda i: _pk.fp8_gemm(a8, b8, scale, torch.float16, out=out), iters, 2).run(reps=5)
-    tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    # accuracy of this very output vs fp32 (the reference's own metric)
+
+    def once():
+        _pk.fp8_gemm(a8, b8, scale, torch.float16, out=out)
+        return out
+
+    y1 = once().clone()
+    y2 = once().clone()
     ref = a.float() @ b.float()
-    rel = (torch.linalg.norm(out.float() - ref) / torch.linalg.norm(ref)).item()
-    return {"workload": "fp8_e4m3_gemm", "M": M, "K": K, "N": N, "ms": round(ms, 4),
+    rel = rel_fro(y1, ref)
+    rel_expr = rel_fro((a8.float() @ b8.float()) * scale, ref)
+    ok = bool(torch.equal(y1, y2))
+    if not (abs(rel - rel_expr) <= 1e-3 and ok):
+        raise RuntimeError(f"fp8 output check failed before timing: rel={rel:.5f} "
+                           f"reference expression {rel_expr:.5f} bitwise_repeat={ok}")
+    del y1, y2, ref
+    ms = GraphTimer(lambda i: once(), iters, 2).run(reps=5)
+    tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    return {"workload": "fp8_e4m3_gemm" if M == 4096 else "fp8_e4m3_gemm_2048x4096x4096",
+            "M": M, "K": K, "N": N, "ms": round(ms, 4),
             "value": round(tflops, 1), "unit": "TFLOP/s", "dtype": "e4m3 MFMA, fp32 acc",
             "rel_fro_vs_fp32": round(rel, 5),
+            "check": {"rel_fro_vs_fp32": round(rel, 5),
+                      "reference_expr_rel_fro_vs_fp32": round(rel_expr, 5),
+                      "diff_pp": round(100 * (rel - rel_expr), 4), "tolerance_pp": 0.1,
+                      "bitwise_repeat": ok},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
                          "peak": MFMA_F8_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / MFMA_F8_PEAK_TFLOPS, 4)}}
 
 
+SWEEP_LAYERS = (("qkv", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up", 4096, 14336),
+                ("down", 14336, 4096))
+
+
 def bench_llama_sweep(dev, iters: int = 50) -> list:
+    """Llama-3-8B layer sweep: each layer at M = 1, 8, 32, 128, checked,
+    then timed over rotating weight copies (more than 600 MB per layer, at most 40 copies):
+    a graph of max(iters, 2 x copies) calls starting after the warm-up's copies, best of 3
+    replays. ``frac`` is the applicable roof (slower of streaming the bytes at 8 TB/s and
+    issuing the MFMAs at the dense fp16 peak) over the measured time."""
     import torch
 
     import _pk
     import gemm_int4
 
     rows = []
-    for name, K, N in (("qkv", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up", 4096, 14336),
-                       ("down", 14336, 4096)):
+    for name, K, N in SWEEP_LAYERS:
         w = (torch.randn(K, N, generator=_gen(6)) * 0.02).half().to(dev)
         qw, sc = gemm_int4.quantize_int4_group(w, 128)
+        del w
         nrot = max(2, min(N_ROTATE, (600 << 20) // (K * N // 2) + 1))
         qws = [qw] + [qw.clone() for _ in range(nrot - 1)]
         scs = [sc] + [sc.clone() for _ in range(nrot - 1)]
         for M in (1, 8, 32, 128):
             a = torch.randn(M, K, generator=_gen(7)).half().to(dev)
             out = torch.empty((M, N), dtype=torch.float16, device=dev)
-            ms = GraphTimer(lambda i: _pk.w4a16_gemm(a, qws[i % nrot], scs[i % nrot], 128, 1.0,
-                                                     torch.float16, out=out), iters, 2).run()
+
+            def step(i):
+                _pk.w4a16_gemm(a, qws[i % nrot], scs[i % nrot], 128, 1.0, torch.float16,
+                               out=out)
+
+            def once():
+                step(0)
+                return out
+
+            check = check_w4a16(once, a, qw, sc)
+            ms = GraphTimer(step, max(iters, 2 * nrot), 2).run(reps=3)
             by = w4a16_bytes(M, K, N)
             flop = 2.0 * M * N * K
-            # the applicable roof: the slower of streaming the bytes and issuing the MFMAs
             t_hbm = by / (HBM_PEAK_GBS * 1e9)
             t_mfma = flop / (MFMA_F16_PEAK_TFLOPS * 1e12)
+            kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
             rows.append({"layer": name, "M": M, "K": K, "N": N, "us": round(ms * 1e3, 2),
                          "GB/s": round(by / (ms * 1e-3) / 1e9, 1),
                          "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
                          "bound": "hbm" if t_hbm >= t_mfma else "mfma",
-                         "frac": round(max(t_hbm, t_mfma) / (ms * 1e-3), 4)})
+                         "frac": round(max(t_hbm, t_mfma) / (ms * 1e-3), 4),
+                         "kernel_id": kid, "split": split,
+                         "launches": _pk.w4a16_launches(M, N, K, 128, 0), "copies": nrot,
+                         "rel_fro": check["rel_fro_vs_fp32_expr"]})
         del qws, scs
     return rows
 
@@ -336,32 +480,123 @@ def bench_gptq(dev) -> dict:
             "higher_is_better": False, "dtype": "fp32"}
 
 
-def cpu_baseline(a, w, seconds: float) -> dict:
-    """The reference's CPU path for the same GEMV (dequantize with the group scales, then an
-    fp32 matmul), run through the numpy oracle on the host cores for a bounded sample."""
-    import numpy as np
+def cpu_setup() -> dict:
+    """Host threads for the CPU baseline: every core os.cpu_count() reports, capped by
+    OMP_NUM_THREADS where the environment sets one (a shared GPU box's CPU share)."""
+    import torch
 
-    import oracle
+    n = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    torch.set_num_threads(n)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "affinity_cpus": len(os.sched_getaffinity(0)), "cpu_model": model}
 
-    threads = _blas_threads()
-    an = a.numpy()
-    codes, _, s16 = oracle.rtn_group_codes(w.numpy(), 4, 128)
-    packed = oracle.pack_int4_n(codes)
-    K, N = codes.shape
-    nbytes = w4a16_bytes(an.shape[0], K, N)
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        q = oracle.unpack_int4_n(packed)         # dequantize: unpack ...
-        y = oracle.w4a16_ref(an, q, s16, 128)    # ... scale and fp32 matmul
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(nbytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": int(threads),
-            "kind": "port", "sample": f"{reps} full GEMVs (M=1, K=4096, N=11008: unpack + "
-            f"group dequant + fp32 matmul) in {el:.1f} s", "ms_per_step": round(el / reps * 1e3, 2),
-            "check": float(np.abs(y).sum())}
+
+def median_ms(fn, runs: int = 5):
+    """One warm-up call, then the median of `runs` timed calls (ms) and the last result."""
+    import statistics
+
+    fn()
+    ts, r = [], None
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        r = fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts) * 1e3, r
+
+
+def cpu_w4a16(a, qw, sc, y_gpu=None, group: int = 128, runs: int = 5) -> dict:
+    """The reference's CPU path for one W4A16 call, in torch on the host: dequantize
+    (unpack, multiply by the scales repeated over each group), then ``a.float() @ deq``
+    (tests/test_gemm_int4.py:26). Dequant, matmul and the two together are each the median
+    of `runs` after a warm-up. With `y_gpu`, also the GPU output's error against this one."""
+    ac, qc, scc = a.cpu(), qw.cpu(), sc.cpu()
+    M, K = ac.shape
+    N = qc.shape[1] * 8
+    t_deq, deq = median_ms(lambda: dequant_expr(qc, scc, group), runs)
+    t_mm, y = median_ms(lambda: ac.float() @ deq, runs)
+    t_tot, _ = median_ms(lambda: ac.float() @ dequant_expr(qc, scc, group), runs)
+    row = {"M": M, "K": K, "N": N, "dequant_ms": round(t_deq, 3), "matmul_ms": round(t_mm, 3),
+           "total_ms": round(t_tot, 3), "GFLOP/s": round(2.0 * M * N * K / (t_tot * 1e-3) / 1e9, 2),
+           "GB/s": round(w4a16_bytes(M, K, N, group) / (t_tot * 1e-3) / 1e9, 3)}
+    if y_gpu is not None:
+        row["gpu_rel_fro_vs_cpu"] = float(f"{rel_fro(y_gpu.cpu(), y):.3e}")
+    return row
+
+
+def cpu_fp8(a8, b8, scale: float, runs: int = 5) -> dict:
+    """The reference's fp8 CPU path in torch on the host: e4m3 bytes to fp32, fp32 matmul,
+    times the output scale (tests/test_gemm_fp8.py:24); timed like cpu_w4a16."""
+    ac, bc = a8.cpu(), b8.cpu()
+    M, K = ac.shape
+    N = bc.shape[1]
+    t_deq, (af, bf) = median_ms(lambda: (ac.float(), bc.float()), runs)
+    t_mm, _ = median_ms(lambda: (af @ bf) * scale, runs)
+    t_tot, _ = median_ms(lambda: (ac.float() @ bc.float()) * scale, runs)
+    return {"M": M, "K": K, "N": N, "dequant_ms": round(t_deq, 3), "matmul_ms": round(t_mm, 3),
+            "total_ms": round(t_tot, 3),
+            "GFLOP/s": round(2.0 * M * N * K / (t_tot * 1e-3) / 1e9, 2)}
+
+
+def cpu_baseline_table(dev, gemv_inputs_dev) -> dict:
+    """The four rows of the CPU baseline table: W4A16 16x1024x1024 (the reference's CPU
+    plumbing config), 1x4096x11008 (the headline's own inputs), 2048x4096x4096 (the prefill
+    line's seeds) and fp8 4096^3 (the fp8 line's seeds). Codes and scales come from this
+    library's quantization on the GPU, copied to the host; only dequant + matmul is timed."""
+    import torch
+
+    import _pk
+    import gemm_fp8
+    import gemm_int4
+
+    info = cpu_setup()
+    rows = {}
+    a = torch.randn(16, 1024, generator=_gen(0)).half().to(dev)
+    w = (torch.randn(1024, 1024, generator=_gen(1)) * 0.02).half().to(dev)
+    qw, sc = gemm_int4.quantize_int4_group(w, 128)
+    y = _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16)
+    rows["w4a16_16x1024x1024"] = cpu_w4a16(a, qw, sc, y)
+    ag, qw, sc = gemv_inputs_dev
+    y = _pk.w4a16_gemm(ag, qw, sc, 128, 1.0, torch.float16)
+    rows["w4a16_1x4096x11008"] = cpu_w4a16(ag, qw, sc, y)
+    a = torch.randn(2048, 4096, generator=_gen(2)).half().to(dev)
+    w = (torch.randn(4096, 4096, generator=_gen(3)) * 0.02).half().to(dev)
+    qw, sc = gemm_int4.quantize_int4_group(w, 128)
+    y = _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16)
+    rows["w4a16_2048x4096x4096"] = cpu_w4a16(a, qw, sc, y)
+    a8, sa = gemm_fp8.quantize(torch.randn(4096, 4096, generator=_gen(4)).half().to(dev))
+    b8, sb = gemm_fp8.quantize(torch.randn(4096, 4096, generator=_gen(5)).half().to(dev))
+    rows["fp8_4096^3"] = cpu_fp8(a8, b8, 1.0 / (sa * sb))
+    return {**info, "rows": rows}
+
+
+def cpu_baseline_decode() -> dict:
+    """The reference's single-query attention (eager_decode, flash_decoding.py:118-125) in
+    torch on the host, on 8 of the 256 (b, h) pairs of the bench shape (N = 8192, D = 128);
+    GB/s of fp16 K/V those pairs hold, median of 5 after a warm-up."""
+    import torch
+
+    import flash_decoding
+
+    H, N, D = 8, 8192, 128
+    q = torch.randn(1, H, 1, D, generator=_gen(30)).half()
+    k = torch.randn(1, H, N, D, generator=_gen(31)).half()
+    v = torch.randn(1, H, N, D, generator=_gen(32)).half()
+    ms, _ = median_ms(lambda: flash_decoding.eager_decode(q, k, v))
+    return {"value": round(flash_decode_bytes(1, H, N, D) / (ms * 1e-3) / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"eager_decode on 1x{H}x{N}x{D} (8 of the 256 heads): median of 5, {ms:.2f} ms"}
 
 
 def _blas_threads() -> int:
@@ -372,73 +607,6 @@ def _blas_threads() -> int:
                         if p.get("user_api") == "blas"), default=1))
     except Exception:  # threadpoolctl missing: numpy's BLAS default
         return os.cpu_count() or 1
-
-
-def cpu_baseline_gemm(kind: str, seconds: float) -> dict:
-    """The reference's CPU path for the GEMM lines, full size, through the numpy oracle:
-    W4A16 2048x4096x4096 = unpack + group dequantize + fp32 matmul of the same seeded inputs
-    as bench_prefill; fp8 4096^3 = the e4m3 bytes decoded to fp32, fp32 matmul, out_scale
-    (the test-path oracle, tests/test_gemm_fp8.py:24). Repeated for about `seconds`."""
-    import numpy as np
-    import torch
-
-    import oracle
-
-    if kind == "w4a16":
-        M, K, N = 2048, 4096, 4096
-        a = torch.randn(M, K, generator=_gen(2)).half().numpy()
-        w = (torch.randn(K, N, generator=_gen(3)) * 0.02).half().numpy()
-        codes, _, s16 = oracle.rtn_group_codes(w, 4, 128)
-        packed = oracle.pack_int4_n(codes)
-
-        def run():
-            return oracle.w4a16_ref(a, oracle.unpack_int4_n(packed), s16, 128)
-    else:
-        M = N = K = 4096
-        a8, sa = oracle.fp8_quantize(torch.randn(M, K, generator=_gen(4)).half().numpy())
-        b8, sb = oracle.fp8_quantize(torch.randn(K, N, generator=_gen(5)).half().numpy())
-
-        def run():
-            return oracle.fp8_gemm_ref(a8, sa, b8, sb)
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        y = run()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    flop = 2.0 * M * N * K
-    return {"value": round(flop * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": _blas_threads(),
-            "kind": "port", "sample": f"{reps} full {M}x{K}x{N} products ({'unpack + group dequant' if kind == 'w4a16' else 'e4m3 decode'} + fp32 matmul) in {el:.1f} s",
-            "ms_per_step": round(el / reps * 1e3, 1), "check": float(np.abs(y).sum())}
-
-
-def cpu_baseline_decode(seconds: float) -> dict:
-    """The reference's single-query attention (eager_decode, flash_decoding.py:126-133) on the
-    host through the float64 oracle, on 8 of the 256 (b, h) pairs of the bench shape
-    (N = 8192, D = 128); GB/s of fp16 K/V those pairs hold."""
-    import numpy as np
-    import torch
-
-    import oracle
-
-    H, N, D = 8, 8192, 128
-    q = torch.randn(1, H, 1, D, generator=_gen(30)).half().numpy()
-    k = torch.randn(1, H, N, D, generator=_gen(31)).half().numpy()
-    v = torch.randn(1, H, N, D, generator=_gen(32)).half().numpy()
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        y = oracle.decode_attention_ref(q, k, v)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(flash_decode_bytes(1, H, N, D) * reps / el / 1e9, 3), "unit": "GB/s",
-            "cores": _blas_threads(), "kind": "port",
-            "sample": f"{reps} calls of 1x{H}x{N}x{D} (8 of the 256 heads) in {el:.1f} s",
-            "check": float(np.abs(y).sum())}
 
 
 def cpu_baseline_gptq(seconds: float) -> dict:
@@ -504,7 +672,7 @@ def traffic_probe(dev) -> int:
 
 def mfma_probe(dev) -> int:
     """Eager launches (no graph) of the GEMMs whose MFMA utilisation is read with rocprofv3
-    --pmc: W4A16 prefill 2048x4096x4096 and 4096^3, fp8 4096^3 (fp16 out), 5 calls each."""
+    --pmc: W4A16 and fp8 GEMMs (fp16 out) at 2048x4096x4096 and 4096^3, 5 calls each."""
     import torch
 
     import _pk
@@ -518,13 +686,14 @@ def mfma_probe(dev) -> int:
         out = torch.empty((M, 4096), dtype=torch.float16, device=dev)
         for _ in range(5):
             _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, out=out)
-    a = torch.randn(4096, 4096, generator=_gen(4)).half().to(dev)
-    b = torch.randn(4096, 4096, generator=_gen(5)).half().to(dev)
-    a8, sa = gemm_fp8.quantize(a)
-    b8, sb = gemm_fp8.quantize(b)
-    out = torch.empty((4096, 4096), dtype=torch.float16, device=dev)
-    for _ in range(5):
-        _pk.fp8_gemm(a8, b8, 1.0 / (sa * sb), torch.float16, out=out)
+    for M in (2048, 4096):
+        a = torch.randn(M, 4096, generator=_gen(4)).half().to(dev)
+        b = torch.randn(4096, 4096, generator=_gen(5)).half().to(dev)
+        a8, sa = gemm_fp8.quantize(a)
+        b8, sb = gemm_fp8.quantize(b)
+        out = torch.empty((M, 4096), dtype=torch.float16, device=dev)
+        for _ in range(5):
+            _pk.fp8_gemm(a8, b8, 1.0 / (sa * sb), torch.float16, out=out)
     torch.cuda.synchronize()
     print("mfma probe done", flush=True)
     return 0
@@ -639,8 +808,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true", help="skip the GEMM lines")
-    ap.add_argument("--sweep", action="store_true", help="add the Llama-3-8B layer sweep")
-    ap.add_argument("--only", choices=("prefill", "gemm4096", "fp8", "flash_decode", "gptq"),
+    ap.add_argument("--no-sweep", action="store_true", help="skip the Llama-3-8B layer sweep")
+    ap.add_argument("--only", choices=("prefill", "gemm4096", "fp8", "fp8_2048", "flash_decode",
+                                       "gptq", "sweep"),
                     help="run one secondary workload alone and print its JSON (for profiling)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only run eager GEMM calls for rocprofv3 --pmc MFMA utilisation")
@@ -685,7 +855,9 @@ def main() -> int:
         return 0
     if args.only:
         fn = {"prefill": bench_prefill, "gemm4096": lambda d: bench_prefill(d, M=4096),
-              "fp8": bench_fp8, "flash_decode": bench_flash_decode, "gptq": bench_gptq}[args.only]
+              "fp8": bench_fp8, "fp8_2048": lambda d: bench_fp8(d, M=2048),
+              "flash_decode": bench_flash_decode, "gptq": bench_gptq,
+              "sweep": lambda d: {"llama3_8b_sweep": bench_llama_sweep(d)}}[args.only]
         print(json.dumps(fn(dev)), flush=True)
         return 0
 
@@ -704,11 +876,17 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4 weights (group 128, fp16 scales) x fp16 activations, fp32 accumulate",
-        "data": "synthetic: seeded CPU generator, A ~ N(0,1) fp16, W ~ N(0,0.02) int4-quantized; "
-                f"{N_ROTATE} rotating weight copies (> 2x Infinity Cache)",
+        "data": "synthetic: seeded CPU generator, A ~ N(0,1) fp16, W ~ N(0,0.02) int4-quantized "
+                f"(group 128); {N_ROTATE} copies of the packed weights and scales rotated "
+                f"({N_ROTATE * g['bytes'] / 1e6:.0f} MB > 2x the 256 MB Infinity Cache): warm-up "
+                f"reads copies 0..{args.warmup - 1}, the timed graph {g['steps_timed']} calls "
+                f"from copy {max(args.warmup, 1) % N_ROTATE} on, best of 3 replays",
         "config": {"workload": "w4a16_decode_gemv", "M": g["M"], "K": g["K"], "N": g["N"],
                    "group_size": 128, "split_k": g["split"], "out_dtype": "fp16",
                    "split_k_sweep_GBs": g["split_sweep_GBs"]},
+        "steps_timed": g["steps_timed"],
+        "check": g["check"],
+        "host": g["host"],
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
@@ -721,20 +899,33 @@ def main() -> int:
     }
     if not args.no_secondary:
         result["secondary"] = [bench_prefill(dev), bench_prefill(dev, M=4096), bench_fp8(dev),
-                               bench_flash_decode(dev), bench_gptq(dev)]
-    if args.sweep:
+                               bench_fp8(dev, M=2048), bench_flash_decode(dev), bench_gptq(dev)]
+    if not args.no_sweep:
         result["llama3_8b_sweep"] = bench_llama_sweep(dev)
     if not args.no_cpu_baseline:
-        a, w = g["inputs"]
-        result["cpu_baseline"] = cpu_baseline(a, w, args.cpu_seconds)
+        table = cpu_baseline_table(dev, g["inputs"])
+        head = table["rows"]["w4a16_1x4096x11008"]
+        result["cpu_baseline"] = {
+            "value": head["GB/s"], "unit": "GB/s", "cores": table["torch_threads"], "kind": "port",
+            "sample": "the reference's CPU path in torch on the host (unpack + group dequant, then "
+                      "a.float() @ deq) on the headline's own inputs: median of 5 after a warm-up, "
+                      f"dequant {head['dequant_ms']} ms + matmul {head['matmul_ms']} ms, "
+                      f"together {head['total_ms']} ms",
+            "ms_per_step": head["total_ms"], "table": table}
         if not args.no_secondary:  # the reference's CPU path beside the GEMM lines too
             for entry in result["secondary"]:
                 if entry["workload"] == "w4a16_prefill_gemm":
-                    entry["cpu_baseline"] = cpu_baseline_gemm("w4a16", args.cpu_seconds / 3)
+                    r = table["rows"]["w4a16_2048x4096x4096"]
+                    entry["cpu_baseline"] = {"value": round(r["GFLOP/s"] / 1e3, 4), "unit": "TFLOP/s",
+                                             "cores": table["torch_threads"], "kind": "port",
+                                             "sample": f"torch dequant + fp32 matmul, median of 5: {r['total_ms']} ms"}
                 elif entry["workload"] == "fp8_e4m3_gemm":
-                    entry["cpu_baseline"] = cpu_baseline_gemm("fp8", args.cpu_seconds / 3)
+                    r = table["rows"]["fp8_4096^3"]
+                    entry["cpu_baseline"] = {"value": round(r["GFLOP/s"] / 1e3, 4), "unit": "TFLOP/s",
+                                             "cores": table["torch_threads"], "kind": "port",
+                                             "sample": f"torch e4m3->fp32 + fp32 matmul, median of 5: {r['total_ms']} ms"}
                 elif entry["workload"] == "split_kv_decode_attention":
-                    entry["cpu_baseline"] = cpu_baseline_decode(args.cpu_seconds / 6)
+                    entry["cpu_baseline"] = cpu_baseline_decode()
                 elif entry["workload"] == "gptq_layer":
                     entry["cpu_baseline"] = cpu_baseline_gptq(args.cpu_seconds / 6)
     print(json.dumps(result), flush=True)
