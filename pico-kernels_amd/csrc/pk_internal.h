@@ -58,6 +58,9 @@ struct SkinnyPlan {
 };
 bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out);
 bool skinny_fits(int M, int N, int K, int64_t lda, int64_t ldq, int group, bool has_gs);
+// Split-K of the skinny kernel adds its slices in L2 inside the launch (one launch).
+bool skinny_l2(const SkinnyPlan& pl);
+size_t skinny_workspace_bytes(const SkinnyPlan& pl, int M, int N);
 int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
                   int64_t ldq, const void* scales, int group, float tensor_scale, void* c,
                   int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,

@@ -1,9 +1,9 @@
 // C ABI for the W4A16 matmul (gemm_int4.int4_gemm + the group-128 / split-K path) and the
 // dense fp16 split-K matmul (gemm_splitk.triton_gemm_splitk).
 //
-// Dispatch: M <= 4 runs the HBM-bound GEMV (w4a16_gemv.hip); 5 <= M <= 64 (<= 128 for layers
-// of at most 4096 x 4096 weights) the register-dequant MFMA kernel (w4a16_skinny.hip); larger
-// M the MFMA GEMM that dequantises B into LDS. All honour an explicit split_k.
+// Dispatch: M <= 4 runs the HBM-bound GEMV (w4a16_gemv.hip); up to 64 rows (128 for layers of
+// at most 4096 x 4096 weights) the register-dequant MFMA kernel (w4a16_skinny.hip); larger M
+// the MFMA GEMMs (B packed in LDS, or dequantised into LDS). All honour an explicit split_k.
 #include "pk_internal.h"
 
 #include <atomic>
@@ -73,8 +73,11 @@ int plan_split(const W4Plan& pl) {
 
 size_t plan_ws(const W4Plan& pl, int M, int N) {
   if (pl.kernel == kKernelGemv) return gemv_workspace_bytes(pl.gemv, M, N);
-  // the skinny kernel (or its GEMM fallback, planned with the same split) needs the same
-  return gemm_workspace_bytes(pl.gemm, M, N);
+  const size_t g = gemm_workspace_bytes(pl.gemm, M, N);
+  if (pl.kernel != kKernelSkinny) return g;
+  // the skinny kernel's tile-padded partials, or its GEMM fallback's (same split)
+  const size_t k = skinny_workspace_bytes(pl.skinny, M, N);
+  return k > g ? k : g;
 }
 
 int plan_launch(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
@@ -122,8 +125,9 @@ extern "C" int pk_w4a16_launches(int M, int N, int K, int group_size, int split_
   }
   const int split = plan_split(pl);
   if (split <= 1) return 1;
-  const bool l2 = splitk_in_l2_ok() && pl.kernel == kKernelGemv && pl.gemv.mfma &&
-                  pl.gemv.tiles <= kWsMaxTiles;
+  const bool l2 = pl.kernel == kKernelGemv
+                      ? splitk_in_l2_ok() && pl.gemv.mfma && pl.gemv.tiles <= kWsMaxTiles
+                      : pl.kernel == kKernelSkinny && skinny_l2(pl.skinny);
   return l2 ? 1 : 2;
 }
 

@@ -269,10 +269,10 @@ __global__ __launch_bounds__(kGemvCW* RL) void w4a16_gemv_kernel(GemvParams p) {
 constexpr int kMfmaRows = 256;  // rows per workgroup = slice length
 constexpr int kMfmaSeg = 36;    // LDS floats per 32-column segment (padding spreads banks)
 
-// Occupancy hint: four workgroups per CU for M = 1 with one row block (three for the
-// per-tensor variant of the one-launch form, which would otherwise spill), else fewer.
+// Occupancy hint: four workgroups per CU with one row block (three for the per-tensor
+// variant of the one-launch form at M = 1, which would otherwise spill), else three.
 template <int MT, bool HAS_GS, bool L2SPLIT, int RB>
-__global__ __launch_bounds__(256, MT == 1 ? (RB == 1 && (HAS_GS || !L2SPLIT) ? 4 : 3) : 2)
+__global__ __launch_bounds__(256, RB == 1 && (MT > 1 || HAS_GS || !L2SPLIT) ? 4 : 3)
 void w4a16_gemv_mfma_kernel(GemvParams p) {
   constexpr int NW = 4;
   constexpr int WROWS = 64 * RB;  // rows per wave: RB blocks of 64, chained through the MFMAs
@@ -325,7 +325,19 @@ void w4a16_gemv_mfma_kernel(GemvParams p) {
   }
   const pk_f4 cin_lo = -coff;
   const pk_f4 cin_raw = coff * -17.0f;
-  float lo_out[MT][16], hi_out[MT][16];  // byte column jb = tile columns 2jb (lo), 2jb+1 (hi)
+  // One row keeps all 16 byte columns of its sums in registers to the end; more rows leave
+  // each j4's 4 byte columns in LDS as soon as they are complete, which keeps the live
+  // registers (and so the waves per SIMD) at the one-row level.
+  constexpr int JB = MT == 1 ? 16 : 4;
+  __shared__ float red[NW][2][MT][8 * kMfmaSeg];
+  const int par = lane >> 5;
+  const bool valid = ((lane & 15) >> 3) == par && ((lane >> 4) & 1) == 0;  // lanes 0-7, 40-47
+  float lo_out[MT][JB], hi_out[MT][JB];  // byte column jb = tile columns 2jb (lo), 2jb+1 (hi)
+  // byte columns 2q, 2q+1 = tile columns 4q..4q+3 of the lane's 32-column chunk
+  auto quad = [&](int r, int q) {
+    const int j = MT == 1 ? 2 * q : 2 * (q & 1);
+    return pk_f4{lo_out[r][j], hi_out[r][j], lo_out[r][j + 1], hi_out[r][j + 1]};
+  };
 #pragma unroll
   for (int j4 = 0; j4 < 4; ++j4) {
     uint32_t wx[RB][8];
@@ -350,25 +362,27 @@ void w4a16_gemv_mfma_kernel(GemvParams p) {
       }
 #pragma unroll
       for (int r = 0; r < MT; ++r) {
-        lo_out[r][4 * j4 + b] = clo[r];
-        hi_out[r][4 * j4 + b] = craw[r] - clo[r];
+        lo_out[r][MT == 1 ? 4 * j4 + b : b] = clo[r];
+        hi_out[r][MT == 1 ? 4 * j4 + b : b] = craw[r] - clo[r];
+      }
+    }
+    if constexpr (MT > 1) {
+      if (valid) {
+#pragma unroll
+        for (int r = 0; r < MT; ++r)
+#pragma unroll
+          for (int q = 2 * j4; q < 2 * j4 + 2; ++q)
+            *reinterpret_cast<pk_f4*>(&red[wave][par][r][cl * kMfmaSeg + 4 * q]) = quad(r, q);
       }
     }
   }
 
-  // ---- lanes whose C rows are complete write them; fold parities and waves -----------
-  __shared__ float red[NW][2][MT][8 * kMfmaSeg];
-  {
-    const int par = lane >> 5;
-    const bool valid = ((lane & 15) >> 3) == par && ((lane >> 4) & 1) == 0;  // lanes 0-7, 40-47
+  // ---- fold parities and waves -------------------------------------------------------------
+  if constexpr (MT == 1) {
     if (valid) {
 #pragma unroll
-      for (int r = 0; r < MT; ++r)
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const pk_f4 v = {lo_out[r][2 * q], hi_out[r][2 * q], lo_out[r][2 * q + 1], hi_out[r][2 * q + 1]};
-          *reinterpret_cast<pk_f4*>(&red[wave][par][r][cl * kMfmaSeg + 4 * q]) = v;
-        }
+      for (int q = 0; q < 8; ++q)
+        *reinterpret_cast<pk_f4*>(&red[wave][par][0][cl * kMfmaSeg + 4 * q]) = quad(0, q);
     }
   }
   __syncthreads();
@@ -400,13 +414,34 @@ __device__ __forceinline__ void gemv_finish_l2(const GemvParams& p, int tile, in
     if (m < p.M) p.partials[((int64_t)slice * p.M + m) * p.npad + col] = mine[m];
   }
   if (!splitk_arrive(p.counters + 32 * tile, p.split)) return;
-  if (col >= p.N) return;
+  if constexpr (MT == 1) {
+    if (col >= p.N) return;
+    const float v = splitk_sum(p.partials + col, (int64_t)p.M * p.npad, p.split, slice, mine[0]);
+    store_from_f32(p.c, p.c_dtype, col, v * p.tensor_scale);
+  } else {
+    // Several rows: quads of 4 columns, all slices of a quad loaded at once (16 at a time),
+    // so the last workgroup waits for ceil(MT / 4) rounds of loads, not MT.
+    const int64_t plane = (int64_t)p.M * p.npad;
+    for (int qi = t; qi < MT * (kGemvTileCols / 4); qi += 256) {
+      const int m = qi / (kGemvTileCols / 4), c = tile * kGemvTileCols + (qi % (kGemvTileCols / 4)) * 4;
+      if (m >= p.M || c >= p.N) continue;  // N % 32 == 0: whole quads
+      const float* src = p.partials + (int64_t)m * p.npad + c;
+      pk_f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int s0 = 0; s0 < p.split; s0 += 16) {
+        pk_f4 pv[16];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    if (m >= p.M) break;
-    const float v = splitk_sum(p.partials + (int64_t)m * p.npad + col, (int64_t)p.M * p.npad,
-                               p.split, slice, mine[m]);
-    store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + col, v * p.tensor_scale);
+        for (int u = 0; u < 16; ++u)
+          pv[u] = *reinterpret_cast<const pk_f4*>(src + (int64_t)min(s0 + u, p.split - 1) * plane);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (s0 + u == 0) v = pv[0];
+          else if (s0 + u < p.split) v += pv[u];
+        }
+      }
+      const int64_t o = (int64_t)m * p.ldc + c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) store_from_f32(p.c, p.c_dtype, o + e, v[e] * p.tensor_scale);
+    }
   }
 }
 
@@ -519,6 +554,19 @@ static void launch_gemv_mfma(const GemvParams& p, int tiles, int rb, hipStream_t
   else launch_gemv_mfma_rb<MT, 1>(p, tiles, s, l2split);
 }
 
+// The MFMA kernel applies: 256- or 512-row slices within one group, 16-byte aligned operands
+// with whole-uint4 rows, and buffers addressable with 32-bit offsets.
+static bool gemv_mfma_ready(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
+                            int64_t ldq, const void* scales, int group, int M, int N, int K) {
+  const int rb = pl.mfma;
+  const bool vec = (reinterpret_cast<uintptr_t>(qw) & 15) == 0 && ldq % 4 == 0 && N % 32 == 0 &&
+                   (scales == nullptr || (reinterpret_cast<uintptr_t>(scales) & 15) == 0);
+  return rb >= 1 && pl.k_slice == kMfmaRows * rb && K % (kMfmaRows * rb) == 0 &&
+         (scales == nullptr || group % (64 * rb) == 0) && vec &&
+         (reinterpret_cast<uintptr_t>(a) & 15) == 0 && lda % 8 == 0 &&
+         (int64_t)K * ldq * 4 < (1ll << 31) && (int64_t)M * lda * 2 < (1ll << 31);
+}
+
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
                 int64_t ldq, const void* scales, int group, float tensor_scale, void* c,
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace,
@@ -545,13 +593,8 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
   p.counters = nullptr;
   p.tiles = pl.tiles;
   p.npad = pl.tiles * kGemvTileCols;
-  // buffer offsets are 32-bit: the MFMA kernel needs the weights and activations below 2 GiB
   const int rb = pl.mfma;
-  const bool mfma = rb >= 1 && pl.k_slice == kMfmaRows * rb && K % (kMfmaRows * rb) == 0 &&
-                    (scales == nullptr || group % (64 * rb) == 0) && p.vec_ok &&
-                    (reinterpret_cast<uintptr_t>(a) & 15) == 0 &&
-                    lda % 8 == 0 && (int64_t)K * ldq * 4 < (1ll << 31) &&
-                    (int64_t)M * lda * 2 < (1ll << 31);
+  const bool mfma = gemv_mfma_ready(pl, a, lda, qw, ldq, scales, group, M, N, K);
   if (mfma) {
     // Slices hand off through L2 unless the caller wants the partials themselves.
     const bool l2split = pl.split > 1 && !partials_only && pl.tiles <= kWsMaxTiles &&

@@ -31,12 +31,15 @@
 // A wave's rows lie in one quantisation group, so its fp32 result is scaled once per column
 // at the end (exact powers of two folded into the scale).
 //
-// Reduction: the waves' tiles are added in LDS in a fixed order; with split-K every slice
-// writes (split, M, N) fp32 partials and splitk_reduce_kernel adds them in slice order, so
-// results are bitwise reproducible, and equal for both tile widths at one wave count.
-// (Adding the slices through one XCD's L2 inside this kernel, as the M <= 4 GEMV does, was
-// measured slower here for every split: the last workgroup of a tile has M * split partials
-// per thread to gather.)
+// Reduction: the waves' tiles are added in LDS in a fixed order. With split-K and one 16-row
+// block the slices of a column tile hand off through one XCD's L2 inside the launch, as the
+// M <= 4 GEMV does: a 1-D grid places the split * row_parts workgroups of a tile on one XCD
+// (xcd = workgroup id mod 8), each writes its fp32 partial block, waits for the stores and
+// bumps the tile's arrival counter; the last to arrive adds the split partials in slice order
+// 0..split-1 -- the arithmetic of splitk_reduce_kernel, so the result is bitwise that of the
+// two-launch form -- and stores C. More rows, the partials-only entry point, and partitions
+// whose XCD count does not divide 8 (or PK_SPLITK_IN_L2=0) write (split, M, N) partials
+// that splitk_reduce_kernel adds in a second launch.
 #include <cstdio>
 #include <cstdlib>
 
@@ -61,7 +64,9 @@ struct SkinnyParams {
   int M, N, K;
   int split, k_slice;
   int tiles, row_parts;
-  float* partials;  // (split, M, N) fp32 when split > 1
+  float* partials;  // (split, M, N) fp32 when split > 1; (split, M, npad) in the L2 handoff
+  unsigned* counters;  // arrival counters of the L2 handoff, one 128-byte line per (tile, part)
+  int npad;            // tiles * tile columns
 };
 
 template <int MB, int WPL>
@@ -73,7 +78,7 @@ struct SkStep {
 // MB: 16-row activation blocks per workgroup; CPL: columns per lane (16: 8-byte weight loads,
 // 256-column tiles; 8: 4-byte loads, 128-column tiles, half the accumulators per block);
 // NW: waves per workgroup, each taking 1/NW of the slice's rows.
-template <int MB, int CPL, int NW, bool HAS_GS, int PD, int OCC>
+template <int MB, int CPL, int NW, bool HAS_GS, int PD, int OCC, bool L2>
 __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams p) {
   constexpr int TC = 16 * CPL;  // tile columns
   constexpr int WPL = CPL / 8;  // words per lane and row
@@ -82,10 +87,20 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int j = lane & 15, g = lane >> 4;
   // Row parts of one (tile, slice) are blocks b and b + 8: the same XCD, dispatched close
-  // together, so the second part's weight reads hit that XCD's L2.
-  const int bx = blockIdx.x, slice = blockIdx.y;
-  const int part = (bx >> 3) % p.row_parts;
-  const int tile = (bx / (8 * p.row_parts)) * 8 + (bx & 7);
+  // together, so the second part's weight reads hit that XCD's L2. In the one-launch split-K
+  // form the 1-D grid also keeps every slice of a tile on that XCD.
+  int part, tile, slice;
+  if constexpr (L2) {
+    const int b = blockIdx.x, jj = b >> 3, per = p.split * p.row_parts;
+    tile = (b & 7) + 8 * (jj / per);
+    slice = (jj % per) / p.row_parts;
+    part = (jj % per) % p.row_parts;
+  } else {
+    const int bx = blockIdx.x;
+    slice = blockIdx.y;
+    part = (bx >> 3) % p.row_parts;
+    tile = (bx / (8 * p.row_parts)) * 8 + (bx & 7);
+  }
   if (tile >= p.tiles) return;
   const int m0 = part * MB * 16;
   const int words_total = p.N >> 3;
@@ -247,6 +262,50 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
   }
   __syncthreads();
   const int rows = min(MB * 16, p.M - m0);
+  if constexpr (L2) {
+    // Quads of 4 columns, QPT per thread: this slice's partial block, then (last workgroup of
+    // the tile) the slices' sum in slice order.
+    constexpr int QPR = TC / 4;  // quads per row
+    constexpr int QPT = MB * 16 * QPR / (64 * NW);
+    static_assert(QPT >= 1 && (MB * 16 * QPR) % (64 * NW) == 0, "quads per thread");
+    const int64_t plane = (int64_t)p.M * p.npad;
+    float* const blk = p.partials + (int64_t)m0 * p.npad + tile * TC;
+    pk_f4 own[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int qi = t + i * 64 * NW, m = qi / QPR, c4 = (qi % QPR) * 4;
+      auto rq = [&](int nb) { return *reinterpret_cast<const pk_f4*>(&red[nb][m][c4]); };
+      if constexpr (NB == 2) own[i] = rq(0) + rq(1);
+      else own[i] = (rq(0) + rq(2)) + (rq(1) + rq(3));
+      if (m < rows) *reinterpret_cast<pk_f4*>(blk + slice * plane + (int64_t)m * p.npad + c4) = own[i];
+    }
+    if (!splitk_arrive(p.counters + 32 * (tile * p.row_parts + part), p.split)) return;
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int qi = t + i * 64 * NW, m = qi / QPR, c4 = (qi % QPR) * 4;
+      const int col = tile * TC + c4;
+      if (m >= rows || col >= p.N) continue;
+      const float* src = blk + (int64_t)m * p.npad + c4;
+      pk_f4 v = own[i];
+      for (int s0 = 0; s0 < p.split; s0 += 8) {
+        pk_f4 pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int sl = min(s0 + u, p.split - 1);
+          pv[u] = sl == slice ? own[i] : *reinterpret_cast<const pk_f4*>(src + sl * plane);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (s0 + u == 0) v = pv[0];
+          else if (s0 + u < p.split) v += pv[u];
+        }
+      }
+      const int64_t o = (int64_t)(m0 + m) * p.ldc + col;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) store_from_f32(p.c, p.c_dtype, o + e, v[e] * p.tensor_scale);
+    }
+    return;
+  }
   for (int idx = t; idx < rows * TC; idx += 64 * NW) {
     const int m = idx / TC, cl = idx % TC;
     const int col = tile * TC + cl;
@@ -344,33 +403,56 @@ bool skinny_fits(int M, int N, int K, int64_t lda, int64_t ldq, int group, bool 
 }
 
 template <int MB, int CPL, int NW, bool GS>
-static void launch_skinny_t(const SkinnyParams& p, hipStream_t s) {
+static void launch_skinny_t(const SkinnyParams& p, bool l2, hipStream_t s) {
   // k-steps in flight per wave, measured on the Llama-3-8B shapes: 3 for one 16-row block of
   // 16 columns per lane (162 VGPRs, three waves per SIMD; 2-3% faster than 4 at two waves),
   // 2 for two blocks; 8 columns per lane halve the weight registers.
   constexpr int PD = CPL == 16 ? (MB == 1 ? 3 : 2) : (MB == 1 ? 4 : MB == 2 ? 3 : 2);
   constexpr int OCC = NW == 4 ? 2 : 1;
+  if (l2) {
+    const unsigned gx = (unsigned)(cdiv(p.tiles, 8) * 8 * p.split * p.row_parts);
+    w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, true><<<gx, 64 * NW, 0, s>>>(p);
+    return;
+  }
   const unsigned gx = p.row_parts == 1 ? (unsigned)p.tiles
                                        : (unsigned)(cdiv(p.tiles, 8) * 8 * p.row_parts);
-  w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC><<<dim3(gx, p.split), 64 * NW, 0, s>>>(p);
+  w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, false><<<dim3(gx, p.split), 64 * NW, 0, s>>>(p);
 }
 
 template <int MB, int CPL, bool GS>
-static void launch_skinny_nw(const SkinnyParams& p, int nw, hipStream_t s) {
-  if (nw == 8) launch_skinny_t<MB, CPL, 8, GS>(p, s);
-  else launch_skinny_t<MB, CPL, 4, GS>(p, s);
+static void launch_skinny_nw(const SkinnyParams& p, int nw, bool l2, hipStream_t s) {
+  if (nw == 8) launch_skinny_t<MB, CPL, 8, GS>(p, l2, s);
+  else launch_skinny_t<MB, CPL, 4, GS>(p, l2, s);
 }
 
 template <bool GS>
-static void launch_skinny_cfg(const SkinnyPlan& pl, const SkinnyParams& p, hipStream_t s) {
+static void launch_skinny_cfg(const SkinnyPlan& pl, const SkinnyParams& p, bool l2, hipStream_t s) {
   if (pl.cpl == 16) {
-    if (pl.mb == 1) launch_skinny_nw<1, 16, GS>(p, pl.nw, s);
-    else launch_skinny_nw<2, 16, GS>(p, pl.nw, s);
+    if (pl.mb == 1) launch_skinny_nw<1, 16, GS>(p, pl.nw, l2, s);
+    else launch_skinny_nw<2, 16, GS>(p, pl.nw, l2, s);
   } else {
-    if (pl.mb == 1) launch_skinny_nw<1, 8, GS>(p, pl.nw, s);
-    else if (pl.mb == 2) launch_skinny_nw<2, 8, GS>(p, pl.nw, s);
-    else launch_skinny_nw<4, 8, GS>(p, pl.nw, s);
+    if (pl.mb == 1) launch_skinny_nw<1, 8, GS>(p, pl.nw, l2, s);
+    else if (pl.mb == 2) launch_skinny_nw<2, 8, GS>(p, pl.nw, l2, s);
+    else launch_skinny_nw<4, 8, GS>(p, pl.nw, l2, s);
   }
+}
+
+// The split-K slices hand off through L2 in the launch (no reduce launch) for one 16-row
+// block. Measured on the Llama-3-8B layers (graphs over rotating weights): M = 8 gains about
+// 1 us on every layer (qkv 11.3 -> 10.3, o_proj 9.4 -> 8.2, gate_up 15.1 -> 14.3, down
+// 15.9 -> 14.8 us); with two or four blocks the last workgroup's gather of M * split
+// partials per tile was slower on the larger layers (gate_up M = 32: 22.3 against 21.5 us,
+// down M = 32: 25.9 against 22.6), so those keep the reduce launch.
+bool skinny_l2(const SkinnyPlan& pl) {
+  return pl.split > 1 && pl.mb == 1 && pl.tiles * pl.row_parts <= kWsMaxTiles &&
+         splitk_in_l2_ok();
+}
+
+size_t skinny_workspace_bytes(const SkinnyPlan& pl, int M, int N) {
+  if (pl.split <= 1) return 0;
+  const size_t flat = (size_t)pl.split * M * N * sizeof(float);
+  const size_t padded = (size_t)pl.split * M * pl.tiles * 16 * pl.cpl * sizeof(float);
+  return kWsCounterBytes + (flat > padded ? flat : padded);
 }
 
 int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
@@ -396,10 +478,13 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
   p.tiles = pl.tiles;
   p.row_parts = pl.row_parts;
   p.partials = pl.split > 1 ? split_partials(workspace, partials_only) : nullptr;
-  if (scales) launch_skinny_cfg<true>(pl, p, s);
-  else launch_skinny_cfg<false>(pl, p, s);
+  p.counters = ws_counters(workspace);
+  p.npad = pl.tiles * 16 * pl.cpl;
+  const bool l2 = !partials_only && skinny_l2(pl);
+  if (scales) launch_skinny_cfg<true>(pl, p, l2, s);
+  else launch_skinny_cfg<false>(pl, p, l2, s);
   PK_LAUNCH_CHECK("w4a16 skinny");
-  if (pl.split > 1 && !partials_only)
+  if (pl.split > 1 && !partials_only && !l2)
     return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);
   return PK_OK;
 }

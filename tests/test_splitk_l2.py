@@ -1,9 +1,9 @@
-"""Split-K slices that hand off through one XCD's L2 (the GEMV for M <= 4): the one-launch
-result must equal, bit for bit, the two-phase form (per-slice partials, then the ordered
-pk_splitk_reduce), whatever the tile count (a multiple of 8, not, fewer than 8), and the
-arrival counters at the head of the workspace must be zero again after every call, so one
-workspace serves any sequence of shapes, including the kernels that reduce in a second
-launch (M >= 5) and the dense split-K GEMM."""
+"""Split-K slices that hand off through one XCD's L2 (the GEMV for M <= 4, the register-dequant
+kernel for 5 <= M <= 16): the one-launch result must equal, bit for bit, the two-phase form
+(per-slice partials, then the ordered pk_splitk_reduce), whatever the tile count (a multiple
+of 8, not, fewer than 8), and the arrival counters at the head of the workspace must be zero
+again after every call, so one workspace serves any sequence of shapes, including the
+kernels that reduce in a second launch (more rows) and the dense split-K GEMM."""
 
 from __future__ import annotations
 
@@ -66,18 +66,42 @@ def test_gemv_l2_handoff_matches_two_phase(M, K, N, cuda):
     assert oracle.rel_fro(one.cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, 128)) <= 1e-4
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 4096, 6144), (8, 4096, 11008), (32, 4096, 4096),
-                                   (17, 2048, 528), (8, 14336, 4096)])
+# Tiles of 128 or 256 columns: 48, 86 (not a multiple of 8), 32, 5 (fewer than 8, ragged);
+# one 16-row block (one launch) and more (two launches: 32, 17, 48, 128, 100).
+@pytest.mark.parametrize("M,K,N", [(8, 4096, 6144), (12, 4096, 11008), (32, 4096, 4096),
+                                   (17, 2048, 528), (8, 14336, 4096), (128, 4096, 4096),
+                                   (100, 2048, 1024), (48, 4096, 2048), (5, 1024, 4112),
+                                   (16, 4096, 1024)])
 def test_skinny_one_call_matches_two_phase(M, K, N, cuda):
     a, qw, sc, codes, s16 = _case(M, K, N, 1100 + M + N % 89, cuda)
     ag = a.to(cuda)
     kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
     assert kid == _pk.KERNEL_SKINNY and split > 1
-    assert _pk.w4a16_launches(M, N, K, 128, 0) == 2
+    assert _pk.w4a16_launches(M, N, K, 128, 0) == (1 if M <= 16 else 2)
     one = gemm_int4.w4a16_gemm(ag, qw, sc, 128, out_dtype=torch.float32)
     assert torch.equal(one, _two_phase(ag, qw, sc, split, cuda))
+    assert torch.equal(one, gemm_int4.w4a16_gemm(ag, qw, sc, 128, out_dtype=torch.float32))
     assert _counters_zero(cuda)
     assert oracle.rel_fro(one.cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, 128)) <= 1e-3
+
+
+@pytest.mark.parametrize("M,split", [(12, 4), (8, 16), (16, 8), (5, 2)])
+def test_skinny_explicit_splits_one_call(M, split, cuda):
+    """Explicit splits run the one-launch handoff too (16 slices take two batches of loads in
+    the last workgroup's sum), with fp16 output and a tensor scale."""
+    K, N = 4096 if split > 2 else 1024, 1024
+    a, qw, sc, codes, s16 = _case(M, K, N, 1150 + M + split, cuda)
+    ag = a.to(cuda)
+    assert _pk.w4a16_plan(M, N, K, 128, split) == (_pk.KERNEL_SKINNY, split)
+    assert _pk.w4a16_launches(M, N, K, 128, split) == 1
+    one = _pk.w4a16_gemm(ag, qw, sc, 128, 0.5, torch.float16, split_k=split)
+    parts = _pk.w4a16_gemm_partials(ag, qw, sc, 128, split)
+    two = torch.empty((M, N), dtype=torch.float16, device=cuda)
+    _pk.splitk_reduce(parts, 0.5, two)
+    assert torch.equal(one, two)
+    assert _counters_zero(cuda)
+    ref = 0.5 * oracle.w4a16_ref(a.numpy(), codes, s16, 128)
+    assert oracle.rel_fro(one.float().cpu().numpy(), ref) <= 2e-3
 
 
 def test_one_workspace_many_shapes(cuda):
