@@ -86,20 +86,21 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int j = lane & 15, g = lane >> 4;
-  // Row parts of one (tile, slice) are blocks b and b + 8: the same XCD, dispatched close
-  // together, so the second part's weight reads hit that XCD's L2. In the one-launch split-K
-  // form the 1-D grid also keeps every slice of a tile on that XCD.
+  // Workgroup b runs on XCD b % 8 (grid widths are multiples of 8). Row parts of one (tile,
+  // slice) are dispatched next to each other on one XCD, so the second part's weight reads
+  // hit that XCD's L2; so are the two 128-column tiles that share each 128-byte weight line
+  // (8 columns per lane): one XCD reads the line from HBM once instead of two XCDs each
+  // reading all of it. In the one-launch split-K form the 1-D grid also keeps every slice of a
+  // tile on that XCD.
   int part, tile, slice;
-  if constexpr (L2) {
-    const int b = blockIdx.x, jj = b >> 3, per = p.split * p.row_parts;
-    tile = (b & 7) + 8 * (jj / per);
-    slice = (jj % per) / p.row_parts;
-    part = (jj % per) % p.row_parts;
-  } else {
-    const int bx = blockIdx.x;
-    slice = blockIdx.y;
-    part = (bx >> 3) % p.row_parts;
-    tile = (bx / (8 * p.row_parts)) * 8 + (bx & 7);
+  {
+    const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+    const int per = (L2 ? p.split : 1) * p.row_parts;  // units per tile on one XCD
+    const int u = (CPL == 8 ? j >> 1 : j) % per;
+    const int g = (CPL == 8 ? j >> 1 : j) / per;
+    tile = CPL == 8 ? 16 * g + 2 * x + (j & 1) : 8 * g + x;
+    part = u % p.row_parts;
+    slice = L2 ? u / p.row_parts : (int)blockIdx.y;
   }
   if (tile >= p.tiles) return;
   const int m0 = part * MB * 16;
@@ -409,14 +410,15 @@ static void launch_skinny_t(const SkinnyParams& p, bool l2, hipStream_t s) {
   // 2 for two blocks; 8 columns per lane halve the weight registers.
   constexpr int PD = CPL == 16 ? (MB == 1 ? 3 : 2) : (MB == 1 ? 4 : MB == 2 ? 3 : 2);
   constexpr int OCC = NW == 4 ? 2 : 1;
+  // tiles rounded up to whole groups of 8 XCDs (of pairs with 8 columns per lane)
+  const unsigned slots = (unsigned)(cdiv(p.tiles, CPL == 8 ? 16 : 8) * (CPL == 8 ? 16 : 8));
   if (l2) {
-    const unsigned gx = (unsigned)(cdiv(p.tiles, 8) * 8 * p.split * p.row_parts);
-    w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, true><<<gx, 64 * NW, 0, s>>>(p);
+    w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, true>
+        <<<slots * p.split * p.row_parts, 64 * NW, 0, s>>>(p);
     return;
   }
-  const unsigned gx = p.row_parts == 1 ? (unsigned)p.tiles
-                                       : (unsigned)(cdiv(p.tiles, 8) * 8 * p.row_parts);
-  w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, false><<<dim3(gx, p.split), 64 * NW, 0, s>>>(p);
+  w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, false>
+      <<<dim3(slots * p.row_parts, p.split), 64 * NW, 0, s>>>(p);
 }
 
 template <int MB, int CPL, bool GS>
