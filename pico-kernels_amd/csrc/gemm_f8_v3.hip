@@ -1,11 +1,14 @@
-// e4m3 fp8 GEMM for gfx950, 256 x 256 tiles, 4-stage LDS pipeline, B in either layout
-// through LDS DMA (v_mfma_f32_32x32x64_f8f6f4).
+// e4m3 fp8 GEMM for gfx950, 256 x 256 (or 256 x 128) tiles, 4-stage LDS pipeline, B in
+// either layout through LDS DMA (v_mfma_f32_32x32x64_f8f6f4).
 //
 // C[m, n] = out_scale * sum_k A[m, k] * B[k, n] (gemm_fp8.py:38-117), A (M, K) row-major,
 // B (K, N) row-major (BLAYOUT 0) or (N, K) row-major (BLAYOUT 1, a transposed view).
 //
 // Design:
 //  * 8 waves (2 x 4), each a 128 x 64 block: 4 x 2 fragments of 32 x 32, 64 k per MFMA.
+//    256 x 128 tiles (for outputs whose 256 x 256 tiles would leave CUs idle: 2048 x 4096
+//    is 128 of them for 256 CUs) use 4 x 2 waves of 64 x 64 (2 x 2 fragments), a B stage of
+//    8 KB and one B DMA per wave and tile.
 //  * K tiles of 64. A tile = 256 rows x 64 bytes, B tile = 64 k x 256 n (BLAYOUT 0) or
 //    256 n x 64 k (BLAYOUT 1); both go global -> LDS with buffer DMA (no VGPR staging).
 //  * Four LDS stages (32 KB each); the loads of tile t+3 are issued right after the barrier
@@ -58,6 +61,11 @@ __device__ __forceinline__ pk_i2v f8_read_tr(const char* lds) {
 __device__ __forceinline__ int f8_swz64(int r, int c) { return (r << 6) + ((c ^ ((r >> 2) & 3)) << 4); }
 // slot of chunk c of row k in a 256-byte-row tile
 __device__ __forceinline__ int f8_swz256(int k, int c) { return (k << 8) + ((c ^ (2 * (k & 7))) << 4); }
+// slot of chunk c of row k in a 128-byte-row tile: the 8 rows a transposing read touches at
+// one chunk land in 8 distinct 16-byte bank groups
+__device__ __forceinline__ int f8_swz128(int k, int c) { return (k << 7) + ((c ^ (k & 7)) << 4); }
+template <int BN>
+__device__ __forceinline__ int f8_swzB(int k, int c) { return BN == 256 ? f8_swz256(k, c) : f8_swz128(k, c); }
 
 // XCD-aware tile order: consecutive logical tiles on one XCD, grouped 4 tile rows deep.
 __device__ __forceinline__ void f8_tile_of(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
@@ -74,23 +82,27 @@ __device__ __forceinline__ void f8_tile_of(int bid, int tiles_m, int tiles_n, in
   *tn = in_g / gm;
 }
 
-template <int BLAYOUT>
+template <int BLAYOUT, int BN>
 __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
-  constexpr int BM = 256, BN = 256, BK = 64;
-  constexpr int WTM = 128, WTN = 64, FM = 4, FN = 2;
-  constexpr int STAGE = BM * BK;  // bytes per operand per stage (16 KB)
+  constexpr int BM = 256, BK = 64;
+  constexpr int WAVES_N = BN / 64, WAVES_M = 8 / WAVES_N;
+  constexpr int WTM = BM / WAVES_M, WTN = 64, FM = WTM / 32, FN = 2;
+  constexpr int STAGE = BM * BK;      // bytes of A per stage (16 KB)
+  constexpr int STAGE_B = BN * BK;    // bytes of B per stage
+  constexpr int NBD = BN / 128;       // B DMA instructions per wave and tile
+  constexpr int PARTS = 2 + NBD;      // DMA instructions per wave and tile
 
   __shared__ __align__(16) char sA0[STAGE];
   __shared__ __align__(16) char sA1[STAGE];
   __shared__ __align__(16) char sA2[STAGE];
   __shared__ __align__(16) char sA3[STAGE];
-  __shared__ __align__(16) char sB0[STAGE];
-  __shared__ __align__(16) char sB1[STAGE];
-  __shared__ __align__(16) char sB2[STAGE];
-  __shared__ __align__(16) char sB3[STAGE];
+  __shared__ __align__(16) char sB0[STAGE_B];
+  __shared__ __align__(16) char sB1[STAGE_B];
+  __shared__ __align__(16) char sB2[STAGE_B];
+  __shared__ __align__(16) char sB3[STAGE_B];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm0 = (wave >> 2) * WTM, wn0 = (wave & 3) * WTN;
+  const int wm0 = (wave / WAVES_N) * WTM, wn0 = (wave % WAVES_N) * WTN;
   int tm, tn;
   f8_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -106,36 +118,37 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
     a_off[i] = (int)((int64_t)min(m0 + r, p.M - 1) * p.lda) + c * 16;
   }
   __amdgpu_buffer_rsrc_t rb;
-  int b_off[2];
+  int b_off[NBD];
   if constexpr (BLAYOUT == 1) {
     rb = make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = (wave * 2 + i) * 16 + (lane >> 2);
+    for (int i = 0; i < NBD; ++i) {
+      const int r = (wave * NBD + i) * 16 + (lane >> 2);
       const int c = (lane & 3) ^ ((r >> 2) & 3);
       b_off[i] = (int)((int64_t)min(n0 + r, p.N - 1) * p.ldb) + c * 16;
     }
   } else {
     rb = make_rsrc(p.b, (uint32_t)((int64_t)p.K * p.ldb));
+    constexpr int CPR = BN / 16;  // 16-byte chunks per k row
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int k = (wave * 2 + i) * 4 + (lane >> 4);  // 4 rows of 256 bytes per instruction
-      const int c = (lane & 15) ^ (2 * (k & 7));
+    for (int i = 0; i < NBD; ++i) {
+      const int k = (wave * NBD + i) * (64 / CPR) + lane / CPR;  // 1 KB of k rows per instruction
+      const int c = BN == 256 ? (lane & 15) ^ (2 * (k & 7)) : (lane & 7) ^ (k & 7);
       b_off[i] = (int)((int64_t)k * p.ldb) + min(n0 + c * 16, p.N - 16);
     }
   }
-  // DMA `part` (0, 1: A; 2, 3: B) of tile kt
+  // DMA `part` (0, 1: A; 2 .. PARTS-1: B) of tile kt
   auto issue_part = [&](int kt, char* sA, char* sB, int part) {
     if (part < 2) {
       f8_dma16(ra, sA + (wave * 2 + part) * 1024, a_off[part], kt * BK);
     } else {
       const int bs = BLAYOUT == 1 ? kt * BK : (int)((int64_t)kt * BK * p.ldb);
-      f8_dma16(rb, sB + (wave * 2 + part - 2) * 1024, b_off[part - 2], bs);
+      f8_dma16(rb, sB + (wave * NBD + part - 2) * 1024, b_off[part - 2], bs);
     }
   };
   auto issue = [&](int kt, char* sA, char* sB) {
 #pragma unroll
-    for (int part = 0; part < 4; ++part) issue_part(kt, sA, sB, part);
+    for (int part = 0; part < PARTS; ++part) issue_part(kt, sA, sB, part);
   };
 
   // ---- fragment offsets inside a stage ----
@@ -157,7 +170,7 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int k = 32 * (lane >> 5) + 8 * q + (i16 >> 1);
-        boff[j][q] = f8_swz256(k, cs >> 4) + (cs & 15);
+        boff[j][q] = f8_swzB<BN>(k, cs >> 4) + (cs & 15);
       }
     }
   }
@@ -201,7 +214,9 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
       for (int j = 0; j < FN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[i][j], 0, 0, 0, 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
-      issue_part(ktn, sAn, sBn, i);
+      // one DMA after each MFMA pair; the last pair issues the rest
+#pragma unroll
+      for (int part = i; part < (i == FM - 1 ? PARTS : i + 1); ++part) issue_part(ktn, sAn, sBn, part);
     }
   };
 
@@ -211,12 +226,13 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
   issue(0, sA0, sB0);
   issue(min(1, last), sA1, sB1);
   issue(min(2, last), sA2, sB2);
-  // s_waitcnt vmcnt(8) expcnt(7) lgkmcnt(15): this wave's DMAs of the oldest tile landed.
-  // The barrier is a bare s_barrier: __syncthreads() adds a workgroup release fence, which
-  // waits for *every* outstanding LDS DMA (vmcnt(0)) and would serialise the pipeline. The
-  // explicit wait above already covers the data this barrier publishes, and the asm memory
-  // clobber keeps the compiler from moving LDS accesses across it.
-  constexpr int kWaitOldest = 0x0f78;
+  // s_waitcnt vmcnt(2 * PARTS) expcnt(7) lgkmcnt(15): this wave's DMAs of the oldest tile
+  // landed (the two younger tiles' stay outstanding). The barrier is a bare s_barrier:
+  // __syncthreads() adds a workgroup release fence, which waits for *every* outstanding LDS
+  // DMA (vmcnt(0)) and would serialise the pipeline. The explicit wait above already covers
+  // the data this barrier publishes, and the asm memory clobber keeps the compiler from
+  // moving LDS accesses across it.
+  constexpr int kWaitOldest = 0x0f70 | (2 * PARTS);
   auto step = [&](int kt, char* sAc, char* sBc, char* sAn, char* sBn) {
     __builtin_amdgcn_s_waitcnt(kWaitOldest);
     asm volatile("s_barrier" ::: "memory");
@@ -237,18 +253,25 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
   mfma_drain();
 
   // ---- epilogue ----
-  // Through LDS when rows are 16-byte aligned: each wave stages 64-row halves of its
-  // 128 x 64 block in one 16 KB stage array (rows of 64 values, 16-byte chunks XOR-swizzled
-  // by row), then writes them back row-contiguous, 16 bytes per lane: every store instruction
-  // covers whole 128-byte lines instead of 16 bytes in each of 32 rows.
+  // Through LDS when rows are 16-byte aligned: each wave stages halves of its block (64 rows
+  // of 128 x 64, or 32 rows of 64 x 64) in a free stage region of its own (rows of 64 values,
+  // 16-byte chunks XOR-swizzled by row), then writes them back row-contiguous, 16 bytes per
+  // lane: every store instruction covers whole 128-byte lines instead of 16 bytes in each of
+  // 32 rows.
   const int esz = p.c_dtype == PK_F32 ? 4 : 2;
   const bool vec16 = (p.ldc * esz) % 16 == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
   const int em = lane & 31, en = 4 * (lane >> 5);
   if (vec16) {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS reads are done
     __syncthreads();                     // and every other wave's: the stages are free
-    char* sW = wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sA2 : wave == 3 ? sA3
-             : wave == 4 ? sB0 : wave == 5 ? sB1 : wave == 6 ? sB2 : sB3;
+    // a wave-uniform region of 64 rows x 64 fp32 (16 KB; 256 x 128 tiles: 32 rows, 8 KB)
+    char* sW;
+    if constexpr (BN == 256)
+      sW = wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sA2 : wave == 3 ? sA3
+         : wave == 4 ? sB0 : wave == 5 ? sB1 : wave == 6 ? sB2 : sB3;
+    else
+      sW = (wave < 2 ? sA0 : wave < 4 ? sA1 : wave < 6 ? sA2 : sA3) + (wave & 1) * 8192;
+    constexpr int HF = FM / 2;  // fragments per staged half
     with_dtype(p.c_dtype, [&](auto DT) {
       constexpr int dt = decltype(DT)::value;
       constexpr int E = dt == PK_F32 ? 4 : 2;
@@ -256,7 +279,7 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
+        for (int ii = 0; ii < HF; ++ii)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -264,8 +287,8 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
               const int r = 32 * ii + em, col = 32 * j + 8 * q + en;
               const int byte = col * E;
               char* dst = sW + r * RB + ((((byte >> 4) ^ (r % NCH)) << 4) | (byte & 15));
-              const pk_f4 acc4 = {acc[2 * h + ii][j][4 * q], acc[2 * h + ii][j][4 * q + 1],
-                                  acc[2 * h + ii][j][4 * q + 2], acc[2 * h + ii][j][4 * q + 3]};
+              const pk_f4 acc4 = {acc[HF * h + ii][j][4 * q], acc[HF * h + ii][j][4 * q + 1],
+                                  acc[HF * h + ii][j][4 * q + 2], acc[HF * h + ii][j][4 * q + 3]};
               const pk_f4 v = acc4 * p.scale;
               if constexpr (dt == PK_F32) {
                 *reinterpret_cast<pk_f4*>(dst) = v;
@@ -280,10 +303,10 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
             }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // the wave's staging writes are in LDS
 #pragma unroll
-        for (int c0 = 0; c0 < 64 * NCH; c0 += 64) {
+        for (int c0 = 0; c0 < 32 * HF * NCH; c0 += 64) {
           const int idx = c0 + lane, r = idx / NCH, ch = idx % NCH;
           const pk_u4v val = *reinterpret_cast<const pk_u4v*>(sW + r * RB + ((ch ^ (r % NCH)) << 4));
-          const int gm = m0 + wm0 + 64 * h + r, gn = n0 + wn0 + ch * (16 / E);
+          const int gm = m0 + wm0 + 32 * HF * h + r, gn = n0 + wn0 + ch * (16 / E);
           if (gm < p.M && gn < p.N)  // N % 16 == 0: a chunk is all in or all out
             *PK_GLOBAL(pk_u4v, reinterpret_cast<char*>(p.c) + ((int64_t)gm * p.ldc + gn) * E) = val;
         }
@@ -335,10 +358,23 @@ int f8_v3_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb,
   p.N = N;
   p.K = K;
   p.tiles_m = (int)cdiv(M, 256);
-  p.tiles_n = (int)cdiv(N, 256);
+  // 256 x 128 tiles where 256 x 256 ones would leave CUs idle
+  int cus = 256;
+  {
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess)
+      (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  }
+  const bool narrow = (int64_t)p.tiles_m * cdiv(N, 256) < cus;
+  p.tiles_n = (int)cdiv(N, narrow ? 128 : 256);
   const dim3 grid(p.tiles_m * p.tiles_n);
-  if (b_layout == 1) gemm_f8_v3_kernel<1><<<grid, 512, 0, s>>>(p);
-  else gemm_f8_v3_kernel<0><<<grid, 512, 0, s>>>(p);
+  if (narrow) {
+    if (b_layout == 1) gemm_f8_v3_kernel<1, 128><<<grid, 512, 0, s>>>(p);
+    else gemm_f8_v3_kernel<0, 128><<<grid, 512, 0, s>>>(p);
+  } else {
+    if (b_layout == 1) gemm_f8_v3_kernel<1, 256><<<grid, 512, 0, s>>>(p);
+    else gemm_f8_v3_kernel<0, 256><<<grid, 512, 0, s>>>(p);
+  }
   PK_LAUNCH_CHECK("fp8 gemm (v3)");
   return PK_OK;
 }

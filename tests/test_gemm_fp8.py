@@ -143,6 +143,23 @@ def test_fp8_full_size_4096(cuda):
     assert 0.02 < err_gpu < 0.06  # the ~3.7% the reference reports for N(0,1) inputs
 
 
+@pytest.mark.parametrize("M,K,N", [(2048, 4096, 4096), (600, 1024, 1008), (256, 256, 4096)])
+def test_fp8_narrow_tiles(M, K, N, cuda):
+    """Outputs whose 256 x 256 tiles would leave CUs idle run 256 x 128 tiles (the bench's
+    2048 x 4096 x 4096; a ragged M and N edge; one tile row): closed form, the reference's
+    error, fp16 output equal to the rounded fp32 one, and both B layouts bit for bit."""
+    a, b, a8, sa, b8, sb = _fp8_case(M, K, N, 5000 + M + N, cuda)
+    c32 = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb)
+    ref8 = oracle.fp8_gemm_ref(_u8(a8), sa, _u8(b8), sb)
+    assert oracle.rel_fro(c32.cpu().numpy(), ref8) < CLOSED_FORM_TOL
+    ref32 = a.float().numpy() @ b.float().numpy()
+    assert abs(oracle.rel_fro(c32.cpu().numpy(), ref32) - oracle.rel_fro(ref8, ref32)) <= ERR_PP
+    c16 = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb, out_dtype=torch.float16)
+    assert torch.equal(c16, c32.half())
+    bt = b8.t().contiguous()
+    assert torch.equal(c32, gemm_fp8.fp8_gemm_precast(a8, sa, bt.t(), sb))
+
+
 @pytest.mark.parametrize("M,K,N", [(256, 512, 384), (600, 384, 784), (100, 384, 272),
                                    (512, 320, 512), (100, 208, 264), (300, 64, 272)])
 def test_fp8_transposed_b_layout(M, K, N, cuda):
