@@ -640,8 +640,10 @@ COPY_PROBE_BYTES = 256 << 20
 def traffic_probe(dev) -> int:
     """Short run for the rocprofv3 --pmc passes: 50 launches of the GEMV's dominant kernel
     on rotating weights (the whole op when its slices add up in L2, else the slice kernel),
-    then 10 device copies of COPY_PROBE_BYTES (the calibration kernel: it must read and
-    write exactly that many bytes)."""
+    then 50 launches of the slices alone writing their partials (pk_w4a16_gemm_partials: the
+    same loads and partial stores, no handoff reads), then 10 device copies of
+    COPY_PROBE_BYTES (the calibration kernel: it must read and write exactly that many
+    bytes)."""
     import torch
 
     import _pk
@@ -655,10 +657,9 @@ def traffic_probe(dev) -> int:
         for i in range(50):
             _pk.w4a16_gemm(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
                            out=out)
-    else:
-        parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
-        for i in range(50):
-            _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
+    parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
+    for i in range(50):
+        _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
     torch.cuda.synchronize()
     src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)

@@ -1,6 +1,7 @@
 """ctypes binding to ``libpk_bench_probes.so``: the ceiling probes behind ``bench.py
---mfma-ceiling`` and ``--hbm-ceiling`` (declared in ``csrc/bench/pk_bench_probes.h``). They are
-measurement tools, kept outside the product library; no product module imports this one."""
+--mfma-ceiling`` and ``--hbm-ceiling`` and the workgroup-placement probe of the tests
+(declared in ``csrc/bench/pk_bench_probes.h``). They are measurement tools, kept outside the
+product library; no product module imports this one."""
 
 from __future__ import annotations
 
@@ -19,6 +20,8 @@ _vp, _i32, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 _SIGNATURES = {
     "pkb_mfma_probe": (_i32, [_i32, _i32, _i32, _i32, _vp, _vp]),
     "pkb_read_probe": (_i32, [_vp, _sz, _vp, _i32, _vp]),
+    "pkb_xcc_count": (_i32, []),
+    "pkb_xcc_probe": (_i32, [_i32, _i32, _i32, _i32, _vp, _vp]),
 }
 
 
@@ -64,3 +67,18 @@ def read_probe(src: torch.Tensor, out: torch.Tensor, grid: int) -> None:
     assert out.dtype == torch.int32 and out.numel() >= grid and out.is_cuda and src.is_cuda
     _check(lib().pkb_read_probe(src.data_ptr(), src.numel() * src.element_size(), out.data_ptr(),
                                 int(grid), _stream(src)), "pkb_read_probe")
+
+
+def xcc_count() -> int:
+    """The current device's XCD count in its partition."""
+    n = lib().pkb_xcc_count()
+    if n < 1:
+        raise ProbeError("pkb_xcc_count failed")
+    return n
+
+
+def xcc_probe(grid: int, threads: int, lds_bytes: int, spin: int, out: torch.Tensor) -> None:
+    """out[b] = the XCC id workgroup b of a (grid, threads, lds_bytes) launch ran on."""
+    assert out.dtype == torch.int32 and out.numel() >= grid and out.is_cuda
+    _check(lib().pkb_xcc_probe(int(grid), int(threads), int(lds_bytes), int(spin), out.data_ptr(),
+                               _stream(out)), "pkb_xcc_probe")

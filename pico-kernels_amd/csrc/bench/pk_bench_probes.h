@@ -1,7 +1,7 @@
 /*
  * pk_bench_probes.h -- measurement probes for bench.py (libpk_bench_probes.so). Not part of
  * the product library or its C ABI (include/pico_kernels_amd.h); no counterpart in the
- * reference. Both return 0, -1 for a bad argument, or the HIP error code of the launch.
+ * reference. The probes return 0, -1 for a bad argument, or the HIP error code of the launch.
  */
 #ifndef PK_BENCH_PROBES_H
 #define PK_BENCH_PROBES_H
@@ -22,6 +22,14 @@ int pkb_mfma_probe(int fp8, int random, int grid, int iters, float* out, void* s
 /* Reads `bytes` (a multiple of 16, 16-byte aligned) with `grid` workgroups of 256 threads and
  * writes one 32-bit word per workgroup (the XOR of the words it read) to out. */
 int pkb_read_probe(const void* src, size_t bytes, uint32_t* out, int grid, void* stream);
+
+/* The partition's XCD count (hipDeviceAttributeNumberOfXccs of the current device), or -1. */
+int pkb_xcc_count(void);
+
+/* Launches `grid` workgroups of `threads` threads (a multiple of 64, at most 1024) holding
+ * `lds_bytes` (4..65536) of LDS; each sleeps about spin * 64 clocks (0..100000) and writes the
+ * XCC id it ran on to out[workgroup]. */
+int pkb_xcc_probe(int grid, int threads, int lds_bytes, int spin, uint32_t* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -85,9 +85,39 @@ __global__ __launch_bounds__(256) void hbm_read_probe_kernel(const pk_u4v* src, 
   if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
+// The XCD (XCC id in the partition) each workgroup runs on. Each workgroup holds `lds_bytes`
+// of dynamic LDS and sleeps about `spin` x 64 clocks before it records, so a grid larger
+// than the machine is dispatched in several waves of residency, as the product's grids are.
+__global__ void xcc_probe_kernel(uint32_t* out, int spin) {
+  extern __shared__ uint32_t lds_hold[];
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  for (int i = 0; i < spin; ++i) __builtin_amdgcn_s_sleep(1);
+  if (threadIdx.x == 0) {
+    lds_hold[0] = v;
+    out[blockIdx.x] = v & 0xfu;
+  }
+}
+
 }  // namespace pk
 
 using namespace pk;
+
+extern "C" int pkb_xcc_count(void) {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) return -1;
+  return n;
+}
+
+extern "C" int pkb_xcc_probe(int grid, int threads, int lds_bytes, int spin, uint32_t* out,
+                             void* stream) {
+  if (out == nullptr || grid < 1 || threads < 64 || threads > 1024 || threads % 64 ||
+      lds_bytes < 4 || lds_bytes > 65536 || spin < 0 || spin > 100000)
+    return -1;
+  xcc_probe_kernel<<<grid, threads, lds_bytes, (hipStream_t)stream>>>(out, spin);
+  return (int)hipGetLastError();
+}
 
 // Status: 0, or -1 for a bad argument, or the HIP error of the launch.
 extern "C" int pkb_read_probe(const void* src, size_t bytes, uint32_t* out, int grid, void* stream) {
