@@ -159,6 +159,26 @@ int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_
  * counterpart in the reference (its split-K is one Triton launch plus atomics). */
 int pk_w4a16_launches(int M, int N, int K, int group_size, int split_k);
 
+/* Activations for a packed layer of the reference's quantize_model layout (one fp32 scale per
+ * input feature over all output rows: quantize.py:52-54 through rtn_layer / gptq_layer with
+ * group_size=None, written back at quantize.py:179): y[m, k] = fp16(x[m, k] * in_scale[k] *
+ * mul) for x (M, K) fp32 / fp16 / bf16 with row stride ldx, y fp16 with 16-byte aligned rows
+ * (ldy % 8 == 0), K % 8 == 0. The layer's product x @ wq^T is then pk_w4a16_gemm of y with
+ * the int4 codes, no group scales and tensor_scale = 1 / mul. in_scale NULL: the input cast
+ * alone. Replaces the dequantisation q * s of quantize_col (quantize.py:54) by the same scale
+ * on the activation side. */
+int pk_w4a16_prep_activations(const void* x, int x_dtype, int64_t ldx, const float* in_scale,
+                              float mul, void* y, int64_t ldy, int M, int K, void* stream);
+
+/* Fixes the register-dequant kernel's (kernel id 3) layout for every later plan in the
+ * process: 8 or 16 output columns per lane and 4 or 8 waves per workgroup; (0, 0) restores
+ * the automatic choice. Layouts with the same wave count give the same bits; the wave count
+ * changes the fp32 summation order only. For layout tests and tuning; the environment
+ * variable PK_SKINNY_CFG="cols,waves" sets the same once, at the first plan. Not thread-safe
+ * against concurrent plans in the sense that a call in flight may use either layout. No
+ * counterpart in the reference. PK_EINVAL for other values. */
+int pk_w4a16_skinny_layout(int cols_per_lane, int waves);
+
 /* pk_w4a16_gemm for callers that cannot allocate (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc): no workspace argument, and the call allocates nothing. No
  * counterpart in the reference. The split-K workspace is a fixed device array inside the

@@ -54,6 +54,8 @@ _SIGNATURES = {
     "pk_w4a16_gemm": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
                              _i32, _i32, _vp, _sz, _vp]),
     "pk_w4a16_noalloc_scratch_bytes": (_sz, []),
+    "pk_w4a16_skinny_layout": (_i32, [_i32, _i32]),
+    "pk_w4a16_prep_activations": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _vp]),
     "pk_w4a16_gemm_noalloc": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
                                      _i32, _i32, _vp]),
     "pk_w4a16_gemm_partials": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _vp, _sz, _i32, _i32, _i32,
@@ -241,6 +243,29 @@ def w4a16_plan(M: int, N: int, K: int, group_size: int, split_k: int) -> tuple[i
     _check(lib().pk_w4a16_plan(M, N, K, group_size, split_k, ctypes.byref(kid), ctypes.byref(spl)),
            "pk_w4a16_plan")
     return kid.value, spl.value
+
+
+def w4a16_prep_activations(x: torch.Tensor, in_scale: torch.Tensor | None, mul: float,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16 ``x * in_scale[k] * mul`` for (M, K) activations of any float dtype (no scale:
+    the cast alone)."""
+    M, K = x.shape
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    if in_scale is not None:
+        assert in_scale.dtype == torch.float32 and in_scale.is_contiguous() and in_scale.numel() == K
+    if out is None:
+        out = torch.empty((M, K), dtype=torch.float16, device=x.device)
+    _check(lib().pk_w4a16_prep_activations(x.data_ptr(), pk_dtype(x.dtype), x.stride(0),
+                                           None if in_scale is None else in_scale.data_ptr(),
+                                           float(mul), out.data_ptr(), out.stride(0), M, K,
+                                           stream_of(x)), "pk_w4a16_prep_activations")
+    return out
+
+
+def w4a16_skinny_layout(cols_per_lane: int, waves: int) -> None:
+    """Fix the register-dequant kernel's layout for later plans ((0, 0): automatic)."""
+    _check(lib().pk_w4a16_skinny_layout(int(cols_per_lane), int(waves)), "pk_w4a16_skinny_layout")
 
 
 def w4a16_launches(M: int, N: int, K: int, group_size: int, split_k: int) -> int:

@@ -196,8 +196,9 @@ __device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shf
 // ---------------------------------------------------------------------------------------
 // Split-K reduction inside one XCD's L2.
 //
-// MI355X dispatches the workgroups of a launch round-robin over its XCDs (XCD = linear
-// workgroup id mod the partition's XCC count, 8, 4, 2 or 1), each XCD with its own L2. A
+// MI355X dispatches the workgroups of a launch round-robin over its XCDs, each with its own
+// L2: workgroup b goes to XCD (b + c) mod the partition's XCC count (8, 4, 2 or 1), the
+// starting XCD c depending on earlier dispatches, so workgroups 8 ids apart share an XCD. A
 // 1-D grid in which workgroup b takes column tile (b % 8) + 8 * ((b / 8) / split) and slice
 // (b / 8) % split therefore keeps all slices of a tile on one XCD, whose L2 orders the
 // handoff: each slice writes its fp32 partials (L1 is write-through) and waits for the

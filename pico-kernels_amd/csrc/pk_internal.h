@@ -57,6 +57,8 @@ struct SkinnyPlan {
   int split, k_slice, tiles;
 };
 bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out);
+// Fix the layout the plan uses (cpl 8 or 16, nw 4 or 8), or restore the automatic one (0, 0).
+bool skinny_layout_set(int cpl, int nw);
 bool skinny_fits(int M, int N, int K, int64_t lda, int64_t ldq, int group, bool has_gs);
 // Split-K of the skinny kernel adds its slices in L2 inside the launch (one launch).
 bool skinny_l2(const SkinnyPlan& pl);

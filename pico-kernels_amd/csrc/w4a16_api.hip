@@ -115,6 +115,13 @@ extern "C" int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, i
   return PK_OK;
 }
 
+extern "C" int pk_w4a16_skinny_layout(int cols_per_lane, int waves) {
+  PK_REQUIRE(skinny_layout_set(cols_per_lane, waves),
+             "pk_w4a16_skinny_layout: (%d, %d) is not (0, 0), or 8 or 16 columns per lane with 4 "
+             "or 8 waves", cols_per_lane, waves);
+  return PK_OK;
+}
+
 extern "C" int pk_w4a16_launches(int M, int N, int K, int group_size, int split_k) {
   W4Plan pl;
   const bool has_gs = group_size > 0;

@@ -40,6 +40,7 @@
 // two-launch form -- and stores C. More rows, the partials-only entry point, and partitions
 // whose XCD count does not divide 8 (or PK_SPLITK_IN_L2=0) write (split, M, N) partials
 // that splitk_reduce_kernel adds in a second launch.
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 
@@ -86,7 +87,8 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int j = lane & 15, g = lane >> 4;
-  // Workgroup b runs on XCD b % 8 (grid widths are multiples of 8). Row parts of one (tile,
+  // Workgroups 8 ids apart run on one XCD (round-robin dispatch; grid widths are multiples of
+  // 8), x = b % 8 naming it. Row parts of one (tile,
   // slice) are dispatched next to each other on one XCD, so the second part's weight reads
   // hit that XCD's L2; so are the two 128-column tiles that share each 128-byte weight line
   // (8 columns per lane): one XCD reads the line from HBM once instead of two XCDs each
@@ -380,16 +382,43 @@ static bool skinny_plan_nw(int M, int N, int K, int group, bool has_gs, int spli
   return true;
 }
 
+// Fixed layout: 0 = automatic, else (cpl << 8) | nw. -1: not yet read from the environment.
+static std::atomic<int> g_skinny_layout{-1};
+
+static int skinny_layout_get() {
+  int v = g_skinny_layout.load(std::memory_order_acquire);
+  if (v >= 0) return v;
+  int c = 0, w = 0, env = 0;
+  if (const char* e = getenv("PK_SKINNY_CFG"))
+    if (sscanf(e, "%d,%d", &c, &w) == 2 && (c == 8 || c == 16) && (w == 4 || w == 8))
+      env = (c << 8) | w;
+  int expected = -1;  // a concurrent setter wins
+  g_skinny_layout.compare_exchange_strong(expected, env, std::memory_order_acq_rel);
+  return g_skinny_layout.load(std::memory_order_acquire);
+}
+
+bool skinny_layout_set(int cpl, int nw) {
+  if (cpl == 0 && nw == 0) {
+    g_skinny_layout.store(0, std::memory_order_release);
+    return true;
+  }
+  if (!((cpl == 8 || cpl == 16) && (nw == 4 || nw == 8))) return false;
+  g_skinny_layout.store((cpl << 8) | nw, std::memory_order_release);
+  return true;
+}
+
 bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out) {
   if (M < kSkinnyMinM || M > kSkinnyMaxM || N % 16 || K % 128) return false;
   // Above 64 rows every weight is read by two row parts; that beat the LDS-tiled GEMM only
   // on layers of at most 4096 x 4096 weights (measured at M = 96 and 128).
   if (M > 64 && (int64_t)K * N > 4096ll * 4096) return false;
-  // PK_SKINNY_CFG="cpl,nw" fixes columns per lane and waves per workgroup (read per plan).
-  if (const char* e = getenv("PK_SKINNY_CFG")) {
-    int c = 0, w = 0;
-    if (sscanf(e, "%d,%d", &c, &w) == 2 && (c == 8 || c == 16) && (w == 4 || w == 8))
-      return skinny_plan_nw(M, N, K, group, has_gs, split_req, w, M > 32 ? 8 : c, out);
+  // A fixed layout (columns per lane, waves per workgroup), set through
+  // pk_w4a16_skinny_layout; the environment variable PK_SKINNY_CFG="cpl,nw" sets it once per
+  // process, at the first plan.
+  const int cfg = skinny_layout_get();
+  if (cfg) {
+    const int c = cfg >> 8, w = cfg & 0xff;
+    return skinny_plan_nw(M, N, K, group, has_gs, split_req, w, M > 32 ? 8 : c, out);
   }
   // 8 waves (half the slices for the same waves in flight); 4 where slices of 8 k-steps do
   // not fit K, the group or the requested split.

@@ -2,21 +2,34 @@
 
 The reference quantizes a model by writing fake-quantized floats back into every
 ``nn.Linear`` (quantize.quantize_model, quantize.py:160-181, ``mod.weight.data = wq`` at
-:179): the weights stay 16-bit in memory and every matmul reads them at full width. This
-module keeps them packed instead:
+:179): the weights stay 16/32-bit in memory and every matmul reads them at full width. This
+module keeps them packed instead, in one of two layouts (``QuantLinear.scheme``):
 
-* ``QuantLinear.from_linear(linear, group_size=128)`` quantizes ``W^T`` ``(in, out)`` with the
-  arithmetic of ``quantize.rtn_layer(W^T, 4, group_size)`` (groups of ``group_size`` input
-  features per output column, ``s = max|w|.clamp_min(1e-12) / 7``, codes in [-7, 7]) and
-  stores the ``(in, out/8)`` int32 words (``pack_int4_n`` byte order) and ``(in/group, out)``
-  fp16 scales; ``forward`` is one ``w4a16_gemm`` call over the flattened leading dimensions.
-* ``quantize_model_int4(model)`` replaces the model's ``nn.Linear`` layers in place.
-* ``save_quantized(model, path)`` / ``load_quantized(model, path)`` write and read every
-  ``QuantLinear``'s tensors as one safetensors file (no pickle) whose metadata records the
-  format, its version and each layer's group size and shape. Loaded layers take the device
-  of the module they replace; ``forward`` needs them on the GPU.
+* ``"per_input"`` -- exactly what the reference's ``quantize_model`` produces: ``rtn_layer``
+  or ``gptq_layer`` with ``group_size=None`` (quantize.py:63-115) quantize every input column
+  of ``W [out, in]`` with one scale over all output rows (quantize.py:52-54), so
+  ``wq[:, j] = q[:, j] * s_j``. ``QuantLinear.from_quantized_weight(wq)`` recovers ``s_j``
+  and the codes ``q`` from such a weight and stores the codes as ``(in, out/8)`` int32 words
+  (``pack_int4_n`` byte order) plus ``s`` as an ``(in,)`` fp32 vector. ``forward`` folds
+  ``s`` into the activations (``pk_w4a16_prep_activations``: ``fp16(x * s / max s)``, the
+  input cast in the same pass) and runs the W4A16 kernel in its per-tensor mode with
+  ``max s`` as the epilogue scale: ``x @ wq^T`` as ``(x * s) @ q^T``.
+* ``"group"`` -- groups of ``group_size`` input features per output column (the layout of
+  ``quantize.rtn_layer(W^T, 4, group_size)``: ``s = max|w|.clamp_min(1e-12) / 7`` per group,
+  codes in [-7, 7]) with ``(in/group, out)`` fp16 scales, the kernel's group mode.
 
-Weights need ``in % group_size == 0`` and ``out % 8 == 0`` (whole int32 words).
+``QuantLinear.from_linear(linear, method=...)``: ``method=None`` quantizes to the group
+layout; ``"rtn"`` / ``"gptq"`` (with calibration inputs ``x``) run this build's ``rtn_layer`` /
+``gptq_layer`` (group_size None) -- the reference's own per-layer call -- and pack the result.
+``quantize_model_int4(model, method=...)`` replaces a model's ``nn.Linear`` layers in place.
+``save_quantized`` / ``load_quantized`` write and read every ``QuantLinear`` as one safetensors
+file (no pickle) whose metadata records the format, its version and each layer's layout and
+shape; ``load_quantized`` checks each tensor's shape and dtype before copying and raises
+``ValueError`` on any mismatch.
+
+The output has the input's dtype (fp16, bf16 or fp32, as ``nn.Linear``); other inputs are
+computed in fp16. Weights need ``out % 8 == 0`` (whole int32 words) and ``in % 32 == 0``
+(the kernel's K), group layers ``in % group_size == 0``.
 """
 
 from __future__ import annotations
@@ -31,31 +44,68 @@ import gemm_int4
 
 __all__ = ["QuantLinear", "quantize_model_int4", "save_quantized", "load_quantized", "FORMAT"]
 
-FORMAT = "pico-kernels-amd/w4a16-group"
-FORMAT_VERSION = 1
+FORMAT = "pico-kernels-amd/w4a16"
+FORMAT_VERSION = 2
+SCHEMES = ("group", "per_input")
+_OUT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
 class QuantLinear(nn.Module):
-    """``y = x @ W^T + b`` with ``W`` stored as group-quantized int4 (see the module doc)."""
+    """``y = x @ W^T + b`` with ``W`` stored as int4 codes and scales (see the module doc)."""
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True,
-                 group_size: int = 128, device: torch.device | str | None = None):
+                 group_size: int = 128, device: torch.device | str | None = None,
+                 scheme: str = "group"):
         super().__init__()
-        assert in_features % group_size == 0, "in_features must be a multiple of group_size"
-        assert out_features % 8 == 0, "out_features must be a multiple of 8"
-        self.in_features, self.out_features, self.group_size = in_features, out_features, group_size
+        if scheme not in SCHEMES:
+            raise ValueError(f"scheme must be one of {SCHEMES}, not {scheme!r}")
+        if out_features % 8:
+            raise ValueError("out_features must be a multiple of 8")
+        if in_features % 32:
+            raise ValueError("in_features must be a multiple of 32")
+        if scheme == "group" and in_features % group_size:
+            raise ValueError("in_features must be a multiple of group_size")
+        self.in_features, self.out_features, self.scheme = in_features, out_features, scheme
+        self.group_size = group_size if scheme == "group" else 0
         self.register_buffer("qweight", torch.zeros(in_features, out_features // 8,
                                                     dtype=torch.int32, device=device))
-        self.register_buffer("scales", torch.zeros(in_features // group_size, out_features,
-                                                   dtype=torch.float16, device=device))
+        if scheme == "group":
+            self.register_buffer("scales", torch.zeros(in_features // group_size, out_features,
+                                                       dtype=torch.float16, device=device))
+        else:
+            self.register_buffer("scales", torch.zeros(in_features, dtype=torch.float32,
+                                                       device=device))
         if bias:
             self.register_buffer("bias", torch.zeros(out_features, dtype=torch.float16,
                                                      device=device))
         else:
             self.bias = None
+        self._smax = 1.0  # per_input: max of the scales (the epilogue scale)
+
+    # ---- construction -------------------------------------------------------------------
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, group_size: int = 128, method: str | None = None,
+                    x: torch.Tensor | None = None) -> "QuantLinear":
+        """Quantize ``linear``: ``method=None`` to the group layout; ``"rtn"`` or ``"gptq"``
+        (calibration inputs ``x``, ``[n, in]``) as the reference's ``quantize_model`` does
+        (quantize.py:175-178), packed in the per-input layout."""
+        if method is None:
+            return cls._from_linear_group(linear, group_size)
+        import quantize
+
+        w = linear.weight.detach()
+        if method == "rtn":
+            wq = quantize.rtn_layer(w, 4)
+        elif method == "gptq":
+            if x is None:
+                raise ValueError("method='gptq' needs calibration inputs x")
+            wq = quantize.gptq_layer(w, x, 4)
+        else:
+            raise ValueError(f"method must be None, 'rtn' or 'gptq', not {method!r}")
+        return cls.from_quantized_weight(wq, None if linear.bias is None else linear.bias.detach())
 
     @classmethod
-    def from_linear(cls, linear: nn.Linear, group_size: int = 128) -> "QuantLinear":
+    def _from_linear_group(cls, linear: nn.Linear, group_size: int) -> "QuantLinear":
         w = linear.weight.detach()
         # quantized on the GPU; the layer lives where the source layer lives
         q = cls(linear.in_features, linear.out_features, linear.bias is not None, group_size,
@@ -68,40 +118,105 @@ class QuantLinear(nn.Module):
             q.bias.copy_(linear.bias.detach().to(torch.float16))
         return q
 
+    @classmethod
+    def from_quantized_weight(cls, wq: torch.Tensor, bias: torch.Tensor | None = None,
+                              bits: int = 4) -> "QuantLinear":
+        """Pack a weight ``[out, in]`` that ``rtn_layer`` / ``gptq_layer`` with
+        ``group_size=None`` wrote (every input column an integer multiple of its own scale,
+        codes within ``±(2^(bits-1) - 1)``): ``s_j = max|wq[:, j]| / qmax``,
+        ``q = round(wq / s)``. Raises ``ValueError`` if ``wq`` is not of that form."""
+        if bits != 4:
+            raise ValueError("only 4-bit codes pack into the W4A16 layout")
+        out_f, in_f = wq.shape
+        dev = wq.device
+        w = wq.detach().to(_pk.gpu_device()).float()
+        qmax = 2 ** (bits - 1) - 1
+        s = w.abs().amax(dim=0) / qmax                  # (in,)
+        safe = torch.where(s > 0, s, torch.ones_like(s))
+        q = torch.round(w / safe)
+        # each element a whole multiple of its column's scale: up to the rounding of the
+        # written-back weight (fp32, or fp16 / bf16 for a half-precision model)
+        if bool((q.abs() > qmax).any()) or not bool(
+                ((w - q * safe).abs() <= 5e-2 * safe + 1e-30).all()):
+            raise ValueError("weight is not a per-input-column int4 quantization "
+                             "(rtn_layer / gptq_layer with group_size=None)")
+        s = torch.where(s > 0, s, torch.full_like(s, 1e-12 / qmax))
+        layer = cls(in_f, out_f, bias is not None, 0, dev, scheme="per_input")
+        codes = q.t().contiguous().to(torch.int8)       # (in, out)
+        layer.qweight.copy_(gemm_int4.pack_int4_n(codes).view(torch.int32))
+        layer.scales.copy_(s)
+        layer._smax = float(s.max().item())
+        if bias is not None:
+            layer.bias.copy_(bias.to(torch.float16))
+        return layer
+
+    # ---- use ----------------------------------------------------------------------------
     def dequantized_weight(self) -> torch.Tensor:
         """``(out, in)`` fp32 ``q * scale`` (for inspection and tests)."""
-        return gemm_int4.dequantize_int4_group(self.qweight, self.scales, self.group_size).t()
+        if self.scheme == "group":
+            return gemm_int4.dequantize_int4_group(self.qweight, self.scales, self.group_size).t()
+        q = gemm_int4.unpack_int4_n(self.qweight.contiguous().view(torch.uint8)).float()
+        return (q * self.scales.to(q.device)[:, None]).t()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         assert x.shape[-1] == self.in_features
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.in_features)
-        if x2.dtype != torch.float16:
-            x2 = x2.half()
-        y = _pk.w4a16_gemm(x2, self.qweight, self.scales, self.group_size, 1.0, torch.float16)
+        out_dtype = x.dtype if x.dtype in _OUT_DTYPES else torch.float16
+        if self.scheme == "per_input":
+            # x * s / max s in fp16 (the input cast in the same pass), then max s in the epilogue
+            s = self.scales if self.scales.dtype == torch.float32 else self.scales.float()
+            xp = _pk.w4a16_prep_activations(x2, s, 1.0 / self._smax)
+            y = _pk.w4a16_gemm(xp, self.qweight, None, 0, self._smax, out_dtype)
+        else:
+            xp = x2 if x2.dtype == torch.float16 else _pk.w4a16_prep_activations(x2, None, 1.0)
+            s = self.scales if self.scales.dtype == torch.float16 else self.scales.half()
+            y = _pk.w4a16_gemm(xp, self.qweight, s, self.group_size, 1.0, out_dtype)
         if self.bias is not None:
-            y = y + self.bias
+            y = y + self.bias.to(out_dtype)
         return y.reshape(*lead, self.out_features)
 
+    def _refresh(self) -> None:
+        if self.scheme == "per_input":
+            self._smax = float(self.scales.float().max().item())
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        super()._load_from_state_dict(*args, **kwargs)
+        self._refresh()
+
     def extra_repr(self) -> str:
+        lay = f"group_size={self.group_size}" if self.scheme == "group" else "per-input scales"
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
-                f"bias={self.bias is not None}, group_size={self.group_size}, int4")
+                f"bias={self.bias is not None}, {lay}, int4")
 
 
-def quantize_model_int4(model: nn.Module, group_size: int = 128,
-                        predicate=None) -> nn.Module:
+def quantize_model_int4(model: nn.Module, group_size: int = 128, predicate=None,
+                        method: str | None = None, x=None) -> nn.Module:
     """Replace every ``nn.Linear`` of ``model`` (those ``predicate(name, module)`` accepts, if
     given) by a ``QuantLinear``; layers whose shapes the packed format cannot hold are left
-    as they are. Returns ``model``."""
+    as they are. ``method=None``: the group layout; ``"rtn"`` / ``"gptq"``: the reference's
+    ``quantize_model`` per layer (quantize.py:175-179), with ``x`` the calibration inputs of
+    each layer for GPTQ -- a mapping from layer name to ``[n, in]`` activations, or a callable
+    ``x(name, module)`` returning them (the reference captures them by running the model,
+    quantize.py:132-157). Returns ``model``."""
     targets = []
     for name, mod in model.named_modules():
         if isinstance(mod, nn.Linear) and (predicate is None or predicate(name, mod)):
-            if mod.in_features % group_size == 0 and mod.out_features % 8 == 0:
+            ok = mod.out_features % 8 == 0 and mod.in_features % 32 == 0
+            if method is None:
+                ok = ok and mod.in_features % group_size == 0
+            if ok:
                 targets.append(name)
     for name in targets:
         parent_name, _, child = name.rpartition(".")
         parent = model.get_submodule(parent_name) if parent_name else model
-        setattr(parent, child, QuantLinear.from_linear(getattr(parent, child), group_size))
+        lin = getattr(parent, child)
+        xs = None
+        if method == "gptq":
+            xs = x(name, lin) if callable(x) else (x or {}).get(name)
+            if xs is None:
+                raise ValueError(f"no calibration inputs for {name}")
+        setattr(parent, child, QuantLinear.from_linear(lin, group_size, method, xs))
     return model
 
 
@@ -121,35 +236,61 @@ def save_quantized(model: nn.Module, path: str) -> None:
         if q.bias is not None:
             tensors[f"{name}.bias"] = q.bias.detach().cpu().contiguous()
         meta[name] = {"in_features": q.in_features, "out_features": q.out_features,
-                      "group_size": q.group_size, "bias": q.bias is not None}
+                      "group_size": q.group_size, "bias": q.bias is not None,
+                      "scheme": q.scheme}
     save_file(tensors, path, metadata={"format": FORMAT, "version": str(FORMAT_VERSION),
                                        "layers": json.dumps(meta, sort_keys=True)})
+
+
+_ST_DTYPES = {torch.int32: "I32", torch.float16: "F16", torch.float32: "F32"}
+
+
+def _read(f, key: str, like: torch.Tensor, path: str) -> torch.Tensor:
+    """The file's tensor `key`, after checking its shape and dtype against `like`."""
+    try:
+        sl = f.get_slice(key)
+    except Exception as e:  # missing tensor
+        raise ValueError(f"{path}: missing tensor {key}") from e
+    shape, dtype = tuple(sl.get_shape()), sl.get_dtype()
+    if shape != tuple(like.shape) or dtype != _ST_DTYPES[like.dtype]:
+        raise ValueError(f"{path}: {key} is {dtype}{list(shape)}, expected "
+                         f"{_ST_DTYPES[like.dtype]}{list(like.shape)}")
+    return f.get_tensor(key)
 
 
 def load_quantized(model: nn.Module, path: str) -> nn.Module:
     """Load a file written by ``save_quantized`` into ``model``: every layer named in the file
     becomes a ``QuantLinear`` (replacing an ``nn.Linear`` of the same shape, or filling an
-    existing ``QuantLinear``). Returns ``model``."""
+    existing ``QuantLinear``). Raises ``ValueError`` when the file's format, version, a layer's
+    shape or any tensor's shape or dtype does not match. Returns ``model``."""
     from safetensors import safe_open
 
     with safe_open(path, framework="pt") as f:
         md = f.metadata() or {}
-        assert md.get("format") == FORMAT, f"{path}: not a {FORMAT} file"
-        assert int(md.get("version", "0")) == FORMAT_VERSION, f"{path}: unsupported version"
-        layers = json.loads(md["layers"])
+        if md.get("format") != FORMAT:
+            raise ValueError(f"{path}: not a {FORMAT} file (format {md.get('format')!r})")
+        if md.get("version") != str(FORMAT_VERSION):
+            raise ValueError(f"{path}: format version {md.get('version')!r}, expected {FORMAT_VERSION}")
+        try:
+            layers = json.loads(md["layers"])
+        except (KeyError, ValueError) as e:
+            raise ValueError(f"{path}: no layer table") from e
         for name, info in layers.items():
             parent_name, _, child = name.rpartition(".")
             parent = model.get_submodule(parent_name) if parent_name else model
             cur = getattr(parent, child)
-            assert isinstance(cur, (nn.Linear, QuantLinear)), f"{name} is not a linear layer"
-            assert (cur.in_features, cur.out_features) == (info["in_features"], info["out_features"]), \
-                f"{name}: shape differs from the file"
+            if not isinstance(cur, (nn.Linear, QuantLinear)):
+                raise ValueError(f"{name} is not a linear layer")
+            if (cur.in_features, cur.out_features) != (info["in_features"], info["out_features"]):
+                raise ValueError(f"{name}: the model's layer is {cur.in_features}x{cur.out_features}, "
+                                 f"the file's {info['in_features']}x{info['out_features']}")
             dev = cur.qweight.device if isinstance(cur, QuantLinear) else cur.weight.device
             q = QuantLinear(info["in_features"], info["out_features"], info["bias"],
-                            info["group_size"], dev)
-            q.qweight.copy_(f.get_tensor(f"{name}.qweight"))
-            q.scales.copy_(f.get_tensor(f"{name}.scales"))
+                            info["group_size"] or 128, dev, scheme=info.get("scheme", "group"))
+            q.qweight.copy_(_read(f, f"{name}.qweight", q.qweight, path))
+            q.scales.copy_(_read(f, f"{name}.scales", q.scales, path))
             if info["bias"]:
-                q.bias.copy_(f.get_tensor(f"{name}.bias"))
+                q.bias.copy_(_read(f, f"{name}.bias", q.bias, path))
+            q._refresh()
             setattr(parent, child, q)
     return model

@@ -119,15 +119,39 @@ def test_skinny_per_tensor_int4_gemm(M, cuda):
     assert oracle.rel_fro(c.cpu().numpy(), ref) < 1e-5
 
 
-def test_skinny_strided_activations(cuda):
-    """A row stride larger than K (a view into a wider buffer) is read in place."""
-    M, K, N = 9, 1024, 512
-    a, qw, sc, codes, s16 = _case(M, K, N, 97, cuda)
+@pytest.mark.parametrize("M", [9, 48, 100])
+def test_skinny_strided_activations(M, cuda):
+    """A row stride larger than K (a view into a wider buffer) is read in place, for one
+    16-row block, several, and two row parts (the second part's A and C rows offset)."""
+    K, N = 1024, 512
+    a, qw, sc, codes, s16 = _case(M, K, N, 97 + M, cuda)
+    assert _pk.w4a16_plan(M, N, K, 128, 0)[0] == _pk.KERNEL_SKINNY
     wide = torch.zeros(M, K + 64, dtype=torch.float16)
     wide[:, :K] = a
     view = wide.to(cuda)[:, :K]
     out = gemm_int4.w4a16_gemm(view, qw, sc, 128, out_dtype=torch.float32)
     assert oracle.rel_fro(out.cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, 128)) <= W4A16_TOL
+
+
+@pytest.mark.parametrize("M", [48, 100])
+@pytest.mark.parametrize("out_dtype,tol", [(torch.float16, 2e-3), (torch.bfloat16, 1e-2)])
+def test_skinny_out_view_and_dtypes(M, out_dtype, tol, cuda):
+    """fp16 / bf16 output into a view of a wider buffer (ldc > N) with lda = K + 64, at two
+    and four 16-row blocks (two row parts at 100): bitwise the contiguous call, the guard
+    columns untouched."""
+    K, N = 2048, 1024
+    a, qw, sc, codes, s16 = _case(M, K, N, 150 + M, cuda)
+    assert _pk.w4a16_plan(M, N, K, 128, 0)[0] == _pk.KERNEL_SKINNY
+    ag = a.to(cuda)
+    dense = _pk.w4a16_gemm(ag, qw, sc, 128, 1.0, out_dtype)
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
+    assert oracle.rel_fro(dense.float().cpu().numpy(), ref) <= tol
+    wide_a = torch.zeros(M, K + 64, dtype=torch.float16, device=cuda)
+    wide_a[:, :K] = ag
+    wide_c = torch.full((M, N + 256), 5.0, dtype=out_dtype, device=cuda)
+    _pk.w4a16_gemm(wide_a[:, :K], qw, sc, 128, 1.0, out_dtype, out=wide_c[:, :N])
+    assert torch.equal(wide_c[:, :N], dense)
+    assert bool((wide_c[:, N:] == 5.0).all())
 
 
 def test_skinny_ineligible_shapes_use_gemm(cuda):
@@ -167,18 +191,37 @@ def test_skinny_four_blocks(M, K, N, cuda):
     assert err <= W4A16_TOL, f"rel err {err:.3e}"
 
 
+@pytest.fixture
+def layout():
+    """Sets the register-dequant layout (pk_w4a16_skinny_layout) and restores the automatic
+    one afterwards."""
+    def set_layout(cfg: str) -> None:
+        c, w = (int(x) for x in cfg.split(","))
+        _pk.w4a16_skinny_layout(c, w)
+    yield set_layout
+    _pk.w4a16_skinny_layout(0, 0)
+
+
+def test_skinny_layout_setter_rejects_bad_values():
+    with pytest.raises(_pk.PicoKernelsError):
+        _pk.w4a16_skinny_layout(12, 8)
+    with pytest.raises(_pk.PicoKernelsError):
+        _pk.w4a16_skinny_layout(8, 6)
+    _pk.w4a16_skinny_layout(0, 0)
+
+
 @pytest.mark.parametrize("M", [8, 24, 64, 128])
-def test_skinny_layouts_agree(M, cuda, monkeypatch):
-    """The tile layouts (PK_SKINNY_CFG = columns per lane, waves): at one wave count the
-    column width changes only which lane holds a column, so 16 and 8 columns per lane give the
-    same bits; 8 waves split a slice's rows differently (fp32 reassociation only)."""
+def test_skinny_layouts_agree(M, cuda, layout):
+    """The tile layouts (columns per lane, waves): at one wave count the column width changes
+    only which lane holds a column, so 16 and 8 columns per lane give the same bits; 8 waves
+    split a slice's rows differently (fp32 reassociation only)."""
     K, N, split = 4096, 1040, 8
     a, qw, sc, codes, s16 = _case(M, K, N, 120 + M, cuda)
     ag = a.to(cuda)
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
     outs = {}
     for cfg in ("16,4", "8,4", "16,8", "8,8"):
-        monkeypatch.setenv("PK_SKINNY_CFG", cfg)
+        layout(cfg)
         if M > 32 and cfg.startswith("16"):
             continue  # four blocks always use 8 columns per lane
         sp = split if cfg.endswith(",4") else 4
@@ -194,10 +237,10 @@ def test_skinny_layouts_agree(M, cuda, monkeypatch):
 
 @pytest.mark.parametrize("cfg", ["8,4", "8,8", "16,8"])
 @pytest.mark.parametrize("M", [5, 20, 40, 97])
-def test_skinny_layouts_edges(cfg, M, cuda, monkeypatch):
+def test_skinny_layouts_edges(cfg, M, cuda, layout):
     """Every layout on ragged tiles, ragged row blocks and parts, per-tensor and group scales,
     and the automatic split (8 waves need slices of 8 * 32 rows)."""
-    monkeypatch.setenv("PK_SKINNY_CFG", cfg)
+    layout(cfg)
     for K, N, G in ((2048, 528, 128), (1024, 784, 64), (2560, 272, 32)):
         assert _pk.w4a16_plan(M, N, K, G, 0)[0] == _pk.KERNEL_SKINNY
         a, qw, sc, codes, s16 = _case(M, K, N, 130 + M + N, cuda, G=G)

@@ -1,9 +1,11 @@
-"""The dispatch order the one-launch split-K forms rely on: workgroup b of a 1-D grid runs on
-XCD b % (XCC count), so all slices of a column tile -- the blocks the GEMV (xcd_tile_slice in
+"""The dispatch order the one-launch split-K forms rely on: the workgroups of a 1-D grid go to
+the XCDs round-robin, workgroup b to XCD (b + c) % (XCC count), where the starting XCD c
+depends on what was dispatched before; so workgroups whose ids differ by a multiple of 8 share
+an XCD, and all slices of a column tile -- the blocks the GEMV (xcd_tile_slice in
 pk_common.h), the register-dequant kernel and split-KV decode attention give one tile -- share
 one XCD and its L2. Recorded per workgroup (hwreg XCC_ID) on launches with the product
 kernels' grid sizes, block sizes and LDS, including grids larger than the machine holds at
-once. A partition mode or dispatcher that broke the mapping fails here instead of silently
+once. A partition mode or dispatcher that broke the rule fails here instead of silently
 corrupting the in-L2 handoff."""
 
 from __future__ import annotations
@@ -50,9 +52,11 @@ def test_workgroups_round_robin_over_xcds(what, grid, threads, lds, split, tile_
     _probes.xcc_probe(grid, threads, lds, spin, out)
     xcc = out.cpu().tolist()
     assert all(0 <= v < nxcc for v in xcc), sorted(set(xcc))
-    # the dispatch rule itself
-    bad = [b for b in range(grid) if xcc[b] != b % nxcc]
-    assert not bad, f"{what}: {len(bad)} workgroups off the b % {nxcc} rule, first {bad[:8]}"
+    # the dispatch rule itself: round-robin from the XCD of workgroup 0
+    c = xcc[0]
+    bad = [b for b in range(grid) if xcc[b] != (b + c) % nxcc]
+    assert not bad, (f"{what}: {len(bad)} workgroups off the (b + {c}) % {nxcc} rule, first "
+                     f"{bad[:8]}; XCC ids of workgroups 0..15: {xcc[:16]}")
     # what the kernels need from it: every slice of a tile on one XCD
     seen: dict[int, int] = {}
     for b in range(grid):
