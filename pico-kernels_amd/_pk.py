@@ -144,12 +144,14 @@ _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _retired_workspaces: list[torch.Tensor] = []
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """The zero-initialised workspace of (device, current stream), grown to `nbytes` on demand
-    (the split-K counters at its head are left zero by every call)."""
+def workspace(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor | None:
+    """The zero-initialised workspace of (device, stream -- the current one by default), grown
+    to `nbytes` on demand (the split-K counters at its head are left zero by every call)."""
     if nbytes <= 0:
         return None
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    if stream is None:
+        stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device.index, stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         old = 0
@@ -266,6 +268,7 @@ def w4a16_prep_activations(x: torch.Tensor, in_scale: torch.Tensor | None, mul: 
 def w4a16_skinny_layout(cols_per_lane: int, waves: int) -> None:
     """Fix the register-dequant kernel's layout for later plans ((0, 0): automatic)."""
     _check(lib().pk_w4a16_skinny_layout(int(cols_per_lane), int(waves)), "pk_w4a16_skinny_layout")
+    _ws_bytes.clear()
 
 
 def w4a16_launches(M: int, N: int, K: int, group_size: int, split_k: int) -> int:
@@ -285,6 +288,11 @@ def _rows_ok(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+# Workspace bytes per W4A16 shape (a pure function of the plan; cleared when the plan rules
+# change through w4a16_skinny_layout), so an eager call makes one C call, not two.
+_ws_bytes: dict[tuple[int, int, int, int, int], int] = {}
+
+
 def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | None,
                group_size: int, tensor_scale: float, out_dtype: torch.dtype,
                split_k: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -293,17 +301,30 @@ def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | No
     a = _rows_ok(a)
     if qweight.stride(1) != 1:
         qweight = qweight.contiguous()
-    if scales is not None:
+    if scales is not None and not scales.is_contiguous():
         scales = scales.contiguous()
+    dev = a.device
     if out is None:
-        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+        out = torch.empty((M, N), dtype=out_dtype, device=dev)
     g = int(group_size) if scales is not None else 0
-    nbytes = lib().pk_w4a16_workspace_bytes(M, N, K, g, int(split_k))
-    ws = workspace(a.device, nbytes)
-    _check(lib().pk_w4a16_gemm(
-        a.data_ptr(), a.stride(0), qweight.data_ptr(), qweight.stride(0), ptr(scales), g,
-        float(tensor_scale), out.data_ptr(), pk_dtype(out.dtype), out.stride(0), M, N, K,
-        int(split_k), ptr(ws), 0 if ws is None else ws.numel(), stream_of(a)), "pk_w4a16_gemm")
+    split_k = int(split_k)
+    key = (M, N, K, g, split_k)
+    nbytes = _ws_bytes.get(key)
+    L = _lib if _lib is not None else lib()
+    if nbytes is None:
+        nbytes = L.pk_w4a16_workspace_bytes(M, N, K, g, split_k)
+        if len(_ws_bytes) > 4096:
+            _ws_bytes.clear()
+        _ws_bytes[key] = nbytes
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ws = workspace(dev, nbytes, stream) if nbytes else None
+    rc = L.pk_w4a16_gemm(
+        a.data_ptr(), a.stride(0), qweight.data_ptr(), qweight.stride(0),
+        None if scales is None else scales.data_ptr(), g, float(tensor_scale), out.data_ptr(),
+        _TORCH_TO_PK[out.dtype], out.stride(0), M, N, K, split_k,
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
+    if rc != PK_OK:
+        _check(rc, "pk_w4a16_gemm")
     return out
 
 

@@ -22,7 +22,7 @@ import torch
 
 import _pk
 
-__all__ = ["KVCache", "flash_decoding", "eager_decode"]
+__all__ = ["KVCache", "flash_decoding", "eager_decode", "check_correctness", "bench"]
 
 
 class KVCache:
@@ -63,3 +63,45 @@ def eager_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Ten
     qf, kf, vf = q.float(), k.float(), v.float()
     s = (qf @ kf.transpose(-2, -1).contiguous()) * (1.0 / math.sqrt(D))
     return (torch.softmax(s, dim=-1) @ vf).to(q.dtype)
+
+
+def check_correctness(N: int = 2048, D: int = 64, split_size: int = 256) -> None:
+    """The reference's self-check (flash_decoding.py:128-138): split-KV decode against
+    eager_decode, max abs error and allclose at 1e-2."""
+    torch.manual_seed(0)
+    B, H = 2, 4
+    q = torch.randn(B, H, 1, D, device="cuda", dtype=torch.float16)
+    k = torch.randn(B, H, N, D, device="cuda", dtype=torch.float16)
+    v = torch.randn(B, H, N, D, device="cuda", dtype=torch.float16)
+    o = flash_decoding(q, k, v, split_size=split_size)
+    ref = eager_decode(q, k, v)
+    err = (o.float() - ref.float()).abs().max().item()
+    print(f"flash-decoding vs eager (N={N}): max abs err {err:.3e} | "
+          f"allclose {torch.allclose(o.float(), ref.float(), atol=1e-2, rtol=1e-2)}")
+
+
+def bench() -> None:
+    """The reference's benchmark table (flash_decoding.py:141-152): eager decode against
+    split-KV decode at B=2, H=4, D=64, split 256, N = 1K..8K (milliseconds)."""
+    from _timing import do_bench
+
+    B, H, D = 2, 4, 64
+    print(f"{'N':>7} {'eager decode':>13} {'flash-decoding':>15} {'speedup':>8}")
+    print("-" * 46)
+    for N in (1024, 2048, 4096, 8192):
+        q = torch.randn(B, H, 1, D, device="cuda", dtype=torch.float16)
+        k = torch.randn(B, H, N, D, device="cuda", dtype=torch.float16)
+        v = torch.randn(B, H, N, D, device="cuda", dtype=torch.float16)
+        ms_eager = do_bench(lambda: eager_decode(q, k, v))
+        ms_fd = do_bench(lambda: flash_decoding(q, k, v, split_size=256))
+        print(f"{N:>7} {ms_eager:>12.3f}m {ms_fd:>12.3f}m {ms_eager / ms_fd:>7.2f}x")
+
+
+if __name__ == "__main__":
+    from _timing import banner
+
+    print(banner())
+    print("=== correctness ===")
+    check_correctness()
+    print("=== benchmark (decode, M=1) ===")
+    bench()

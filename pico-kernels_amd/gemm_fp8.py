@@ -19,7 +19,7 @@ import torch
 
 import _pk
 
-__all__ = ["_E4M3_MAX", "quantize", "fp8_gemm_precast", "fp8_gemm"]
+__all__ = ["_E4M3_MAX", "quantize", "fp8_gemm_precast", "fp8_gemm", "check_correctness", "bench"]
 
 _E4M3_MAX = float(torch.finfo(torch.float8_e4m3fn).max)
 
@@ -56,3 +56,45 @@ def fp8_gemm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     a8, a_scale = quantize(a)
     b8, b_scale = quantize(b)
     return fp8_gemm_precast(a8, a_scale, b8, b_scale)
+
+
+def check_correctness(M: int = 1024, K: int = 1024, N: int = 1024) -> None:
+    """The reference's self-check (gemm_fp8.py:127-136): fp8_gemm against the fp32 product."""
+    torch.manual_seed(0)
+    a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+    b = torch.randn(K, N, device="cuda", dtype=torch.float16)
+    c = fp8_gemm(a, b)
+    ref = a.float() @ b.float()
+    rel_fro = torch.norm(c - ref) / torch.norm(ref)
+    print(f"fp8 vs fp32: rel Frobenius err {rel_fro.item():.4%} | "
+          f"max abs err {(c - ref).abs().max().item():.3e}")
+
+
+def bench() -> None:
+    """The reference's benchmark table (gemm_fp8.py:139-156): GFLOPS of the fp16 matmul
+    (hipBLASLt through torch) and of fp8_gemm_precast (cast done once, untimed)."""
+    from _timing import do_bench
+
+    print(f"{'size':>7} {'fp16 hipBLASLt':>14} {'fp8 HIP':>12} {'speedup':>8}")
+    print("-" * 46)
+    for size in (512, 1024, 2048, 4096):
+        a = torch.randn(size, size, device="cuda", dtype=torch.float16)
+        b = torch.randn(size, size, device="cuda", dtype=torch.float16)
+        a8, a_scale = quantize(a)
+        b8, b_scale = quantize(b)
+        flops = 2 * size**3 / 1e9
+        ms_fp16 = do_bench(lambda: a @ b)
+        ms_fp8 = do_bench(lambda: fp8_gemm_precast(a8, a_scale, b8, b_scale))
+        g_fp16 = flops / (ms_fp16 / 1e3)
+        g_fp8 = flops / (ms_fp8 / 1e3)
+        print(f"{size:>7} {g_fp16:>11.0f} G {g_fp8:>9.0f} G {g_fp8 / g_fp16:>7.2f}x")
+
+
+if __name__ == "__main__":
+    from _timing import banner
+
+    print(banner())
+    print("=== correctness (fp8 vs fp32 reference) ===")
+    check_correctness()
+    print("=== benchmark (GFLOPS - higher is better; cast is pre-done) ===")
+    bench()

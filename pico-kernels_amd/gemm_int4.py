@@ -31,6 +31,8 @@ __all__ = [
     "quantize_int4_group",
     "dequantize_int4_group",
     "w4a16_gemm",
+    "check_correctness",
+    "bench",
 ]
 
 
@@ -137,3 +139,54 @@ def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
         "w4a16_gemm: scales must be fp16 (K//group_size, N)")
     return _pk.w4a16_gemm(a, qweight, scales, group_size, 1.0, out_dtype,
                           split_k=0 if split_k is None else int(split_k))
+
+
+def check_correctness(M: int = 128, K: int = 256, N: int = 256) -> None:
+    """The reference's self-check (gemm_int4.py:95-104): per-tensor int4 GEMM against the
+    fp32 product of the dequantised weights, relative Frobenius error printed."""
+    torch.manual_seed(0)
+    a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+    w = torch.randn(K, N, device="cuda", dtype=torch.float16)
+    w_q, scale = quantize_int4(w)
+    w_packed = pack_int4_n(w_q)
+    c = int4_gemm(a, w_packed, scale)
+    ref = a.float() @ (w_q.float() * scale)
+    rel = torch.norm(c - ref) / torch.norm(ref)
+    print(f"int4 vs fp16-quantized ref: rel Frobenius err {rel.item():.4%}")
+
+
+def bench() -> None:
+    """The reference's benchmark table (gemm_int4.py:107-130): GFLOPS of the fp16 matmul
+    (hipBLASLt through torch) and of int4_gemm at its four shapes, HIP-event timed."""
+    from _timing import do_bench
+
+    print(f"{'shape (M,N,K)':>16} {'fp16':>12} {'int4':>12} {'speedup':>8}  regime")
+    print("-" * 60)
+    cases = [
+        (16, 4096, 4096, "memory-bound (decode)"),
+        (16, 8192, 8192, "memory-bound (decode)"),
+        (1024, 4096, 4096, "mixed"),
+        (4096, 4096, 4096, "compute-bound"),
+    ]
+    for M, N, K, label in cases:
+        a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+        w = torch.randn(K, N, device="cuda", dtype=torch.float16)
+        w_q, scale = quantize_int4(w)
+        w_packed = pack_int4_n(w_q)
+        flops = 2 * M * N * K / 1e9
+        ms_fp16 = do_bench(lambda: a @ w)
+        ms_int4 = do_bench(lambda: int4_gemm(a, w_packed, scale))
+        g_fp16 = flops / (ms_fp16 / 1e3)
+        g_int4 = flops / (ms_int4 / 1e3)
+        print(f"{(M, N, K)!s:>16} {g_fp16:>9.0f} G {g_int4:>9.0f} G "
+              f"{g_int4 / g_fp16:>7.2f}x  {label}")
+
+
+if __name__ == "__main__":
+    from _timing import banner
+
+    print(banner())
+    print("=== correctness (int4 vs quantized fp16 ref) ===")
+    check_correctness()
+    print("=== benchmark (GFLOPS - memory-bound is the win) ===")
+    bench()
