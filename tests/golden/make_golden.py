@@ -60,6 +60,19 @@ def main() -> int:
         "qi4_f16_n002": (torch.randn(512, 256, generator=_gen(1)) * 0.02).half(),
         "qi4_f32": torch.randn(128, 64, generator=_gen(2)),
     }
+    # fp32 values one to three ulps around (k + 1/2) * scale: w / scale and w * (1 / scale)
+    # round to different codes for some of them, so this case tells true division from a
+    # reciprocal multiply (fp16 inputs cannot: their quotient is rounded to fp16 first)
+    mx = np.float32(1.4501545429229736)
+    step = np.float32(float(mx) / 7.0)
+
+    def nudge(v, d):
+        for _ in range(abs(d)):
+            v = np.nextafter(v, np.float32(np.inf) if d > 0 else np.float32(-np.inf))
+        return v
+
+    ties = [nudge(np.float32((k + 0.5) * float(step)), d) for k in range(-7, 7) for d in range(-3, 4)]
+    cases["qi4_f32_ties"] = torch.from_numpy(np.array(ties + [mx], dtype=np.float32).reshape(9, 11))
     for name, w in cases.items():
         q, scale = gemm_int4.quantize_int4(w)
         arrays[name + "_in"] = _np(w)

@@ -82,7 +82,7 @@ def test_pack_shape_and_host_tensors(cuda):
 # ---------------------------------------------------------------------------------------
 def test_quantize_int4_golden(golden, cuda):
     arrays, meta = golden
-    for name in ("qi4_f16_n01", "qi4_f16_n002", "qi4_f32"):
+    for name in ("qi4_f16_n01", "qi4_f16_n002", "qi4_f32", "qi4_f32_ties"):
         w = torch.from_numpy(arrays[name + "_in"]).to(cuda)
         q, scale = gemm_int4.quantize_int4(w)
         assert scale == meta["cases"][name]["scale"], name

@@ -68,7 +68,7 @@ def test_e4m3_roundtrip_is_identity_on_the_grid():
 # ---------------------------------------------------------------------------------------
 def test_quantize_int4_matches_reference(golden):
     arrays, meta = golden
-    for name in ("qi4_f16_n01", "qi4_f16_n002", "qi4_f32"):
+    for name in ("qi4_f16_n01", "qi4_f16_n002", "qi4_f32", "qi4_f32_ties"):
         codes, scale = oracle.quantize_int4(arrays[name + "_in"])
         assert scale == meta["cases"][name]["scale"], name
         assert np.array_equal(codes, arrays[name + "_codes"]), name
@@ -230,20 +230,33 @@ def test_fp8_and_splitk_refs_brute_force():
 # planted mistakes: plausible wrong restatements must fail the golden checks
 # ---------------------------------------------------------------------------------------
 def test_planted_reciprocal_division_is_caught(golden):
-    """Multiplying by 1/scale instead of dividing (what torch does on GPU tensors) changes
-    some codes of the fp16 fixture: the golden check is sensitive to the division."""
+    """Multiplying by 1/scale instead of dividing (what torch does on GPU tensors): on fp32
+    inputs one to three ulps around (k + 1/2) * scale (the reference's own codes for them are
+    the qi4_f32_ties fixture) the two round to different codes, so the golden check catches
+    this restatement."""
     arrays, meta = golden
-    name = "qi4_f16_n01"
+    name = "qi4_f32_ties"
     w = arrays[name + "_in"]
     scale = meta["cases"][name]["scale"]
     inv = np.float32(1.0) / np.float32(scale)
-    t = (w.astype(np.float32) * inv).astype(np.float16).astype(np.float32)
-    wrong = np.clip(np.rint(t), -8, 7).astype(np.int8)
-    right = arrays[name + "_codes"]
-    # Either the fixture distinguishes the two, or they coincide on this input; record it.
-    differs = np.count_nonzero(wrong != right)
-    no_round16 = np.clip(np.rint(w.astype(np.float32) / np.float32(scale)), -8, 7).astype(np.int8)
-    assert differs > 0 or np.count_nonzero(no_round16 != right) > 0
+    wrong = np.clip(np.rint(w.astype(np.float32) * inv), -8, 7).astype(np.int8)
+    assert np.count_nonzero(wrong != arrays[name + "_codes"]) > 0
+    codes, _ = oracle.quantize_int4(w)
+    assert np.array_equal(codes, arrays[name + "_codes"])
+
+
+def test_reciprocal_division_same_codes_for_fp16_inputs():
+    """Why the fp16 fixtures cannot tell the two apart: an fp16 input's quotient is rounded to
+    fp16 before the round-to-integer, which absorbs the one-ulp fp32 difference. Checked on
+    every finite fp16 value up to the maximum, for several maxima."""
+    u = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    for mx in np.float16([0.7, 1.0, 1.4501545, 3.1251962, 9.487]):
+        h = u[np.isfinite(u) & (np.abs(u) <= mx)]
+        w = np.concatenate([h, np.array([mx], dtype=np.float16)]).reshape(1, -1)
+        codes, scale = oracle.quantize_int4(w)
+        inv = np.float32(1.0) / np.float32(scale)
+        t = (w.astype(np.float32) * inv).astype(np.float16).astype(np.float32)
+        assert np.array_equal(np.clip(np.rint(t), -8, 7).astype(np.int8), codes)
 
 
 def test_planted_missing_fp16_rounding_is_caught(golden):
