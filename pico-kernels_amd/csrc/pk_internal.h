@@ -94,14 +94,16 @@ int v2_f8_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb,
                  hipStream_t s);
 
 // W4A16 GEMM with the int4 B tile kept packed in LDS and read with transposing 4-bit reads,
-// 128 x 256 tiles, eight waves splitting each k-tile in halves (w4a16_tr4.hip); split 1,
-// N % 256 == 0, K % 128 == 0.
+// 128 x 256 tiles, eight waves splitting each k-tile in halves (w4a16_tr4.hip); N % 256 == 0,
+// K % (128 * split) == 0; split > 1 writes fp32 partial planes and reduces them.
 bool tr4_shape_ok(int M, int N, int K, int group, bool has_gs);
+bool tr4_split_ok(int K, int split);
+int tr4_pick_split(int M, int N, int K);
 bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ldb, int64_t ldc,
-            int c_dtype, const void* c);
+            int c_dtype, const void* c, int split);
 int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
                int group, float scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
-               hipStream_t s);
+               int split, void* workspace, hipStream_t s, bool partials_only);
 
 // 256 x 256 fp8 GEMM with a 4-stage DMA pipeline and transposing LDS reads for (K, N) B
 // (gemm_f8_v3.hip).

@@ -1,9 +1,11 @@
 // C ABI for the W4A16 matmul (gemm_int4.int4_gemm + the group-128 / split-K path) and the
 // dense fp16 split-K matmul (gemm_splitk.triton_gemm_splitk).
 //
-// Dispatch: M <= 4 runs the HBM-bound GEMV (w4a16_gemv.hip); up to 64 rows (128 for layers of
-// at most 4096 x 4096 weights) the register-dequant MFMA kernel (w4a16_skinny.hip); larger M
-// the MFMA GEMMs (B packed in LDS, or dequantised into LDS). All honour an explicit split_k.
+// Dispatch: M <= 4 runs the HBM-bound GEMV (w4a16_gemv.hip); up to 64 rows the register-dequant
+// MFMA kernel (w4a16_skinny.hip); larger M the GEMM that keeps B packed in LDS
+// (w4a16_tr4.hip, split-K where its tiles leave CUs idle) where its shape rules hold, else the
+// register-dequant kernel (up to 128 rows of layers of at most 4096 x 4096 weights) or the
+// GEMMs that dequantise into LDS. All honour an explicit split_k.
 #include "pk_internal.h"
 
 #include <atomic>
@@ -41,6 +43,7 @@ int check_w4a16(const void* a, int64_t lda, const uint32_t* qw, int64_t ldq, con
 
 struct W4Plan {
   int kernel;
+  int tr4_split;  // kKernelGemmTr4: its split (gemm holds the same split for the fallback)
   GemvPlan gemv;
   GemmPlan gemm;
   SkinnyPlan skinny;
@@ -50,6 +53,17 @@ bool make_plan(int M, int N, int K, int group_size, bool has_gs, int split_k, W4
   if (M <= 4 && gemv_plan(M, N, K, group_size, has_gs, split_k, &pl->gemv)) {
     pl->kernel = kKernelGemv;
     return true;
+  }
+  // Above the skinny kernel's 64 rows: the packed-B GEMM where its shape rules hold, with the
+  // GEMM that dequantises into LDS at the same split as its fallback (operands misaligned for
+  // it, or beyond its 32-bit offsets), so the workspace covers both.
+  if (M > 64 && tr4_shape_ok(M, N, K, group_size, has_gs)) {
+    const int s = split_k > 0 ? split_k : tr4_pick_split(M, N, K);
+    if (tr4_split_ok(K, s) && gemm_plan(M, N, K, group_size, has_gs, s, &pl->gemm)) {
+      pl->kernel = kKernelGemmTr4;
+      pl->tr4_split = s;
+      return true;
+    }
   }
   // The skinny kernel's split must also be one the GEMM accepts: the GEMM is its fallback
   // when a buffer exceeds 32-bit offsets, and the workspace size is the same (split*M*N*4).
@@ -90,6 +104,10 @@ int plan_launch(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw
   if (pl.kernel == kKernelSkinny && skinny_fits(M, N, K, lda, ldq, group, scales != nullptr))
     return skinny_launch(pl.skinny, a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype,
                          ldc, M, N, K, workspace, s, partials_only);
+  if (pl.kernel == kKernelGemmTr4 &&
+      tr4_ok(M, N, K, group, scales != nullptr, lda, ldq, ldc, c_dtype, c, pl.tr4_split))
+    return tr4_launch(a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype, ldc, M, N, K,
+                      pl.tr4_split, workspace, s, partials_only);
   return gemm_launch(pl.gemm, 1, a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype, ldc,
                      M, N, K, workspace, s, partials_only);
 }
@@ -105,12 +123,8 @@ extern "C" int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, i
               group_size, split_k);
     return PK_EUNSUPPORTED;
   }
-  int kid = pl.kernel;
-  // the unsplit GEMM runs the kernel that keeps B packed in LDS where its shape rules hold
-  // (and its operands are aligned, which this report assumes)
-  if (kid == kKernelGemm && pl.gemm.split == 1 && tr4_shape_ok(M, N, K, has_gs ? group_size : K, has_gs))
-    kid = kKernelGemmTr4;
-  if (kernel_id) *kernel_id = kid;
+  // (kKernelGemmTr4 assumes operands aligned for it: misaligned ones run kKernelGemm)
+  if (kernel_id) *kernel_id = pl.kernel;
   if (split_used) *split_used = plan_split(pl);
   return PK_OK;
 }
@@ -235,7 +249,21 @@ extern "C" int pk_w4a16_gemm_noalloc(const void* a, int64_t lda, const uint32_t*
               "groups (group %d, multiple of 32 rows)", split_k, K, group);
     return PK_EINVAL;
   }
-  const size_t need = plan_ws(pl, M, N);
+  size_t need = plan_ws(pl, M, N);
+  // An automatic packed-B split whose partials exceed the array: the largest smaller split
+  // that fits (an explicit split_k is taken as given).
+  if (split_k == 0 && pl.kernel == kKernelGemmTr4 && need > kNoAllocScratchBytes) {
+    for (int sp = pl.tr4_split - 1; sp >= 1; --sp) {
+      W4Plan alt;
+      if (!tr4_split_ok(K, sp) || !make_plan(M, N, K, group, has_gs, sp, &alt)) continue;
+      const size_t alt_need = plan_ws(alt, M, N);
+      if (alt_need <= kNoAllocScratchBytes) {
+        pl = alt;
+        need = alt_need;
+        break;
+      }
+    }
+  }
   if (need > kNoAllocScratchBytes) {
     set_error("pk_w4a16_gemm_noalloc: this shape and split need %zu bytes of split-K scratch, "
               "above the library's fixed %zu (use pk_w4a16_gemm with a workspace, or a smaller "

@@ -358,10 +358,6 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
                 int64_t ldb, const void* scales, int group, float tensor_scale, void* c,
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only) {
-  // Unsplit int4 GEMMs of at least 256 rows: the kernel that keeps B packed in LDS.
-  if (bmode == kBInt4 && pl.split == 1 && !partials_only &&
-      tr4_ok(M, N, K, group, scales != nullptr, lda, ldb, ldc, c_dtype, c))
-    return tr4_launch(a, lda, b, ldb, scales, group, tensor_scale, c, c_dtype, ldc, M, N, K, s);
   // 128/256-row tiles: the large-tile 32x32-MFMA kernel when its constraints hold.
   if (pl.cfg.bm >= 128 &&
       v2_f16_ok(M, N, K, pl.k_slice, group, scales != nullptr, lda, ldb, bmode == kBInt4))

@@ -37,9 +37,13 @@
 //  * Epilogue: the k-half-1 waves leave their accumulators in LDS; the k-half-0 waves add
 //    them, scale, convert, stage slices and store whole lines.
 //
-// Requires N % 256 == 0, K % 128 == 0, a group size that is a multiple of 64 (or per-tensor),
-// 16-byte aligned A rows and output rows, and buffers addressable with 32-bit offsets. Rows
-// past M are clamped to row M-1 for loading and never stored.
+//  * Split-K: workgroup (tile, slice) runs k-tiles slice * K / (128 S) .. and stores its fp32
+//    partial plane; a fixed-order reduce adds the S planes (for shapes whose tiles alone
+//    leave CUs idle).
+//
+// Requires N % 256 == 0, K % 128 S == 0, a group size that is a multiple of 64 (or
+// per-tensor), 16-byte aligned A rows and output rows, and buffers addressable with 32-bit
+// offsets. Rows past M are clamped to row M-1 for loading and never stored.
 #include "pk_internal.h"
 
 namespace pk {
@@ -60,6 +64,8 @@ struct Tr4Params {
   int64_t ldc;
   int M, N, K;
   int tiles_m, tiles_n;
+  int kt_slice;     // k-tiles per split-K slice (all of K when unsplit)
+  int64_t c_slice;  // elements between the slices' outputs (fp32 partial planes)
 };
 
 // global -> LDS DMA, 16 or 4 bytes per lane (lane L writes lds + 16 L / lds + 4 L)
@@ -120,7 +126,9 @@ void w4a16_tr4_kernel(Tr4Params p) {
   int tm, tn;
   tr4_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int ktiles = p.K / 128;
+  // split-K slice blockIdx.y covers k-tiles kt0 .. kt0 + kt_slice - 1
+  const int kt0 = blockIdx.y * p.kt_slice;
+  const int ktiles = p.kt_slice;
   const int last = ktiles - 1;
 
   // ---- DMA sources. A: instruction i of wave w fills rows 4 (4 w + i) .. +3 (lane L: row
@@ -147,7 +155,7 @@ void w4a16_tr4_kernel(Tr4Params p) {
   const int s_half = (wave >> 1) & 1, s_part = wave & 1;
   const int s_off = (n0 + 128 * s_part + 2 * lane) * 2;
   auto issue = [&](int kt, char* sA, char* sB, char* sS) {
-    const int k0 = kt * 128;
+    const int k0 = (kt0 + kt) * 128;
 #pragma unroll
     for (int i = 0; i < A_DMA; ++i) tr4_dma16(ra, sA + (4 * wave + i) * 1024, a_off[i], k0 * 2);
 #pragma unroll
@@ -357,6 +365,7 @@ void w4a16_tr4_kernel(Tr4Params p) {
   // XOR-swizzled by row), stored row-contiguous
   char* const stg = region;
   char* const out_base = reinterpret_cast<char*>(p.c);
+  const int64_t out_off = (int64_t)blockIdx.y * p.c_slice;
   const float oscale = p.scale;
   with_dtype(p.c_dtype, [&](auto DT) {
     constexpr int dt = decltype(DT)::value;
@@ -396,36 +405,56 @@ void w4a16_tr4_kernel(Tr4Params p) {
         const int gm = m0 + 32 * i0 + r, gn = n0 + wn0 + ch * (16 / E);
         // non-temporal: the output is written once and not read here (measured on MI355X:
         // 2048 x 4096 x 4096 about 4% faster than with ordinary stores)
-        if (gm < p.M) __builtin_nontemporal_store(val, PK_GLOBAL(pk_u4v, out_base + ((int64_t)gm * p.ldc + gn) * E));
+        if (gm < p.M) __builtin_nontemporal_store(val, PK_GLOBAL(pk_u4v, out_base + (out_off + (int64_t)gm * p.ldc + gn) * E));
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // the slice is read back before the next one lands
     }
   });
 }
 
-// The unsplit int4 GEMMs this kernel runs: at least 256 rows (one CU per 128 x 256 tile fills
-// the GPU from 2048 rows at N = 4096; below 256 rows split-K kernels have more parallelism).
+// Shapes the kernel takes (any M: rows past M are clamped for loading and never stored).
 bool tr4_shape_ok(int M, int N, int K, int group, bool has_gs) {
-  if (M < 256 || N % 256 || K % 128 || K < 128) return false;
+  if (M < 1 || N % 256 || K % 128 || K < 128) return false;
   if (has_gs && group % 64) return false;
   return true;
 }
 
+bool tr4_split_ok(int K, int split) { return split >= 1 && K % (128 * split) == 0; }
+
+// Split-K for the shape: the most equal k-slices (a divisor of K / 128, at most 16) that keep
+// tiles x slices <= 224 workgroups, one slice wherever that is 1. Measured on MI355X (M = 65 to
+// 1024 at K = 4096 and 14336, N = 4096 to 14336): each slice costs its fp32 partial plane
+// written and read back plus the reduce launch (about 7 us of fixed cost and 0.34 us per MB of
+// planes), while k-tile time rises from 1.4 us with up to 128 busy CUs to 1.9 us with all 256,
+// so the best split stops short of filling every CU.
+int tr4_pick_split(int M, int N, int K) {
+  const int kt = K / 128;
+  const int64_t tiles = cdiv(M, 128) * (int64_t)(N / 256);
+  int best = 1;
+  for (int s = 2; s <= 16 && s <= kt; ++s)
+    if (kt % s == 0 && tiles * s <= 224) best = s;
+  return best;
+}
+
 bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ldb, int64_t ldc,
-            int c_dtype, const void* c) {
-  if (!tr4_shape_ok(M, N, K, group, has_gs)) return false;
+            int c_dtype, const void* c, int split) {
+  if (!tr4_shape_ok(M, N, K, group, has_gs) || !tr4_split_ok(K, split)) return false;
   if (lda % 8) return false;
+  // unsplit: the epilogue stores 16-byte chunks of the output itself
   const int esz = c_dtype == PK_F32 ? 4 : 2;
-  if ((ldc * esz) % 16 || (reinterpret_cast<uintptr_t>(c) & 15)) return false;
+  if (split == 1 && ((ldc * esz) % 16 || (reinterpret_cast<uintptr_t>(c) & 15))) return false;
   // 32-bit buffer offsets
   if ((int64_t)M * lda * 2 >= (1ll << 31)) return false;
   if ((int64_t)K * ldb * 4 >= (1ll << 31)) return false;
   return true;
 }
 
+// split > 1: slice s writes its fp32 partial plane s of the workspace (one full k-range
+// product per (tile, slice)), then the fixed-order reduce adds the planes and applies the
+// tensor scale (partials_only: the planes alone, at `workspace` itself).
 int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
                int group, float scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
-               hipStream_t s) {
+               int split, void* workspace, hipStream_t s, bool partials_only) {
   Tr4Params p;
   p.a = reinterpret_cast<const pk_half*>(a);
   p.lda = lda;
@@ -433,20 +462,32 @@ int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const voi
   p.ldb = ldb;
   p.scales = reinterpret_cast<const pk_half*>(scales);
   p.group = group > 0 ? group : K;
-  p.scale = scale;
-  p.c = c;
-  p.c_dtype = c_dtype;
-  p.ldc = ldc;
   p.M = M;
   p.N = N;
   p.K = K;
   p.tiles_m = (int)cdiv(M, 128);
   p.tiles_n = N / 256;
-  const dim3 grid(p.tiles_m * p.tiles_n);
+  p.kt_slice = K / 128 / split;
+  float* const partials = split > 1 ? split_partials(workspace, partials_only) : nullptr;
+  if (split > 1) {
+    p.scale = 1.0f;
+    p.c = partials;
+    p.c_dtype = PK_F32;
+    p.ldc = N;
+    p.c_slice = (int64_t)M * N;
+  } else {
+    p.scale = scale;
+    p.c = c;
+    p.c_dtype = c_dtype;
+    p.ldc = ldc;
+    p.c_slice = 0;
+  }
+  const dim3 grid(p.tiles_m * p.tiles_n, split);
   if (scales) w4a16_tr4_kernel<true><<<grid, 512, 0, s>>>(p);
   else w4a16_tr4_kernel<false><<<grid, 512, 0, s>>>(p);
   PK_LAUNCH_CHECK("w4a16 gemm (int4 B in LDS)");
-  return PK_OK;
+  if (split <= 1 || partials_only) return PK_OK;
+  return splitk_reduce(partials, split, M, N, scale, c, c_dtype, ldc, s);
 }
 
 }  // namespace pk

@@ -48,12 +48,13 @@ def test_w4a16_plans():
         assert _pk.w4a16_plan(1, 11008, 4096, 128, s) == (_pk.KERNEL_GEMV, s)
     # prefill: the MFMA GEMM that keeps B packed in LDS, no split needed at 2048 rows
     assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (_pk.KERNEL_GEMM_TR4, 1)
-    assert _pk.w4a16_plan(128, 6144, 4096, 128, 0)[0] == _pk.KERNEL_GEMM
+    assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (_pk.KERNEL_GEMM_TR4, 8)
     # per-tensor mode (group_size 0) for the drop-in int4_gemm
     assert _pk.w4a16_plan(256, 512, 256, 0, 0)[0] == _pk.KERNEL_GEMM_TR4
     assert _pk.w4a16_plan(256, 520, 256, 0, 0)[0] == _pk.KERNEL_GEMM   # N % 256 != 0
     assert _pk.w4a16_plan(256, 512, 192, 0, 0)[0] == _pk.KERNEL_GEMM   # K % 128 != 0
-    assert _pk.w4a16_plan(128, 512, 256, 0, 0)[0] == _pk.KERNEL_SKINNY
+    assert _pk.w4a16_plan(128, 512, 256, 0, 0) == (_pk.KERNEL_GEMM_TR4, 2)
+    assert _pk.w4a16_plan(64, 512, 256, 0, 0)[0] == _pk.KERNEL_SKINNY
     # slices may cut a group (scales are applied per 16-row chunk) ...
     assert _pk.w4a16_plan(1, 4096, 4096, 128, 64) == (_pk.KERNEL_GEMV, 64)
     # ... but a split must divide K into multiples of the row chunk
@@ -88,20 +89,27 @@ def test_w4a16_plans_by_row_count():
     # ineligible shapes (N % 16, K % 128) stay on the GEMM
     assert _pk.w4a16_plan(8, 520, 1024, 32, 0)[0] == C
     assert _pk.w4a16_plan(8, 512, 1056, 32, 0)[0] == C
-    # M = 65..128: two row parts of the register-dequant kernel on layers of at most
-    # 4096 x 4096 weights; otherwise the LDS-tiled GEMM, whose large tiles take the most slices
-    # that fit 256 workgroups
-    assert _pk.w4a16_plan(128, 4096, 4096, 128, 0) == (S, 4)     # 32 tiles x 2 parts x 4
-    assert _pk.w4a16_plan(96, 4096, 4096, 128, 0) == (S, 4)
-    assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (C, 4)     # 48 tiles x 4
-    assert _pk.w4a16_plan(128, 14336, 4096, 128, 0) == (C, 2)    # 112 tiles x 2
-    assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (C, 8)
-    assert _pk.w4a16_plan(256, 6144, 4096, 128, 0) == (C, 4)
-    # unsplit from 256 rows on: the GEMM that keeps B packed in LDS (N % 256, K % 128, group % 64)
+    # M > 64: the GEMM that keeps B packed in LDS where its shape rules hold (N % 256,
+    # K % 128, group % 64), 128 x 256 tiles with the most equal k-slices (at most 16) that keep
+    # tiles x slices <= 224, unsplit where the tiles alone reach that
     T = _pk.KERNEL_GEMM_TR4
+    assert _pk.w4a16_plan(128, 4096, 4096, 128, 0) == (T, 8)      # 16 tiles x 8
+    assert _pk.w4a16_plan(96, 4096, 4096, 128, 0) == (T, 8)
+    assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (T, 8)      # 24 tiles x 8
+    assert _pk.w4a16_plan(128, 14336, 4096, 128, 0) == (T, 4)     # 56 tiles x 4
+    assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (T, 14)    # 16 tiles x 14 (112 k-tiles)
+    assert _pk.w4a16_plan(256, 6144, 4096, 128, 0) == (T, 4)      # 48 tiles x 4
+    assert _pk.w4a16_plan(1024, 4096, 4096, 128, 0) == (T, 1)     # 128 tiles (x 2 > 224)
     assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (T, 1)
     assert _pk.w4a16_plan(4096, 4096, 4096, 128, 0) == (T, 1)
+    assert _pk.w4a16_plan(128, 4096, 4096, 128, 4) == (T, 4)      # explicit split
+    # other shapes: two row parts of the register-dequant kernel up to 128 rows of layers of at
+    # most 4096 x 4096 weights, else the LDS-tiled GEMM (most slices fitting 256 workgroups)
+    assert _pk.w4a16_plan(128, 4000, 4096, 128, 0) == (S, 4)      # N % 256 != 0
+    assert _pk.w4a16_plan(128, 6160, 4096, 128, 0) == (C, 4)      # 49 tiles x 4
     assert _pk.w4a16_plan(2048, 4096, 4096, 32, 0) == (C, 1)      # group % 64 != 0
+    with pytest.raises(_pk.PicoKernelsError):
+        _pk.w4a16_plan(128, 4096, 4096, 128, 3)                    # 32 k-tiles, 3 slices
 
 
 def test_workspace_sizes():

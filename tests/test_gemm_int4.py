@@ -191,12 +191,11 @@ def test_llama3_sweep_shapes(M, K, N, cuda):
 
 
 def test_gemm_split_k_deterministic_and_consistent(cuda):
-    """The LDS-tiled GEMMs (M = 256 is above the register-dequant kernel's range) at every
-    split -- unsplit, the kernel that keeps B packed in LDS; split, the one that dequantises B
-    into LDS: bitwise reproducible, and splits agree up to fp32 reassociation."""
-    M, K, N = 256, 4096, 1024
-    assert _pk.w4a16_plan(M, N, K, 128, 1) == (_pk.KERNEL_GEMM_TR4, 1)
-    assert all(_pk.w4a16_plan(M, N, K, 128, s) == (_pk.KERNEL_GEMM, s) for s in (2, 4, 8))
+    """The GEMM that dequantises B into LDS (N % 256 != 0 keeps the packed-B kernel out; M = 256
+    is above the register-dequant kernel's range) at every split: bitwise reproducible, and
+    splits agree up to fp32 reassociation."""
+    M, K, N = 256, 4096, 1152
+    assert all(_pk.w4a16_plan(M, N, K, 128, s) == (_pk.KERNEL_GEMM, s) for s in (1, 2, 4, 8))
     a, w, qw, sc, codes, s16 = _group_case(M, K, N, 400, cuda)
     ag = a.to(cuda)
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
@@ -247,7 +246,7 @@ def test_int4_gemm_any_m_no_oob(cuda):
         assert oracle.rel_fro(c.cpu().numpy(), ref) < 1e-5
 
 
-@pytest.mark.parametrize("M,split", [(1, 8), (3, 16), (64, 4)])
+@pytest.mark.parametrize("M,split", [(1, 8), (3, 16), (64, 4), (128, 4)])
 def test_partials_then_reduce_equals_fused(M, split, cuda):
     """The two phases of split-K (per-slice partials, ordered reduce) reproduce the fused
     call bit for bit, and each slice's partial is that K range's product."""

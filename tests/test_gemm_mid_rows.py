@@ -35,8 +35,8 @@ def _case(M, K, N, G, seed, cuda):
 
 # (K, N, group, splits): N % 16 != 0 (automatic split 2, and unsplit); K % 128 != 0 (group
 # 32); an explicit split of 1 the register-dequant kernel rejects (wave rows > group);
-# K * N > 4096^2 (rows above 64 only)
-SHAPES = [(1024, 520, 128, (0, 1)), (1056, 512, 32, (0,)), (2048, 1024, 128, (1,)),
+# K * N > 4096^2 (rows above 64 only). Every N is off the packed-B kernel's N % 256 == 0.
+SHAPES = [(1024, 520, 128, (0, 1)), (1056, 512, 32, (0,)), (2048, 1040, 128, (1,)),
           (1024, 16400, 128, (0, 2))]
 
 

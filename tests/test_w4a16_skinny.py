@@ -122,8 +122,9 @@ def test_skinny_per_tensor_int4_gemm(M, cuda):
 @pytest.mark.parametrize("M", [9, 48, 100])
 def test_skinny_strided_activations(M, cuda):
     """A row stride larger than K (a view into a wider buffer) is read in place, for one
-    16-row block, several, and two row parts (the second part's A and C rows offset)."""
-    K, N = 1024, 512
+    16-row block, several, and two row parts (the second part's A and C rows offset). N % 256
+    != 0 keeps the packed-B GEMM out above 64 rows."""
+    K, N = 1024, 528
     a, qw, sc, codes, s16 = _case(M, K, N, 97 + M, cuda)
     assert _pk.w4a16_plan(M, N, K, 128, 0)[0] == _pk.KERNEL_SKINNY
     wide = torch.zeros(M, K + 64, dtype=torch.float16)
@@ -139,7 +140,7 @@ def test_skinny_out_view_and_dtypes(M, out_dtype, tol, cuda):
     """fp16 / bf16 output into a view of a wider buffer (ldc > N) with lda = K + 64, at two
     and four 16-row blocks (two row parts at 100): bitwise the contiguous call, the guard
     columns untouched."""
-    K, N = 2048, 1024
+    K, N = 2048, 1040
     a, qw, sc, codes, s16 = _case(M, K, N, 150 + M, cuda)
     assert _pk.w4a16_plan(M, N, K, 128, 0)[0] == _pk.KERNEL_SKINNY
     ag = a.to(cuda)
@@ -179,10 +180,11 @@ def test_skinny_per_tensor_long_wave_rows(M, K, split, cuda):
 
 
 @pytest.mark.parametrize("M", [33, 48, 64, 65, 100, 128])
-@pytest.mark.parametrize("K,N", [(4096, 4096), (1152, 784), (640, 16)])
+@pytest.mark.parametrize("K,N", [(4096, 4000), (1152, 784), (640, 16)])
 def test_skinny_four_blocks(M, K, N, cuda):
     """33 <= M <= 128: four 16-row blocks and 128-column tiles; above 64 rows two row parts
-    per tile (their workgroups paired on one XCD), the second part ragged unless M = 128."""
+    per tile (their workgroups paired on one XCD), the second part ragged unless M = 128
+    (N % 256 != 0 there: the packed-B GEMM takes the others)."""
     assert _pk.w4a16_plan(M, N, K, 128, 0)[0] == _pk.KERNEL_SKINNY
     a, qw, sc, codes, s16 = _case(M, K, N, 7 * M + K % 89 + N % 83, cuda)
     out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, 128, out_dtype=torch.float32)

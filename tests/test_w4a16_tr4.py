@@ -1,8 +1,9 @@
 """The W4A16 GEMM that keeps the int4 weights packed in LDS (w4a16_tr4.hip, plan kernel id 4):
 against the float64 dequantise-and-matmul oracle, through the C ABI, on every k-tile remainder
 its unrolled loop has (1 to 7 tiles of 128 k), ragged M, group sizes 64 / 128 / 256 and the
-per-tensor mode, strided activations, an output view wider than N, every output dtype; results
-bitwise reproducible run to run."""
+per-tensor mode, strided activations, an output view wider than N, every output dtype; split-K
+(fp32 partial planes and the ordered reduce) from 65 rows, automatic and explicit splits;
+results bitwise reproducible run to run."""
 
 from __future__ import annotations
 
@@ -40,9 +41,9 @@ def _case(M, K, N, G, seed, cuda):
 ])
 def test_tr4_matches_oracle(M, K, N, G, cuda):
     a, codes, s16, qw, sc = _case(M, K, N, G, M + K + N, cuda)
-    assert _pk.w4a16_plan(M, N, K, G, 0) == (_pk.KERNEL_GEMM_TR4, 1)
-    out = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float32)
-    again = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float32)
+    assert _pk.w4a16_plan(M, N, K, G, 1) == (_pk.KERNEL_GEMM_TR4, 1)
+    out = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float32, split_k=1)
+    again = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float32, split_k=1)
     assert torch.equal(out, again), "not bitwise reproducible"
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, G)
     err = oracle.rel_fro(out.cpu().numpy(), ref)
@@ -88,3 +89,55 @@ def test_tr4_strided_operands(cuda):
     ref = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float16)
     assert torch.equal(out_view, ref)
     assert torch.all(big[:, :128] == 7.0) and torch.all(big[:, 128 + N:] == 7.0)
+
+
+# (M, K, N, G, automatic split): the sweep's qkv layer at 128 rows, ragged rows with a one-tile
+# slice, group 64 and 256, the largest slice count (16) and a slice count that is not a power
+# of two (14 of 112 k-tiles)
+SPLIT_CASES = [
+    (128, 4096, 6144, 128, 8),
+    (65, 1024, 512, 64, 8),
+    (100, 2048, 768, 256, 16),
+    (129, 2048, 1024, 128, 16),
+    (128, 14336, 4096, 128, 14),
+]
+
+
+@pytest.mark.parametrize("M,K,N,G,auto", SPLIT_CASES)
+def test_tr4_split_k_matches_oracle(M, K, N, G, auto, cuda):
+    a, codes, s16, qw, sc = _case(M, K, N, G, 40 + M + N, cuda)
+    assert _pk.w4a16_plan(M, N, K, G, 0) == (_pk.KERNEL_GEMM_TR4, auto)
+    ag = a.to(cuda)
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, G)
+    base = None
+    for s in (0, 1, 2):
+        out = _pk.w4a16_gemm(ag, qw, sc, G, 1.0, torch.float32, split_k=s)
+        again = _pk.w4a16_gemm(ag, qw, sc, G, 1.0, torch.float32, split_k=s)
+        assert torch.equal(out, again), f"split {s} not bitwise reproducible"
+        err = oracle.rel_fro(out.cpu().numpy(), ref)
+        assert err < 1e-3, (s, err)
+        # splits differ only by fp32 reassociation
+        base = out if base is None else base
+        assert oracle.rel_fro(out.cpu().numpy(), base.cpu().numpy()) < 1e-6
+
+
+def test_tr4_split_k_per_tensor_strided_out(cuda):
+    """Per-tensor mode through split-K (the tensor scale applied by the reduce), fp16 out into
+    a view wider than N: the same bits as a contiguous output, the margins untouched."""
+    g = torch.Generator()
+    g.manual_seed(12)
+    M, K, N = 96, 2048, 512
+    a = torch.randn(M, K, generator=g).half()
+    q = torch.randint(-8, 8, (K, N), generator=g, dtype=torch.int8)
+    packed = torch.from_numpy(oracle.pack_int4_n(q.numpy()).view(np.int32).copy()).to(cuda)
+    kid, split = _pk.w4a16_plan(M, N, K, 0, 0)
+    assert kid == _pk.KERNEL_GEMM_TR4 and split > 1
+    ag = a.to(cuda)
+    out = _pk.w4a16_gemm(ag, packed, None, 0, 0.037, torch.float32)
+    ref = (a.double().numpy() @ q.double().numpy()) * 0.037
+    assert oracle.rel_fro(out.cpu().numpy(), ref) < 1e-5  # codes are exact in fp16
+    dense = _pk.w4a16_gemm(ag, packed, None, 0, 0.037, torch.float16)
+    big = torch.full((M, N + 256), 3.0, dtype=torch.float16, device=cuda)
+    _pk.w4a16_gemm(ag, packed, None, 0, 0.037, torch.float16, out=big[:, 128:128 + N])
+    assert torch.equal(big[:, 128:128 + N], dense)
+    assert torch.all(big[:, :128] == 3.0) and torch.all(big[:, 128 + N:] == 3.0)

@@ -1,8 +1,9 @@
 """pk_w4a16_gemm_noalloc (the W4A16 entry point that allocates nothing: its split-K scratch is a
 fixed device array in the library) against pk_w4a16_gemm with a caller workspace, through the
 C ABI: bitwise equal on two calls in a row, the second smaller, for the GEMV (split-K counters
-and partials in the scratch), the register-dequant kernel with its reduce launch, the LDS-tiled
-GEMM and an unsplit shape; a shape whose plan needs more scratch than the array is rejected."""
+and partials in the scratch), the register-dequant kernel with its reduce launch, the packed-B
+and LDS-tiled GEMMs and an unsplit shape; an automatic split too large for the array is
+lowered, an explicit one rejected."""
 
 from __future__ import annotations
 
@@ -40,7 +41,8 @@ def _noalloc(a, qw, sc, split, out):
     [(1, 4096, 11008, 0), (1, 1024, 512, 4)],       # GEMV, slices added through the scratch
     [(4, 4096, 4096, 16), (2, 2048, 1024, 8)],
     [(32, 4096, 6144, 0), (8, 1024, 2048, 2)],      # register-dequant kernel + reduce launch
-    [(256, 4096, 1024, 4), (128, 2048, 512, 2)],    # LDS-tiled GEMM, split-K
+    [(256, 4096, 1024, 4), (128, 2048, 512, 2)],    # packed-B GEMM, split-K + reduce launch
+    [(256, 4096, 1152, 4), (128, 2048, 520, 2)],    # LDS-tiled GEMM, split-K
     [(2048, 512, 2048, 0), (256, 512, 512, 1)],     # unsplit: no scratch used
 ])
 def test_noalloc_matches_workspace_entry_point(shapes, cuda):
@@ -52,6 +54,21 @@ def test_noalloc_matches_workspace_entry_point(shapes, cuda):
         assert _noalloc(a, qw, sc, split, got) == _pk.PK_OK, _pk.lib().pk_last_error()
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"call {i} {M}x{K}x{N} split {split}"
+
+
+def test_noalloc_smaller_automatic_split(cuda):
+    """An automatic packed-B split whose partials exceed the scratch (8 slices of 128 x 6144
+    fp32, 25 MB) runs the largest smaller split that fits (4): the same bits as the workspace
+    entry point at that split."""
+    M, K, N = 128, 4096, 6144
+    assert _pk.w4a16_plan(M, N, K, 128, 0) == (_pk.KERNEL_GEMM_TR4, 8)
+    assert _pk.lib().pk_w4a16_workspace_bytes(M, N, K, 128, 4) <= 16 << 20
+    a, qw, sc = _inputs(M, K, N, 11, cuda)
+    want = _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, split_k=4)
+    got = torch.full((M, N), float("nan"), dtype=torch.float16, device=cuda)
+    assert _noalloc(a, qw, sc, 0, got) == _pk.PK_OK, _pk.lib().pk_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
 
 
 def test_noalloc_rejects_oversized_plan(cuda):
