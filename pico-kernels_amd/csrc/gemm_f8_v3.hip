@@ -11,9 +11,11 @@
 //    8 KB and one B DMA per wave and tile.
 //  * K tiles of 64. A tile = 256 rows x 64 bytes, B tile = 64 k x 256 n (BLAYOUT 0) or
 //    256 n x 64 k (BLAYOUT 1); both go global -> LDS with buffer DMA (no VGPR staging).
-//  * Four LDS stages (32 KB each); the loads of tile t+3 are issued right after the barrier
-//    of tile t, so three tiles of loads are in flight while one is multiplied. One barrier
-//    per tile; the wait before it lets the two younger tiles' DMAs stay outstanding.
+//  * Four LDS stages (32 KB each). One barrier per tile, in its middle: each tile's first
+//    half of MFMAs runs on fragments read during the previous tile, the barrier publishes
+//    tile t+1 (whose DMAs went out two tiles earlier; tile t+2's stay outstanding), the DMAs
+//    of tile t+3 go into tile t-1's stage, and the second half of MFMAs runs while tile t+1's
+//    fragments are read into registers -- no wave waits on LDS reads after the barrier.
 //  * k-contiguous tiles (A; B^T) use 64-byte rows in 4 chunks of 16 B, chunk c of row r in
 //    slot c ^ ((r >> 2) & 3): 16 lanes reading 16 consecutive rows at one chunk hit 16
 //    distinct 16-byte bank groups.
@@ -181,75 +183,109 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = (pk_f16v){};
 
-  // The fragment reads of the tile, then its MFMAs in pairs with one of the next DMAs after
-  // each pair: issuing the DMAs in one burst fills the TA address FIFO and stalls the wave
-  // before its first MFMA.
-  auto compute_issue = [&](const char* sA, const char* sB, int ktn, char* sAn, char* sBn) {
-    pk_i8v bf[FN];
+  // Operand registers: A fragments (the first part's are reloaded for the next tile while the
+  // second part runs) and B fragments by tile parity. The first part is P1 fragment rows.
+  constexpr int HF = FM / 2;
+  constexpr int P1 = HF;
+  pk_i8v af[FM];
+  pk_i8v bf[2][FN];
+  auto read_b = [&](const char* sB, int par) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       if constexpr (BLAYOUT == 1) {
         const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sB + boff[j][0]);
         const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sB + boff[j][1]);
-        bf[j] = (pk_i8v){(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+        bf[par][j] = (pk_i8v){(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
       } else {
         const pk_i2v y0 = f8_read_tr(sB + boff[j][0]);
         const pk_i2v y1 = f8_read_tr(sB + boff[j][1]);
         const pk_i2v y2 = f8_read_tr(sB + boff[j][2]);
         const pk_i2v y3 = f8_read_tr(sB + boff[j][3]);
-        bf[j] = (pk_i8v){y0[0], y0[1], y1[0], y1[1], y2[0], y2[1], y3[0], y3[1]};
+        bf[par][j] = (pk_i8v){y0[0], y0[1], y1[0], y1[1], y2[0], y2[1], y3[0], y3[1]};
       }
     }
-    pk_i8v af[FM];
+  };
+  auto read_a = [&](const char* sA, int i0, int i1) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
+    for (int i = i0; i < i1; ++i) {
       const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sA + aoff[i][0]);
       const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sA + aoff[i][1]);
       af[i] = (pk_i8v){(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
     }
+  };
+  auto mfma_rows = [&](int i0, int i1, int par) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      __builtin_amdgcn_sched_barrier(0);
+    for (int i = i0; i < i1; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], acc[i][j], 0, 0, 0, 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      // one DMA after each MFMA pair; the last pair issues the rest
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[par][j], af[i], acc[i][j], 0, 0, 0, 0, 0, 0);
+  };
+  auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+  // NM MFMAs with ND LDS reads and NV DMAs spread between them.
+  auto pattern = [](auto NM, auto ND, auto NV) {
+    constexpr int nd = decltype(ND)::value, nv = decltype(NV)::value;
+    constexpr int nm = decltype(NM)::value;
+    constexpr int dper = (nd + nm - 1) / nm;
 #pragma unroll
-      for (int part = i; part < (i == FM - 1 ? PARTS : i + 1); ++part) issue_part(ktn, sAn, sBn, part);
+    for (int m = 0; m < nm; ++m) {
+      if (m < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (m * dper < nd) __builtin_amdgcn_sched_group_barrier(0x100, dper, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
   };
 
-  // ---- pipeline. Tiles past the end are re-reads of the last tile into a stage nobody
-  // reads, so every step has exactly the same number of DMAs in flight (4 per tile). ----
+  // ---- pipeline. Tile t (stage t % 4) starts with its B fragments and first-half A
+  // fragments in registers. First half: MFMAs of rows 0 .. HF-1 while the second half's A
+  // fragments are read. Then every wave waits for its DMAs of tile t+1 and the workgroup meets
+  // (tile t+1 is in LDS everywhere; every wave has finished tile t-1, so its stage is free)
+  // and the DMAs of tile t+3 go into that stage, between the second half's MFMAs, which also
+  // read tile t+1's B and first-half A fragments: the next tile starts with its operands in
+  // registers and no wave waits on LDS after the barrier. Tiles past the end are re-reads of
+  // the last tile into a stage nobody reads, so every tile has the same DMA count in flight.
   const int last = ktiles - 1;
   issue(0, sA0, sB0);
   issue(min(1, last), sA1, sB1);
   issue(min(2, last), sA2, sB2);
-  // s_waitcnt vmcnt(2 * PARTS) expcnt(7) lgkmcnt(15): this wave's DMAs of the oldest tile
-  // landed (the two younger tiles' stay outstanding). The barrier is a bare s_barrier:
-  // __syncthreads() adds a workgroup release fence, which waits for *every* outstanding LDS
-  // DMA (vmcnt(0)) and would serialise the pipeline. The explicit wait above already covers
-  // the data this barrier publishes, and the asm memory clobber keeps the compiler from
-  // moving LDS accesses across it.
-  constexpr int kWaitOldest = 0x0f70 | (2 * PARTS);
-  auto step = [&](int kt, char* sAc, char* sBc, char* sAn, char* sBn) {
-    __builtin_amdgcn_s_waitcnt(kWaitOldest);
+  // s_waitcnt vmcnt(n) expcnt(7) lgkmcnt(15). The barrier is a bare s_barrier: __syncthreads()
+  // adds a workgroup release fence, which waits for *every* outstanding LDS DMA (vmcnt(0)) and
+  // would serialise the pipeline. The explicit wait covers the data the barrier publishes, and
+  // the asm memory clobber keeps the compiler from moving LDS accesses across it.
+  constexpr int kWaitTile0 = 0x0f70 | (2 * PARTS);  // tile 0 landed, tiles 1 and 2 in flight
+  constexpr int kWaitNext = 0x0f70 | PARTS;         // tile t+1 landed, tile t+2 in flight
+  __builtin_amdgcn_s_waitcnt(kWaitTile0);
+  asm volatile("s_barrier" ::: "memory");
+  read_b(sB0, 0);
+  read_a(sA0, 0, P1);
+
+  auto step = [&](int kt, const char* sAc, const char* sAn, const char* sBn, char* sAx, char* sBx,
+                  auto PAR) {
+    constexpr int par = decltype(PAR)::value;
+    fence();
+    mfma_rows(0, P1, par);
+    read_a(sAc, P1, FM);
+    pattern(pk_int_c<P1 * FN>{}, pk_int_c<2 * (FM - P1)>{}, pk_int_c<0>{});
+    fence();
+    __builtin_amdgcn_s_waitcnt(kWaitNext);
     asm volatile("s_barrier" ::: "memory");
-    compute_issue(sAc, sBc, min(kt + 3, last), sAn, sBn);
-    __builtin_amdgcn_sched_barrier(0);
+    fence();
+    issue(min(kt + 3, last), sAx, sBx);
+    mfma_rows(P1, FM, par);
+    read_b(sBn, par ^ 1);
+    read_a(sAn, 0, P1);
+    pattern(pk_int_c<(FM - P1) * FN>{}, pk_int_c<(BLAYOUT == 1 ? 2 : 4) * FN + 2 * P1>{}, pk_int_c<PARTS>{});
+    fence();
   };
   int kt = 0;
   for (; kt + 3 < ktiles; kt += 4) {
-    step(kt, sA0, sB0, sA3, sB3);
-    step(kt + 1, sA1, sB1, sA0, sB0);
-    step(kt + 2, sA2, sB2, sA1, sB1);
-    step(kt + 3, sA3, sB3, sA2, sB2);
+    step(kt, sA0, sA1, sB1, sA3, sB3, pk_int_c<0>{});
+    step(kt + 1, sA1, sA2, sB2, sA0, sB0, pk_int_c<1>{});
+    step(kt + 2, sA2, sA3, sB3, sA1, sB1, pk_int_c<0>{});
+    step(kt + 3, sA3, sA0, sB0, sA2, sB2, pk_int_c<1>{});
   }
-  if (kt < ktiles) step(kt, sA0, sB0, sA3, sB3);
-  if (kt + 1 < ktiles) step(kt + 1, sA1, sB1, sA0, sB0);
-  if (kt + 2 < ktiles) step(kt + 2, sA2, sB2, sA1, sB1);
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no DMA into LDS outlives the waves
+  if (kt < ktiles) step(kt, sA0, sA1, sB1, sA3, sB3, pk_int_c<0>{});
+  if (kt + 1 < ktiles) step(kt + 1, sA1, sA2, sB2, sA0, sB0, pk_int_c<1>{});
+  if (kt + 2 < ktiles) step(kt + 2, sA2, sA3, sB3, sA1, sB1, pk_int_c<0>{});
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): no DMA into LDS outlives the waves
   mfma_drain();
 
   // ---- epilogue ----
@@ -271,7 +307,6 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
          : wave == 4 ? sB0 : wave == 5 ? sB1 : wave == 6 ? sB2 : sB3;
     else
       sW = (wave < 2 ? sA0 : wave < 4 ? sA1 : wave < 6 ? sA2 : sA3) + (wave & 1) * 8192;
-    constexpr int HF = FM / 2;  // fragments per staged half
     with_dtype(p.c_dtype, [&](auto DT) {
       constexpr int dt = decltype(DT)::value;
       constexpr int E = dt == PK_F32 ? 4 : 2;
