@@ -144,6 +144,18 @@ int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight, int64_t l
                   int c_dtype, int64_t ldc, int M, int N, int K, int split_k, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* pk_w4a16_gemm with a bias in the epilogue: C[m, n] = tensor_scale * (A @ dequant(B))[m, n]
+ * + bias[n], rounded once to the output dtype, where bias is N values of bias_dtype (PK_F32,
+ * PK_F16 or PK_BF16; null: none). Every kernel pk_w4a16_gemm runs adds it where it stores
+ * the output (its own epilogue, the split-K handoff or the reduce launch). Same plan,
+ * workspace and errors as pk_w4a16_gemm. Replaces the linear layer's `x @ w.T + b` of the
+ * reference's quantized model (quantize.py:160-181 writes w back into nn.Linear, whose
+ * forward adds the layer's bias). */
+int pk_w4a16_gemm_bias(const void* a, int64_t lda, const uint32_t* qweight, int64_t ldq,
+                       const void* scales, int group_size, float tensor_scale, const void* bias,
+                       int bias_dtype, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                       int split_k, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Which kernel pk_w4a16_gemm would run and its split factor (for reporting/benchmarks):
  * writes kernel id (1 = GEMV for M <= 4, 2 = LDS-tiled MFMA GEMM that dequantises B into LDS,
  * 3 = register-dequant MFMA kernel for 5 <= M <= 64, and M <= 128 on layers of at most

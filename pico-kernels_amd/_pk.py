@@ -53,6 +53,8 @@ _SIGNATURES = {
                              ctypes.POINTER(_i32)]),
     "pk_w4a16_gemm": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
                              _i32, _i32, _vp, _sz, _vp]),
+    "pk_w4a16_gemm_bias": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _vp, _i32,
+                                  _i64, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
     "pk_w4a16_noalloc_scratch_bytes": (_sz, []),
     "pk_w4a16_skinny_layout": (_i32, [_i32, _i32]),
     "pk_w4a16_prep_activations": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _vp]),
@@ -295,9 +297,16 @@ _ws_bytes: dict[tuple[int, int, int, int, int], int] = {}
 
 def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | None,
                group_size: int, tensor_scale: float, out_dtype: torch.dtype,
-               split_k: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+               split_k: int = 0, out: torch.Tensor | None = None,
+               bias: torch.Tensor | None = None) -> torch.Tensor:
+    """out = tensor_scale * (a @ dequant(qweight, scales)) (+ bias, N values of fp32 / fp16 /
+    bf16 added in the kernels' epilogue: pk_w4a16_gemm_bias)."""
     M, K = a.shape
     N = qweight.shape[1] * 8
+    if bias is not None and (bias.numel() != N or bias.dtype not in _TORCH_TO_PK
+                             or not bias.is_contiguous()):
+        raise ValueError(f"w4a16_gemm: bias must be {N} contiguous fp32 / fp16 / bf16 values, "
+                         f"got {tuple(bias.shape)} {bias.dtype}")
     a = _rows_ok(a)
     if qweight.stride(1) != 1:
         qweight = qweight.contiguous()
@@ -318,13 +327,23 @@ def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | No
         _ws_bytes[key] = nbytes
     stream = torch.cuda.current_stream(dev).cuda_stream
     ws = workspace(dev, nbytes, stream) if nbytes else None
-    rc = L.pk_w4a16_gemm(
+    if bias is None:
+        rc = L.pk_w4a16_gemm(
+            a.data_ptr(), a.stride(0), qweight.data_ptr(), qweight.stride(0),
+            None if scales is None else scales.data_ptr(), g, float(tensor_scale), out.data_ptr(),
+            _TORCH_TO_PK[out.dtype], out.stride(0), M, N, K, split_k,
+            None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
+        if rc != PK_OK:
+            _check(rc, "pk_w4a16_gemm")
+        return out
+    rc = L.pk_w4a16_gemm_bias(
         a.data_ptr(), a.stride(0), qweight.data_ptr(), qweight.stride(0),
-        None if scales is None else scales.data_ptr(), g, float(tensor_scale), out.data_ptr(),
-        _TORCH_TO_PK[out.dtype], out.stride(0), M, N, K, split_k,
-        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
+        None if scales is None else scales.data_ptr(), g, float(tensor_scale), bias.data_ptr(),
+        _TORCH_TO_PK[bias.dtype], out.data_ptr(), _TORCH_TO_PK[out.dtype], out.stride(0), M, N,
+        K, split_k, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+        stream)
     if rc != PK_OK:
-        _check(rc, "pk_w4a16_gemm")
+        _check(rc, "pk_w4a16_gemm_bias")
     return out
 
 

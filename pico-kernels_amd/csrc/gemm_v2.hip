@@ -62,7 +62,7 @@ struct V2Params {
   int64_t ldb;            // words (int4) or elements
   const pk_half* scales;  // int4 group scales (K/G, N) or null
   int group;
-  float scale;            // epilogue scale (tensor scale / fp8 out_scale)
+  OutEpi epi;             // epilogue: tensor scale / fp8 out_scale, optional bias
   void* c;
   int c_dtype;
   int64_t ldc;
@@ -412,7 +412,7 @@ void gemm_v3_f16_kernel(V2Params p) {
             const int byte = col * E;
             char* dst = sW + r * RB + ((((byte >> 4) ^ (r % NCH)) << 4) | (byte & 15));
             pk_f4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-            if (!part) v *= p.scale;
+            if (!part) v = p.epi(v, n0 + wn0 + col);
             if constexpr (dt == PK_F32) {
               *reinterpret_cast<pk_f4*>(dst) = v;
             } else if constexpr (dt == PK_F16) {
@@ -453,7 +453,7 @@ void gemm_v3_f16_kernel(V2Params p) {
             if (part) {
               store4_as<PK_F32>(part, (int64_t)gm * p.N + gn, v, true);
             } else {
-              v *= p.scale;
+              v = p.epi(v, gn);
               store4_as<dt>(p.c, (int64_t)gm * p.ldc + gn, v, vec);
             }
           }
@@ -657,7 +657,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_v2_f8_kernel(V2Pa
           const int gn = n0 + wn0 + 32 * j + 8 * q + en;  // N % 16 == 0: all four in or out
           if (gm < p.M && gn < p.N) {
             pk_f4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-            v *= p.scale;
+            v = p.epi(v, gn);
             store4_as<dt>(p.c, (int64_t)gm * p.ldc + gn, v, vec);
           }
         }
@@ -678,14 +678,14 @@ bool v2_f16_ok(int M, int N, int K, int k_slice, int group, bool has_gs, int64_t
 }
 
 int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, int64_t ldb,
-                  const void* scales, int group, float scale, void* c, int c_dtype, int64_t ldc,
+                  const void* scales, int group, OutEpi epi, void* c, int c_dtype, int64_t ldc,
                   int M, int N, int K, int split, void* workspace, hipStream_t s,
                   bool partials_only) {
   V2Params p;
   p.a = a; p.lda = lda; p.b = b; p.ldb = ldb;
   p.scales = reinterpret_cast<const pk_half*>(scales);
   p.group = group > 0 ? group : K;
-  p.scale = scale; p.c = c; p.c_dtype = c_dtype; p.ldc = ldc;
+  p.epi = epi; p.c = c; p.c_dtype = c_dtype; p.ldc = ldc;
   p.M = M; p.N = N; p.K = K; p.split = split; p.k_slice = K / split;
   p.partials = split > 1 ? split_partials(workspace, partials_only) : nullptr;
   const int bn = 128;
@@ -713,7 +713,7 @@ int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, 
     else gemm_v3_f16_kernel<kV2F16KN, false, 128, 2, 4><<<grid, 512, 0, s>>>(p);
   }
   PK_LAUNCH_CHECK("gemm v2 f16");
-  if (split > 1 && !partials_only) return splitk_reduce(p.partials, split, M, N, scale, c, c_dtype, ldc, s);
+  if (split > 1 && !partials_only) return splitk_reduce(p.partials, split, M, N, epi, c, c_dtype, ldc, s);
   return PK_OK;
 }
 
@@ -722,7 +722,7 @@ int v2_f8_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb,
                  hipStream_t s) {
   V2Params p;
   p.a = a8; p.lda = lda; p.b = b8; p.ldb = ldb; p.scales = nullptr; p.group = K;
-  p.scale = out_scale; p.c = c; p.c_dtype = c_dtype; p.ldc = ldc;
+  p.epi = OutEpi(out_scale); p.c = c; p.c_dtype = c_dtype; p.ldc = ldc;
   p.M = M; p.N = N; p.K = K; p.split = 1; p.k_slice = K; p.partials = nullptr;
   const bool big = (int64_t)M * N >= (int64_t)2048 * 2048;
   const int bm = big ? 256 : 128, bn = big ? 256 : 128;

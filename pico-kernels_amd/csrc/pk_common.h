@@ -96,6 +96,29 @@ __device__ __forceinline__ void store_from_f32(void* p, int dtype, int64_t i, fl
   else reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_rne(v);
 }
 
+// Output epilogue of the W4A16 matmuls: y[m, n] = scale * v (+ bias[n], a vector of N fp32 /
+// fp16 / bf16 values, when one is given), rounded once to the output dtype by the store.
+struct OutEpi {
+  float scale;
+  const void* bias;
+  int bias_dtype;
+  __host__ __device__ OutEpi(float s = 1.0f, const void* b = nullptr, int bd = PK_F16)
+      : scale(s), bias(b), bias_dtype(bd) {}
+  __device__ __forceinline__ float operator()(float v, int64_t n) const {
+    v *= scale;
+    if (bias != nullptr) v += load_as_f32(bias, bias_dtype, n);
+    return v;
+  }
+  __device__ __forceinline__ pk_f4 operator()(pk_f4 v, int64_t n) const {
+    v *= scale;
+    if (bias != nullptr) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += load_as_f32(bias, bias_dtype, n + e);
+    }
+    return v;
+  }
+};
+
 // Waits out in-flight MFMAs before vector instructions read their accumulators. Measured on
 // gfx950: when the last MFMA of an accumulation chain issues behind a predecessor that was
 // itself issued late, the wait states the compiler counts from issue are not enough and an

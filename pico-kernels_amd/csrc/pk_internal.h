@@ -30,7 +30,7 @@ bool splitk_in_l2_ok();
 int set_lds_limit_once(const void* kernel, int bytes, std::atomic<uint64_t>* done);
 
 // C = scale * sum over slices of the (S, M, N) fp32 partials, in slice order.
-int splitk_reduce(const float* partials, int S, int M, int N, float scale, void* c, int c_dtype,
+int splitk_reduce(const float* partials, int S, int M, int N, OutEpi epi, void* c, int c_dtype,
                   int64_t ldc, hipStream_t s);
 
 struct GemvPlan {
@@ -42,7 +42,7 @@ size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N);
 // Launches the GEMV; with split > 1 the slices' partials go to `workspace` and, unless
 // partials_only, the ordered reduction into C follows.
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
-                const void* scales, int group, float tensor_scale, void* c, int c_dtype,
+                const void* scales, int group, OutEpi epi, void* c, int c_dtype,
                 int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only = false);
 
@@ -64,7 +64,7 @@ bool skinny_fits(int M, int N, int K, int64_t lda, int64_t ldq, int group, bool 
 bool skinny_l2(const SkinnyPlan& pl);
 size_t skinny_workspace_bytes(const SkinnyPlan& pl, int M, int N);
 int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
-                  int64_t ldq, const void* scales, int group, float tensor_scale, void* c,
+                  int64_t ldq, const void* scales, int group, OutEpi epi, void* c,
                   int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                   bool partials_only = false);
 
@@ -78,7 +78,7 @@ struct GemmPlan {
 bool gemm_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemmPlan* out);
 size_t gemm_workspace_bytes(const GemmPlan& pl, int M, int N);
 int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const void* b,
-                int64_t ldb, const void* scales, int group, float tensor_scale, void* c,
+                int64_t ldb, const void* scales, int group, OutEpi epi, void* c,
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only = false);
 
@@ -86,7 +86,7 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
 bool v2_f16_ok(int M, int N, int K, int k_slice, int group, bool has_gs, int64_t lda, int64_t ldb,
                bool int4);
 int v2_f16_launch(int bm, int bmode, const void* a, int64_t lda, const void* b, int64_t ldb,
-                  const void* scales, int group, float scale, void* c, int c_dtype, int64_t ldc,
+                  const void* scales, int group, OutEpi epi, void* c, int c_dtype, int64_t ldc,
                   int M, int N, int K, int split, void* workspace, hipStream_t s,
                   bool partials_only);
 int v2_f8_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb, int b_layout,
@@ -102,7 +102,7 @@ int tr4_pick_split(int M, int N, int K);
 bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ldb, int64_t ldc,
             int c_dtype, const void* c, int split);
 int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
-               int group, float scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+               int group, OutEpi epi, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
                int split, void* workspace, hipStream_t s, bool partials_only);
 
 // 256 x 256 fp8 GEMM with a 4-stage DMA pipeline and transposing LDS reads for (K, N) B

@@ -1,5 +1,5 @@
 // Fixed-order split-K reduction shared by the GEMV and the MFMA GEMM:
-//   C[m, n] = scale * (((P[0][m][n] + P[1][m][n]) + P[2][m][n]) + ... + P[S-1][m][n])
+//   C[m, n] = scale * (((P[0][m][n] + P[1][m][n]) + P[2][m][n]) + ... + P[S-1][m][n]) (+ bias[n])
 // where P is the (S, M, N) fp32 workspace written by the slices. Summing in slice order on
 // the same element by the same thread makes the result independent of launch timing
 // (the reference's split-K uses fp32 atomics instead, gemm_splitk.py:64).
@@ -45,7 +45,7 @@ bool splitk_in_l2_ok() {
 // flight at once (the kernel is one memory round trip, not S of them).
 template <int S>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partials,
-                                                            int M, int N, float scale,
+                                                            int M, int N, OutEpi epi,
                                                             void* __restrict__ c, int c_dtype,
                                                             int64_t ldc) {
   const int64_t plane4 = (int64_t)M * N / 4;  // N % 8 == 0, so rows hold whole quads
@@ -61,15 +61,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const int64_t e = q * 4;
   const int64_t m = e / N, n = e - m * N;
   const int64_t o = m * ldc + n;
+  v = epi(v, n);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i] * scale);
+  for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i]);
 }
 
 // Generic slice count: the same fixed order. Loads go out in batches of 32 that are all in
 // flight together, so S slices cost ceil(S / 32) memory round trips, not S.
 constexpr int kReduceBatch = 32;
 __global__ __launch_bounds__(256) void splitk_reduce_any_kernel(const float* __restrict__ partials,
-                                                                int S, int M, int N, float scale,
+                                                                int S, int M, int N, OutEpi epi,
                                                                 void* __restrict__ c, int c_dtype,
                                                                 int64_t ldc) {
   const int64_t plane4 = (int64_t)M * N / 4;
@@ -91,22 +92,23 @@ __global__ __launch_bounds__(256) void splitk_reduce_any_kernel(const float* __r
   const int64_t e = q * 4;
   const int64_t m = e / N, n = e - m * N;
   const int64_t o = m * ldc + n;
+  v = epi(v, n);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i] * scale);
+  for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i]);
 }
 
-int splitk_reduce(const float* partials, int S, int M, int N, float scale, void* c, int c_dtype,
+int splitk_reduce(const float* partials, int S, int M, int N, OutEpi epi, void* c, int c_dtype,
                   int64_t ldc, hipStream_t s) {
   const int64_t quads = (int64_t)M * N / 4;
   const unsigned blocks = (unsigned)cdiv(quads, 256);
   switch (S) {
-    case 2: splitk_reduce_kernel<2><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
-    case 4: splitk_reduce_kernel<4><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
-    case 8: splitk_reduce_kernel<8><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
-    case 16: splitk_reduce_kernel<16><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
-    case 32: splitk_reduce_kernel<32><<<blocks, 256, 0, s>>>(partials, M, N, scale, c, c_dtype, ldc); break;
+    case 2: splitk_reduce_kernel<2><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
+    case 4: splitk_reduce_kernel<4><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
+    case 8: splitk_reduce_kernel<8><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
+    case 16: splitk_reduce_kernel<16><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
+    case 32: splitk_reduce_kernel<32><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
     default:
-      splitk_reduce_any_kernel<<<blocks, 256, 0, s>>>(partials, S, M, N, scale, c, c_dtype, ldc);
+      splitk_reduce_any_kernel<<<blocks, 256, 0, s>>>(partials, S, M, N, epi, c, c_dtype, ldc);
   }
   PK_LAUNCH_CHECK("split-K reduce");
   return PK_OK;

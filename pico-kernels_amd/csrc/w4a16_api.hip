@@ -95,20 +95,20 @@ size_t plan_ws(const W4Plan& pl, int M, int N) {
 }
 
 int plan_launch(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
-                const void* scales, int group, float tensor_scale, void* c, int c_dtype,
+                const void* scales, int group, OutEpi epi, void* c, int c_dtype,
                 int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only) {
   if (pl.kernel == kKernelGemv)
-    return gemv_launch(pl.gemv, a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype, ldc,
+    return gemv_launch(pl.gemv, a, lda, qw, ldq, scales, group, epi, c, c_dtype, ldc,
                        M, N, K, workspace, s, partials_only);
   if (pl.kernel == kKernelSkinny && skinny_fits(M, N, K, lda, ldq, group, scales != nullptr))
-    return skinny_launch(pl.skinny, a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype,
+    return skinny_launch(pl.skinny, a, lda, qw, ldq, scales, group, epi, c, c_dtype,
                          ldc, M, N, K, workspace, s, partials_only);
   if (pl.kernel == kKernelGemmTr4 &&
       tr4_ok(M, N, K, group, scales != nullptr, lda, ldq, ldc, c_dtype, c, pl.tr4_split))
-    return tr4_launch(a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype, ldc, M, N, K,
+    return tr4_launch(a, lda, qw, ldq, scales, group, epi, c, c_dtype, ldc, M, N, K,
                       pl.tr4_split, workspace, s, partials_only);
-  return gemm_launch(pl.gemm, 1, a, lda, qw, ldq, scales, group, tensor_scale, c, c_dtype, ldc,
+  return gemm_launch(pl.gemm, 1, a, lda, qw, ldq, scales, group, epi, c, c_dtype, ldc,
                      M, N, K, workspace, s, partials_only);
 }
 
@@ -159,10 +159,11 @@ extern "C" size_t pk_w4a16_workspace_bytes(int M, int N, int K, int group_size, 
   return plan_ws(pl, M, N);
 }
 
-extern "C" int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight, int64_t ldq,
-                             const void* scales, int group_size, float tensor_scale, void* c,
-                             int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
-                             void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+int w4a16_gemm_ws(const char* name, const void* a, int64_t lda, const uint32_t* qweight,
+                  int64_t ldq, const void* scales, int group_size, OutEpi epi, void* c,
+                  int c_dtype, int64_t ldc, int M, int N, int K, int split_k, void* workspace,
+                  size_t workspace_bytes, void* stream) {
   int rc = check_w4a16(a, lda, qweight, ldq, scales, group_size, c, c_dtype, ldc, M, N, K,
                        split_k);
   if (rc != PK_OK) return rc;
@@ -170,17 +171,40 @@ extern "C" int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight
   const int group = has_gs ? group_size : K;
   W4Plan pl;
   if (!make_plan(M, N, K, group, has_gs, split_k, &pl)) {
-    set_error("pk_w4a16_gemm: split_k=%d does not divide K=%d into slices of whole groups "
-              "(group %d, multiple of 32 rows)", split_k, K, group);
+    set_error("%s: split_k=%d does not divide K=%d into slices of whole groups "
+              "(group %d, multiple of 32 rows)", name, split_k, K, group);
     return PK_EINVAL;
   }
   const size_t need = plan_ws(pl, M, N);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
-    set_error("pk_w4a16_gemm: workspace of %zu bytes needed (got %zu)", need, workspace_bytes);
+    set_error("%s: workspace of %zu bytes needed (got %zu)", name, need, workspace_bytes);
     return PK_EWORKSPACE;
   }
-  return plan_launch(pl, a, lda, qweight, ldq, scales, group, tensor_scale, c, c_dtype, ldc, M,
-                     N, K, workspace, (hipStream_t)stream, false);
+  return plan_launch(pl, a, lda, qweight, ldq, scales, group, epi, c, c_dtype, ldc, M, N, K,
+                     workspace, (hipStream_t)stream, false);
+}
+}  // namespace
+
+extern "C" int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight, int64_t ldq,
+                             const void* scales, int group_size, float tensor_scale, void* c,
+                             int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  return w4a16_gemm_ws("pk_w4a16_gemm", a, lda, qweight, ldq, scales, group_size,
+                       OutEpi(tensor_scale), c, c_dtype, ldc, M, N, K, split_k, workspace,
+                       workspace_bytes, stream);
+}
+
+extern "C" int pk_w4a16_gemm_bias(const void* a, int64_t lda, const uint32_t* qweight,
+                                  int64_t ldq, const void* scales, int group_size,
+                                  float tensor_scale, const void* bias, int bias_dtype, void* c,
+                                  int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  PK_REQUIRE(bias == nullptr || bias_dtype == PK_F32 || bias_dtype == PK_F16 ||
+                 bias_dtype == PK_BF16,
+             "pk_w4a16_gemm_bias: bias dtype %d", bias_dtype);
+  return w4a16_gemm_ws("pk_w4a16_gemm_bias", a, lda, qweight, ldq, scales, group_size,
+                       OutEpi(tensor_scale, bias, bias_dtype), c, c_dtype, ldc, M, N, K,
+                       split_k, workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------------------------------

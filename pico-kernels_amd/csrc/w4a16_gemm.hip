@@ -35,7 +35,7 @@ struct GemmParams {
   int64_t ldb;    // words (int4) or elements (fp16)
   const pk_half* scales;  // int4 group scales (K/G, N) or null
   int group;
-  float tensor_scale;
+  OutEpi epi;  // tensor scale and optional bias
   void* c;
   int c_dtype;
   int64_t ldc;
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmP
         for (int r = 0; r < 4; ++r) {
           const int gm = m0 + wm0 + 16 * i + erow + r, gn = n0 + wn0 + 16 * j + ecol;
           if (gm < p.M && gn < p.N)
-            store_from_f32(p.c, p.c_dtype, (int64_t)gm * p.ldc + gn, acc[i][j][r] * p.tensor_scale);
+            store_from_f32(p.c, p.c_dtype, (int64_t)gm * p.ldc + gn, p.epi(acc[i][j][r], gn));
         }
     return;
   }
@@ -355,14 +355,14 @@ static int launch_mode(const GemmPlan& pl, const GemmParams& p, hipStream_t s) {
 }
 
 int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const void* b,
-                int64_t ldb, const void* scales, int group, float tensor_scale, void* c,
+                int64_t ldb, const void* scales, int group, OutEpi epi, void* c,
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only) {
   // 128/256-row tiles: the large-tile 32x32-MFMA kernel when its constraints hold.
   if (pl.cfg.bm >= 128 &&
       v2_f16_ok(M, N, K, pl.k_slice, group, scales != nullptr, lda, ldb, bmode == kBInt4))
     return v2_f16_launch(pl.cfg.bm, bmode == kBInt4 ? 0 : (bmode == kBDenseBF16 ? 2 : 1), a, lda, b, ldb, scales, group,
-                         tensor_scale, c, c_dtype, ldc, M, N, K, pl.split, workspace, s,
+                         epi, c, c_dtype, ldc, M, N, K, pl.split, workspace, s,
                          partials_only);
   GemmParams p;
   p.a = reinterpret_cast<const pk_half*>(a);
@@ -371,7 +371,7 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
   p.ldb = ldb;
   p.scales = reinterpret_cast<const pk_half*>(scales);
   p.group = group > 0 ? group : K;
-  p.tensor_scale = tensor_scale;
+  p.epi = epi;
   p.c = c;
   p.c_dtype = c_dtype;
   p.ldc = ldc;
@@ -387,7 +387,7 @@ int gemm_launch(const GemmPlan& pl, int bmode, const void* a, int64_t lda, const
            : bmode == kBDenseBF16 ? launch_mode<kBDenseBF16>(pl, p, s)
                                   : launch_mode<kBDenseF16>(pl, p, s);
   if (rc != PK_OK || pl.split <= 1 || partials_only) return rc;
-  return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);
+  return splitk_reduce(p.partials, pl.split, M, N, epi, c, c_dtype, ldc, s);
 }
 
 }  // namespace pk

@@ -43,7 +43,7 @@ struct GemvParams {
   int64_t ldq;
   const pk_half* scales;  // (K/G, N) or null
   int group;
-  float tensor_scale;
+  OutEpi epi;  // tensor scale and optional bias
   void* c;
   int c_dtype;
   int64_t ldc;
@@ -70,7 +70,7 @@ __device__ __forceinline__ void gemv_finish(const GemvParams& p, int tile, int s
     if (m >= p.M || col_base + col >= p.N) continue;
     const float v = fold(m, col);
     if (p.split == 1)
-      store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + col_base + col, v * p.tensor_scale);
+      store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + col_base + col, p.epi(v, col_base + col));
     else
       p.partials[((int64_t)slice * p.M + m) * p.N + col_base + col] = v;
   }
@@ -417,7 +417,7 @@ __device__ __forceinline__ void gemv_finish_l2(const GemvParams& p, int tile, in
   if constexpr (MT == 1) {
     if (col >= p.N) return;
     const float v = splitk_sum(p.partials + col, (int64_t)p.M * p.npad, p.split, slice, mine[0]);
-    store_from_f32(p.c, p.c_dtype, col, v * p.tensor_scale);
+    store_from_f32(p.c, p.c_dtype, col, p.epi(v, col));
   } else {
     // Several rows: quads of 4 columns, all slices of a quad loaded at once (16 at a time),
     // so the last workgroup waits for ceil(MT / 4) rounds of loads, not MT.
@@ -439,8 +439,9 @@ __device__ __forceinline__ void gemv_finish_l2(const GemvParams& p, int tile, in
         }
       }
       const int64_t o = (int64_t)m * p.ldc + c;
+      v = p.epi(v, c);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) store_from_f32(p.c, p.c_dtype, o + e, v[e] * p.tensor_scale);
+      for (int e = 0; e < 4; ++e) store_from_f32(p.c, p.c_dtype, o + e, v[e]);
     }
   }
 }
@@ -568,7 +569,7 @@ static bool gemv_mfma_ready(const GemvPlan& pl, const void* a, int64_t lda, cons
 }
 
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
-                int64_t ldq, const void* scales, int group, float tensor_scale, void* c,
+                int64_t ldq, const void* scales, int group, OutEpi epi, void* c,
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace,
                 hipStream_t s, bool partials_only) {
   GemvParams p;
@@ -578,7 +579,7 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
   p.ldq = ldq;
   p.scales = reinterpret_cast<const pk_half*>(scales);
   p.group = group > 0 ? group : K;
-  p.tensor_scale = tensor_scale;
+  p.epi = epi;
   p.c = c;
   p.c_dtype = c_dtype;
   p.ldc = ldc;
@@ -618,7 +619,7 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
   }
   PK_LAUNCH_CHECK("w4a16 gemv");
   if (pl.split > 1 && !partials_only)
-    return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);
+    return splitk_reduce(p.partials, pl.split, M, N, epi, c, c_dtype, ldc, s);
   return PK_OK;
 }
 

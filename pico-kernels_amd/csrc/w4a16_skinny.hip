@@ -58,7 +58,7 @@ struct SkinnyParams {
   int64_t ldq;
   const pk_half* scales;  // (K/G, N) or null
   int group;
-  float tensor_scale;
+  OutEpi epi;  // tensor scale and optional bias
   void* c;
   int c_dtype;
   int64_t ldc;
@@ -304,8 +304,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
         }
       }
       const int64_t o = (int64_t)(m0 + m) * p.ldc + col;
+      v = p.epi(v, col);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) store_from_f32(p.c, p.c_dtype, o + e, v[e] * p.tensor_scale);
+      for (int e = 0; e < 4; ++e) store_from_f32(p.c, p.c_dtype, o + e, v[e]);
     }
     return;
   }
@@ -317,7 +318,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
     if constexpr (NB == 2) v = red[0][m][cl] + red[1][m][cl];
     else v = (red[0][m][cl] + red[2][m][cl]) + (red[1][m][cl] + red[3][m][cl]);
     if (p.split == 1)
-      store_from_f32(p.c, p.c_dtype, (int64_t)(m0 + m) * p.ldc + col, v * p.tensor_scale);
+      store_from_f32(p.c, p.c_dtype, (int64_t)(m0 + m) * p.ldc + col, p.epi(v, col));
     else
       p.partials[((int64_t)slice * p.M + m0 + m) * p.N + col] = v;
   }
@@ -487,7 +488,7 @@ size_t skinny_workspace_bytes(const SkinnyPlan& pl, int M, int N) {
 }
 
 int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
-                  int64_t ldq, const void* scales, int group, float tensor_scale, void* c,
+                  int64_t ldq, const void* scales, int group, OutEpi epi, void* c,
                   int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                   bool partials_only) {
   SkinnyParams p;
@@ -497,7 +498,7 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
   p.ldq = ldq;
   p.scales = reinterpret_cast<const pk_half*>(scales);
   p.group = scales ? group : K;
-  p.tensor_scale = tensor_scale;
+  p.epi = epi;
   p.c = c;
   p.c_dtype = c_dtype;
   p.ldc = ldc;
@@ -516,7 +517,7 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
   else launch_skinny_cfg<false>(pl, p, l2, s);
   PK_LAUNCH_CHECK("w4a16 skinny");
   if (pl.split > 1 && !partials_only && !l2)
-    return splitk_reduce(p.partials, pl.split, M, N, tensor_scale, c, c_dtype, ldc, s);
+    return splitk_reduce(p.partials, pl.split, M, N, epi, c, c_dtype, ldc, s);
   return PK_OK;
 }
 

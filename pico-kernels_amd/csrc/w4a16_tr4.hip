@@ -58,7 +58,7 @@ struct Tr4Params {
   int64_t ldb;            // words
   const pk_half* scales;  // (K / group, N) or null
   int group;
-  float scale;            // epilogue scale (tensor scale)
+  OutEpi epi;             // epilogue: tensor scale and optional bias
   void* c;
   int c_dtype;
   int64_t ldc;
@@ -366,7 +366,6 @@ void w4a16_tr4_kernel(Tr4Params p) {
   char* const stg = region;
   char* const out_base = reinterpret_cast<char*>(p.c);
   const int64_t out_off = (int64_t)blockIdx.y * p.c_slice;
-  const float oscale = p.scale;
   with_dtype(p.c_dtype, [&](auto DT) {
     constexpr int dt = decltype(DT)::value;
     constexpr int E = dt == PK_F32 ? 4 : 2;
@@ -384,8 +383,9 @@ void w4a16_tr4_kernel(Tr4Params p) {
             const int r = 32 * ii + l32, col = 32 * j + 8 * qq + 4 * lh;
             const int byte = col * E;
             char* dst = stg + r * RB + ((((byte >> 4) ^ (r % NCH)) << 4) | (byte & 15));
-            const pk_f4 v = {acc[i0 + ii][j][4 * qq] * oscale, acc[i0 + ii][j][4 * qq + 1] * oscale,
-                             acc[i0 + ii][j][4 * qq + 2] * oscale, acc[i0 + ii][j][4 * qq + 3] * oscale};
+            const pk_f4 v = p.epi((pk_f4){acc[i0 + ii][j][4 * qq], acc[i0 + ii][j][4 * qq + 1],
+                                          acc[i0 + ii][j][4 * qq + 2], acc[i0 + ii][j][4 * qq + 3]},
+                                  n0 + wn0 + col);
             if constexpr (dt == PK_F32) {
               *reinterpret_cast<pk_f4*>(dst) = v;
             } else if constexpr (dt == PK_F16) {
@@ -453,7 +453,7 @@ bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ld
 // product per (tile, slice)), then the fixed-order reduce adds the planes and applies the
 // tensor scale (partials_only: the planes alone, at `workspace` itself).
 int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
-               int group, float scale, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+               int group, OutEpi epi, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
                int split, void* workspace, hipStream_t s, bool partials_only) {
   Tr4Params p;
   p.a = reinterpret_cast<const pk_half*>(a);
@@ -470,13 +470,13 @@ int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const voi
   p.kt_slice = K / 128 / split;
   float* const partials = split > 1 ? split_partials(workspace, partials_only) : nullptr;
   if (split > 1) {
-    p.scale = 1.0f;
+    p.epi = OutEpi(1.0f);
     p.c = partials;
     p.c_dtype = PK_F32;
     p.ldc = N;
     p.c_slice = (int64_t)M * N;
   } else {
-    p.scale = scale;
+    p.epi = epi;
     p.c = c;
     p.c_dtype = c_dtype;
     p.ldc = ldc;
@@ -487,7 +487,7 @@ int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const voi
   else w4a16_tr4_kernel<false><<<grid, 512, 0, s>>>(p);
   PK_LAUNCH_CHECK("w4a16 gemm (int4 B in LDS)");
   if (split <= 1 || partials_only) return PK_OK;
-  return splitk_reduce(partials, split, M, N, scale, c, c_dtype, ldc, s);
+  return splitk_reduce(partials, split, M, N, epi, c, c_dtype, ldc, s);
 }
 
 }  // namespace pk

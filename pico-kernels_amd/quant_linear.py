@@ -163,17 +163,17 @@ class QuantLinear(nn.Module):
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.in_features)
         out_dtype = x.dtype if x.dtype in _OUT_DTYPES else torch.float16
+        # the bias is added in the matmul's epilogue (before the one rounding to out_dtype)
         if self.scheme == "per_input":
             # x * s / max s in fp16 (the input cast in the same pass), then max s in the epilogue
             s = self.scales if self.scales.dtype == torch.float32 else self.scales.float()
             xp = _pk.w4a16_prep_activations(x2, s, 1.0 / self._smax)
-            y = _pk.w4a16_gemm(xp, self.qweight, None, 0, self._smax, out_dtype)
+            y = _pk.w4a16_gemm(xp, self.qweight, None, 0, self._smax, out_dtype, bias=self.bias)
         else:
             xp = x2 if x2.dtype == torch.float16 else _pk.w4a16_prep_activations(x2, None, 1.0)
             s = self.scales if self.scales.dtype == torch.float16 else self.scales.half()
-            y = _pk.w4a16_gemm(xp, self.qweight, s, self.group_size, 1.0, out_dtype)
-        if self.bias is not None:
-            y = y + self.bias.to(out_dtype)
+            y = _pk.w4a16_gemm(xp, self.qweight, s, self.group_size, 1.0, out_dtype,
+                               bias=self.bias)
         return y.reshape(*lead, self.out_features)
 
     def _refresh(self) -> None:
