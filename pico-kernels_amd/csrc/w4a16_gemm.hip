@@ -1,6 +1,6 @@
 // MFMA GEMM for W4A16 prefill / batched decode, and the dense fp16 split-K GEMM.
 //
-// C[M,N] = tensor_scale * A[M,K] (fp16) @ B[K,N], fp32 accumulate on
+// C[M,N] = tensor_scale * A[M,K] (fp16) @ B[K,N] (+ bias[N]), fp32 accumulate on
 // v_mfma_f32_16x16x32_f16, with B either
 //   * packed int4 (pack_int4_n words, gemm_int4.py:65-72), dequantised while it is staged
 //     into LDS: q (exact in fp16 via the 0x6400 exponent trick) times the fp16 group scale,

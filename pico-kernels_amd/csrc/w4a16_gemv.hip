@@ -1,6 +1,6 @@
 // W4A16 skinny GEMV (M <= 4) with deterministic split-K -- the HBM-bound decode path.
 //
-// Computes C[m, n] = tensor_scale * sum_k A[m, k] * q[k, n] * S[k / G, n] for the packed
+// Computes C[m, n] = tensor_scale * sum_k A[m, k] * q[k, n] * S[k / G, n] (+ bias[n]) for the packed
 // layout of gemm_int4.pack_int4_n (gemm_int4.py:65-72) viewed as int32 words: word j of
 // row k holds columns 8j..8j+7, nibble i = column 8j+i, two's complement.
 //

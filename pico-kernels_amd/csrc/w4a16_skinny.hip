@@ -1,5 +1,5 @@
 // W4A16 matmul for 5 <= M <= 128 activation rows: the HBM-bound middle between the GEMV
-// (M <= 4) and the LDS-tiled GEMM. C = tensor_scale * A (M, K) fp16 @ deq(W) (K, N), with W in
+// (M <= 4) and the LDS-tiled GEMM. C = tensor_scale * A (M, K) fp16 @ deq(W) (K, N) (+ bias), W in
 // the packed layout of gemm_int4.pack_int4_n (gemm_int4.py:65-72) viewed as int32 words
 // (word j of row k = columns 8j..8j+7, nibble i = column 8j+i) and the group scales of
 // quantize.rtn_layer along K (quantize.py:63-68).
