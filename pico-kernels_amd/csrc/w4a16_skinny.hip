@@ -470,13 +470,17 @@ static void launch_skinny_cfg(const SkinnyPlan& pl, const SkinnyParams& p, bool 
 }
 
 // The split-K slices hand off through L2 in the launch (no reduce launch) for one 16-row
-// block. Measured on the Llama-3-8B layers (graphs over rotating weights): M = 8 gains about
-// 1 us on every layer (qkv 11.3 -> 10.3, o_proj 9.4 -> 8.2, gate_up 15.1 -> 14.3, down
-// 15.9 -> 14.8 us); with two or four blocks the last workgroup's gather of M * split
-// partials per tile was slower on the larger layers (gate_up M = 32: 22.3 against 21.5 us,
-// down M = 32: 25.9 against 22.6), so those keep the reduce launch.
+// block, and for two on layers of at most 4096 x 6144 weights. Measured on the Llama-3-8B
+// layers (graphs over rotating weights): M = 8 gains about 1 us on every layer (qkv 11.3 ->
+// 10.3, o_proj 9.4 -> 8.2, gate_up 15.1 -> 14.3, down 15.9 -> 14.8 us); at M = 32 the last
+// workgroup's gather of 32 * split partial rows per tile pays on the smaller layers (qkv
+// 13.85 -> 13.1, o_proj 12.1 -> 10.6 us) but not on the larger (gate_up 22.1 -> 22.8, down
+// 22.7 -> 26.1), and with four blocks it was slower everywhere, so those keep the reduce
+// launch.
 bool skinny_l2(const SkinnyPlan& pl) {
-  return pl.split > 1 && pl.mb == 1 && pl.tiles * pl.row_parts <= kWsMaxTiles &&
+  const int64_t weights = (int64_t)pl.split * pl.k_slice * pl.tiles * 16 * pl.cpl;
+  const bool blocks_ok = pl.mb == 1 || (pl.mb == 2 && weights <= 4096ll * 6144);
+  return pl.split > 1 && blocks_ok && pl.tiles * pl.row_parts <= kWsMaxTiles &&
          splitk_in_l2_ok();
 }
 
