@@ -112,6 +112,18 @@ def test_group_quant_matches_oracle(golden, cuda):
         assert np.array_equal(sc.cpu().numpy(), s16)
 
 
+@pytest.mark.parametrize("K,N", [(4096, 11008), (14336, 4096)])
+def test_group_quant_bitwise_at_full_size(K, N, cuda):
+    """The GPU's packed codes and fp16 scales at the headline GEMV's and the down
+    projection's sizes are the oracle's bit for bit, so the full-size matmul parity tests
+    (which hand the oracle its own codes) compare the same weights."""
+    w = (torch.randn(K, N, generator=_gen(40 + K % 13)) * 0.02).half()
+    qw, sc = gemm_int4.quantize_int4_group(w.to(cuda), 128)
+    codes, _, s16 = oracle.rtn_group_codes(w.numpy(), 4, 128)
+    assert np.array_equal(qw.cpu().numpy().view(np.uint8), oracle.pack_int4_n(codes))
+    assert np.array_equal(sc.cpu().numpy().view(np.uint16), s16.view(np.uint16))
+
+
 # ---------------------------------------------------------------------------------------
 # W4A16 matmul parity
 # ---------------------------------------------------------------------------------------
