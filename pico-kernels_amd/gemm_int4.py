@@ -75,13 +75,19 @@ def int4_gemm(a: torch.Tensor, w_packed: torch.Tensor, scale: float,
     Returns a new fp32 ``(M, N)`` tensor. The ``BLOCK_*`` arguments are accepted for
     signature compatibility; tiles are chosen by the library. Unlike the reference kernel,
     any M is valid (no out-of-bounds rows); N must be a multiple of 8 and K of 32.
+
+    bf16 activations (admitted by the reference wrapper, gemm_int4.py:78) are converted to
+    fp16 in one pass (``pk_w4a16_prep_activations``) and run on the fp16 kernels: the
+    conversion is exact for 2^-17 <= |x| <= 65504 (and 0), so there the products with the
+    exact integer codes, and the fp32 sums, are those of a bf16 dot; smaller magnitudes keep
+    fp16's subnormal precision and larger ones overflow.
     """
     assert a.is_cuda and a.dtype in (torch.float16, torch.bfloat16)
     M, K = a.shape
     K2, N_half = w_packed.shape
     assert K2 == K, "int4_gemm: w_packed must be (K, N//2) for a of shape (M, K)"
-    if a.dtype != torch.float16:
-        raise NotImplementedError("int4_gemm: the MI355X kernels take fp16 activations")
+    if a.dtype == torch.bfloat16:
+        a = _pk.w4a16_prep_activations(a, None, 1.0)
     N = N_half * 2
     assert N % 8 == 0, "int4_gemm: N must be a multiple of 8 (whole int32 words)"
     wp = w_packed if w_packed.is_cuda else w_packed.to(a.device)

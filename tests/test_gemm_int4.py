@@ -258,6 +258,27 @@ def test_int4_gemm_any_m_no_oob(cuda):
         assert oracle.rel_fro(c.cpu().numpy(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("M", [1, 8, 100, 256])
+def test_int4_gemm_bf16_activations(M, cuda):
+    """bf16 activations (the reference wrapper admits them, gemm_int4.py:78): values within
+    fp16's range convert exactly, so the result is bitwise the fp16 call on the same values
+    (edge values 0, 2^-17 and -60000 included), and within 1e-5 of the float64 product of the
+    bf16 values and the codes."""
+    w = torch.randn(512, 512, generator=_gen(9)).half()
+    w_q, scale = gemm_int4.quantize_int4(w.to(cuda))
+    wp = gemm_int4.pack_int4_n(w_q)
+    a = (torch.randn(M, 512, generator=_gen(20 + M)) * 3.0).to(torch.bfloat16)
+    got = gemm_int4.int4_gemm(a.to(cuda), wp, scale)
+    assert got.dtype == torch.float32
+    assert torch.equal(got, gemm_int4.int4_gemm(a.to(cuda).half(), wp, scale))
+    ref = (a.double().numpy() @ w_q.cpu().double().numpy()) * scale
+    assert oracle.rel_fro(got.cpu().numpy(), ref) < 1e-5
+    edge = a.clone()
+    edge[0, :4] = torch.tensor([0.0, 2.0 ** -17, -60000.0, 1.5e-3], dtype=torch.bfloat16)
+    assert torch.equal(gemm_int4.int4_gemm(edge.to(cuda), wp, scale),
+                       gemm_int4.int4_gemm(edge.to(cuda).half(), wp, scale))
+
+
 @pytest.mark.parametrize("M,split", [(1, 8), (3, 16), (64, 4), (128, 4)])
 def test_partials_then_reduce_equals_fused(M, split, cuda):
     """The two phases of split-K (per-slice partials, ordered reduce) reproduce the fused
