@@ -42,11 +42,12 @@ bool splitk_in_l2_ok() {
 }
 
 // One thread per 4 consecutive outputs; the S slice loads are unrolled so they are all in
-// flight at once (the kernel is one memory round trip, not S of them).
-template <int S>
+// flight at once (the kernel is one memory round trip, not S of them). The four outputs go
+// out as one 8-byte (fp16 / bf16) or 16-byte (fp32) store when `vec` (aligned rows).
+template <int S, int DT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partials,
                                                             int M, int N, OutEpi epi,
-                                                            void* __restrict__ c, int c_dtype,
+                                                            void* __restrict__ c, bool vec,
                                                             int64_t ldc) {
   const int64_t plane4 = (int64_t)M * N / 4;  // N % 8 == 0, so rows hold whole quads
   const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -61,17 +62,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const int64_t e = q * 4;
   const int64_t m = e / N, n = e - m * N;
   const int64_t o = m * ldc + n;
-  v = epi(v, n);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i]);
+  store4_as<DT>(c, o, epi(v, n), vec);
 }
 
 // Generic slice count: the same fixed order. Loads go out in batches of 32 that are all in
 // flight together, so S slices cost ceil(S / 32) memory round trips, not S.
 constexpr int kReduceBatch = 32;
+template <int DT>
 __global__ __launch_bounds__(256) void splitk_reduce_any_kernel(const float* __restrict__ partials,
                                                                 int S, int M, int N, OutEpi epi,
-                                                                void* __restrict__ c, int c_dtype,
+                                                                void* __restrict__ c, bool vec,
                                                                 int64_t ldc) {
   const int64_t plane4 = (int64_t)M * N / 4;
   const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -92,24 +92,30 @@ __global__ __launch_bounds__(256) void splitk_reduce_any_kernel(const float* __r
   const int64_t e = q * 4;
   const int64_t m = e / N, n = e - m * N;
   const int64_t o = m * ldc + n;
-  v = epi(v, n);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) store_from_f32(c, c_dtype, o + i, v[i]);
+  store4_as<DT>(c, o, epi(v, n), vec);
 }
 
 int splitk_reduce(const float* partials, int S, int M, int N, OutEpi epi, void* c, int c_dtype,
                   int64_t ldc, hipStream_t s) {
   const int64_t quads = (int64_t)M * N / 4;
   const unsigned blocks = (unsigned)cdiv(quads, 256);
-  switch (S) {
-    case 2: splitk_reduce_kernel<2><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
-    case 4: splitk_reduce_kernel<4><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
-    case 8: splitk_reduce_kernel<8><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
-    case 16: splitk_reduce_kernel<16><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
-    case 32: splitk_reduce_kernel<32><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, c_dtype, ldc); break;
-    default:
-      splitk_reduce_any_kernel<<<blocks, 256, 0, s>>>(partials, S, M, N, epi, c, c_dtype, ldc);
-  }
+  const int esz = c_dtype == PK_F32 ? 4 : 2;
+  const bool vec = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & (4 * esz - 1)) == 0;
+  auto go = [&](auto DTC) {
+    constexpr int dt = decltype(DTC)::value;
+    switch (S) {
+      case 2: splitk_reduce_kernel<2, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
+      case 4: splitk_reduce_kernel<4, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
+      case 8: splitk_reduce_kernel<8, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
+      case 16: splitk_reduce_kernel<16, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
+      case 32: splitk_reduce_kernel<32, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
+      default:
+        splitk_reduce_any_kernel<dt><<<blocks, 256, 0, s>>>(partials, S, M, N, epi, c, vec, ldc);
+    }
+  };
+  if (c_dtype == PK_F32) go(pk_int_c<PK_F32>{});
+  else if (c_dtype == PK_F16) go(pk_int_c<PK_F16>{});
+  else go(pk_int_c<PK_BF16>{});
   PK_LAUNCH_CHECK("split-K reduce");
   return PK_OK;
 }
