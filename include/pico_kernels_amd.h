@@ -159,8 +159,9 @@ int pk_w4a16_gemm_bias(const void* a, int64_t lda, const uint32_t* qweight, int6
 /* Which kernel pk_w4a16_gemm would run and its split factor (for reporting/benchmarks):
  * writes kernel id (1 = GEMV for M <= 4, 2 = LDS-tiled MFMA GEMM that dequantises B into LDS,
  * 3 = register-dequant MFMA kernel for 5 <= M <= 64, and M <= 128 on layers of at most
- * 4096 x 4096 weights, 4 = MFMA GEMM that keeps B packed in LDS, for unsplit M >= 256,
- * N % 256 == 0, K % 128 == 0, group % 64 == 0, assuming 16-byte aligned operands) and the
+ * 4096 x 4096 weights the next kernel does not take, 4 = MFMA GEMM that keeps B packed in
+ * LDS, for M > 64 with N % 256 == 0, K % 128 == 0, group % 64 == 0 (split-K with a reduce
+ * launch where its tiles leave CUs idle), assuming 16-byte aligned operands) and the
  * effective split. */
 int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_id,
                   int* split_used);
