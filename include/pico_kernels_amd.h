@@ -130,10 +130,11 @@ int pk_cast_e4m3(const void* x, int x_dtype, int64_t n, float scale, uint8_t* ou
  * (K/s a multiple of 8 for M <= 4, of 64 otherwise) whose fp32 partial sums are reduced in a
  * fixed order (results are bitwise reproducible run to run).
  * workspace: pk_w4a16_workspace_bytes() bytes, zero-filled once at allocation (split-K
- * arrival counters, then fp32 partials of the slices). For M <= 4 on MI355X the slices of a
- * column tile are placed on one XCD and the last to finish adds them through that XCD's L2,
- * in the same fixed order as pk_splitk_reduce (bitwise the same result), so no second
- * launch is needed; larger M adds them with a pk_splitk_reduce launch.
+ * arrival counters, then fp32 partials of the slices). For M <= 16 on MI355X (M <= 32 on
+ * layers of at most 4096 x 6144 weights) the slices of a column tile are placed on one XCD
+ * and the last to finish adds them through that XCD's L2, in the same fixed order as
+ * pk_splitk_reduce (bitwise the same result), so no second launch is needed; larger M adds
+ * them with a pk_splitk_reduce launch (pk_w4a16_launches reports which).
  * Replaces gemm_int4.int4_gemm (gemm_int4.py:75-92, per-tensor mode, the `c * scale`
  * epilogue fused) and provides the group-128 / split-K W4A16 path; the split-K semantics
  * (contiguous K slices of K / split_k) follow gemm_splitk.triton_gemm_splitk
