@@ -55,6 +55,8 @@ _SIGNATURES = {
                              _i32, _i32, _vp, _sz, _vp]),
     "pk_w4a16_gemm_bias": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _vp, _i32,
                                   _i64, _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "pk_w4a16_gemm_tiled": (_i32, [_vp, _i64, _vp, _vp, _i32, _f32, _vp, _i32, _vp, _i32, _i64,
+                                   _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
     "pk_w4a16_noalloc_scratch_bytes": (_sz, []),
     "pk_w4a16_skinny_layout": (_i32, [_i32, _i32]),
     "pk_w4a16_prep_activations": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _vp]),
@@ -295,12 +297,35 @@ def _rows_ok(t: torch.Tensor) -> torch.Tensor:
 _ws_bytes: dict[tuple[int, int, int, int, int], int] = {}
 
 
+def tiles_ok(K: int, N: int, group_size: int) -> bool:
+    """Shapes whose weights pk_w4a16_gemm_tiled reads in column tiles (group 0: per-tensor)."""
+    return N % 256 == 0 and K % 256 == 0 and group_size % 64 == 0
+
+
+def tile_weights(qweight: torch.Tensor) -> torch.Tensor:
+    """(K, N/8) int32 words in pack_int4_n order -> the same codes in column tiles: the 32
+    words of each 256-column tile contiguous over all K rows (still shaped (K, N/8))."""
+    K, W = qweight.shape
+    if W % 32:
+        raise ValueError(f"tile_weights: N = {8 * W} is not a multiple of 256")
+    return qweight.reshape(K, W // 32, 32).permute(1, 0, 2).contiguous().view(K, W)
+
+
+def untile_weights(qtiled: torch.Tensor) -> torch.Tensor:
+    """Inverse of tile_weights: column tiles -> (K, N/8) words in pack_int4_n order."""
+    K, W = qtiled.shape
+    if W % 32:
+        raise ValueError(f"untile_weights: N = {8 * W} is not a multiple of 256")
+    return qtiled.contiguous().view(W // 32, K, 32).permute(1, 0, 2).contiguous().view(K, W)
+
+
 def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | None,
                group_size: int, tensor_scale: float, out_dtype: torch.dtype,
                split_k: int = 0, out: torch.Tensor | None = None,
-               bias: torch.Tensor | None = None) -> torch.Tensor:
+               bias: torch.Tensor | None = None, tiled: bool = False) -> torch.Tensor:
     """out = tensor_scale * (a @ dequant(qweight, scales)) (+ bias, N values of fp32 / fp16 /
-    bf16 added in the kernels' epilogue: pk_w4a16_gemm_bias)."""
+    bf16 added in the kernels' epilogue: pk_w4a16_gemm_bias). ``tiled``: qweight holds the
+    codes in column tiles (tile_weights; pk_w4a16_gemm_tiled)."""
     M, K = a.shape
     N = qweight.shape[1] * 8
     if bias is not None and (bias.numel() != N or bias.dtype not in _TORCH_TO_PK
@@ -327,6 +352,19 @@ def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | No
         _ws_bytes[key] = nbytes
     stream = torch.cuda.current_stream(dev).cuda_stream
     ws = workspace(dev, nbytes, stream) if nbytes else None
+    if tiled:
+        if not qweight.is_contiguous():
+            raise ValueError("w4a16_gemm: column-tile weights must be contiguous")
+        rc = L.pk_w4a16_gemm_tiled(
+            a.data_ptr(), a.stride(0), qweight.data_ptr(),
+            None if scales is None else scales.data_ptr(), g, float(tensor_scale),
+            None if bias is None else bias.data_ptr(),
+            _TORCH_TO_PK[bias.dtype] if bias is not None else PK_F16, out.data_ptr(),
+            _TORCH_TO_PK[out.dtype], out.stride(0), M, N, K, split_k,
+            None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
+        if rc != PK_OK:
+            _check(rc, "pk_w4a16_gemm_tiled")
+        return out
     if bias is None:
         rc = L.pk_w4a16_gemm(
             a.data_ptr(), a.stride(0), qweight.data_ptr(), qweight.stride(0),

@@ -20,6 +20,20 @@ inline unsigned* ws_counters(void* ws) { return reinterpret_cast<unsigned*>(ws);
 inline float* split_partials(void* ws, bool partials_only) {
   return partials_only ? reinterpret_cast<float*>(ws) : ws_partials(ws);
 }
+// Where the packed int4 weight words live. Rows (gemm_int4.pack_int4_n's layout viewed as a
+// (K, ldq) int32 array): word w of row k at k * ldq + w. Column tiles (pk_w4a16_gemm_tiled):
+// the 32 words (256 columns) of tile t = w / 32 are contiguous over all K rows, word w of row
+// k at (w / 32) * 32 K + 32 k + w % 32. A kernel reads a 16-byte chunk (four words of one
+// tile) at byte (w / 32) * tile_bytes + k * row_bytes + (w % 32) * 4, which is k * ldq * 4 +
+// w * 4 for rows.
+struct QLayout {
+  int row_bytes;   // between consecutive rows of one tile: ldq * 4, or 128
+  int tile_bytes;  // between consecutive 256-column tiles: 128, or K * 128
+};
+inline QLayout qlayout(bool tiled, int64_t ldq, int K) {
+  return tiled ? QLayout{128, K * 128} : QLayout{(int)(ldq * 4), 128};
+}
+
 // Host: split-K slices may hand off through one XCD's L2 on the current device (its XCC count
 // divides 8; the environment variable PK_SPLITK_IN_L2=0 turns it off).
 bool splitk_in_l2_ok();
@@ -41,10 +55,14 @@ bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvP
 size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N);
 // Launches the GEMV; with split > 1 the slices' partials go to `workspace` and, unless
 // partials_only, the ordered reduction into C follows.
+// `tiled`: the weights are in column tiles (QLayout; the MFMA kernel only, see gemv_tiled_ok).
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
                 const void* scales, int group, OutEpi epi, void* c, int c_dtype,
                 int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
-                bool partials_only = false);
+                bool partials_only = false, bool tiled = false);
+// The plan and operands run the MFMA kernel, the one that reads column tiles.
+bool gemv_tiled_ok(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
+                   int64_t ldq, const void* scales, int group, int M, int N, int K);
 
 // W4A16 for kSkinnyMinM <= M <= kSkinnyMaxM (w4a16_skinny.hip): weights to registers, MFMA
 // per 16 activation rows, LDS reduction over the workgroup's waves, split-K partials.
@@ -66,7 +84,7 @@ size_t skinny_workspace_bytes(const SkinnyPlan& pl, int M, int N);
 int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
                   int64_t ldq, const void* scales, int group, OutEpi epi, void* c,
                   int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
-                  bool partials_only = false);
+                  bool partials_only = false, bool tiled = false);
 
 struct GemmCfg {
   int bm, bn, wm, wn;
@@ -103,7 +121,7 @@ bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ld
             int c_dtype, const void* c, int split);
 int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
                int group, OutEpi epi, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
-               int split, void* workspace, hipStream_t s, bool partials_only);
+               int split, void* workspace, hipStream_t s, bool partials_only, bool tiled = false);
 
 // 256 x 256 fp8 GEMM with a 4-stage DMA pipeline and transposing LDS reads for (K, N) B
 // (gemm_f8_v3.hip).

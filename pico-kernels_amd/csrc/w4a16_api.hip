@@ -94,20 +94,37 @@ size_t plan_ws(const W4Plan& pl, int M, int N) {
   return k > g ? k : g;
 }
 
+// The kernel the plan runs reads column-tile weights (the GEMV's MFMA form, the register-
+// dequant kernel, the packed-B GEMM) and its launch conditions hold, so no fallback to a
+// rows-only kernel can happen.
+bool plan_reads_tiles(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw,
+                      int64_t ldq, const void* scales, int group, const void* c, int c_dtype,
+                      int64_t ldc, int M, int N, int K) {
+  if (pl.kernel == kKernelGemv) return gemv_tiled_ok(pl.gemv, a, lda, qw, ldq, scales, group, M, N, K);
+  if (pl.kernel == kKernelSkinny) return skinny_fits(M, N, K, lda, ldq, group, scales != nullptr);
+  if (pl.kernel == kKernelGemmTr4)
+    return tr4_ok(M, N, K, group, scales != nullptr, lda, ldq, ldc, c_dtype, c, pl.tr4_split);
+  return false;
+}
+
 int plan_launch(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
                 const void* scales, int group, OutEpi epi, void* c, int c_dtype,
                 int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
-                bool partials_only) {
+                bool partials_only, bool tiled = false) {
   if (pl.kernel == kKernelGemv)
     return gemv_launch(pl.gemv, a, lda, qw, ldq, scales, group, epi, c, c_dtype, ldc,
-                       M, N, K, workspace, s, partials_only);
+                       M, N, K, workspace, s, partials_only, tiled);
   if (pl.kernel == kKernelSkinny && skinny_fits(M, N, K, lda, ldq, group, scales != nullptr))
     return skinny_launch(pl.skinny, a, lda, qw, ldq, scales, group, epi, c, c_dtype,
-                         ldc, M, N, K, workspace, s, partials_only);
+                         ldc, M, N, K, workspace, s, partials_only, tiled);
   if (pl.kernel == kKernelGemmTr4 &&
       tr4_ok(M, N, K, group, scales != nullptr, lda, ldq, ldc, c_dtype, c, pl.tr4_split))
     return tr4_launch(a, lda, qw, ldq, scales, group, epi, c, c_dtype, ldc, M, N, K,
-                      pl.tr4_split, workspace, s, partials_only);
+                      pl.tr4_split, workspace, s, partials_only, tiled);
+  if (tiled) {
+    set_error("pk_w4a16_gemm_tiled: no kernel reads column-tile weights for M=%d N=%d K=%d", M, N, K);
+    return PK_EUNSUPPORTED;
+  }
   return gemm_launch(pl.gemm, 1, a, lda, qw, ldq, scales, group, epi, c, c_dtype, ldc,
                      M, N, K, workspace, s, partials_only);
 }
@@ -163,7 +180,7 @@ namespace {
 int w4a16_gemm_ws(const char* name, const void* a, int64_t lda, const uint32_t* qweight,
                   int64_t ldq, const void* scales, int group_size, OutEpi epi, void* c,
                   int c_dtype, int64_t ldc, int M, int N, int K, int split_k, void* workspace,
-                  size_t workspace_bytes, void* stream) {
+                  size_t workspace_bytes, void* stream, bool tiled = false) {
   int rc = check_w4a16(a, lda, qweight, ldq, scales, group_size, c, c_dtype, ldc, M, N, K,
                        split_k);
   if (rc != PK_OK) return rc;
@@ -175,13 +192,18 @@ int w4a16_gemm_ws(const char* name, const void* a, int64_t lda, const uint32_t* 
               "(group %d, multiple of 32 rows)", name, split_k, K, group);
     return PK_EINVAL;
   }
+  if (tiled && !plan_reads_tiles(pl, a, lda, qweight, ldq, scales, group, c, c_dtype, ldc, M, N, K)) {
+    set_error("%s: no kernel reads column-tile weights for M=%d N=%d K=%d split_k=%d (the plan "
+              "picked kernel %d, or its operands are misaligned)", name, M, N, K, split_k, pl.kernel);
+    return PK_EUNSUPPORTED;
+  }
   const size_t need = plan_ws(pl, M, N);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_error("%s: workspace of %zu bytes needed (got %zu)", name, need, workspace_bytes);
     return PK_EWORKSPACE;
   }
   return plan_launch(pl, a, lda, qweight, ldq, scales, group, epi, c, c_dtype, ldc, M, N, K,
-                     workspace, (hipStream_t)stream, false);
+                     workspace, (hipStream_t)stream, false, tiled);
 }
 }  // namespace
 
@@ -192,6 +214,25 @@ extern "C" int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight
   return w4a16_gemm_ws("pk_w4a16_gemm", a, lda, qweight, ldq, scales, group_size,
                        OutEpi(tensor_scale), c, c_dtype, ldc, M, N, K, split_k, workspace,
                        workspace_bytes, stream);
+}
+
+extern "C" int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* qtiled,
+                                   const void* scales, int group_size, float tensor_scale,
+                                   const void* bias, int bias_dtype, void* c, int c_dtype,
+                                   int64_t ldc, int M, int N, int K, int split_k,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  PK_REQUIRE(N % 256 == 0 && K % 256 == 0,
+             "pk_w4a16_gemm_tiled: column tiles need N %% 256 == 0 and K %% 256 == 0 (N=%d K=%d)",
+             N, K);
+  PK_REQUIRE(scales == nullptr || group_size % 64 == 0,
+             "pk_w4a16_gemm_tiled: group_size=%d must be a multiple of 64", group_size);
+  PK_REQUIRE(qtiled != nullptr && aligned16(qtiled), "pk_w4a16_gemm_tiled: weights must be 16-byte aligned");
+  PK_REQUIRE(bias == nullptr || bias_dtype == PK_F32 || bias_dtype == PK_F16 ||
+                 bias_dtype == PK_BF16,
+             "pk_w4a16_gemm_tiled: bias dtype %d", bias_dtype);
+  return w4a16_gemm_ws("pk_w4a16_gemm_tiled", a, lda, qtiled, N / 8, scales, group_size,
+                       OutEpi(tensor_scale, bias, bias_dtype), c, c_dtype, ldc, M, N, K,
+                       split_k, workspace, workspace_bytes, stream, true);
 }
 
 extern "C" int pk_w4a16_gemm_bias(const void* a, int64_t lda, const uint32_t* qweight,

@@ -53,6 +53,7 @@ struct GemvParams {
   float* partials;  // (split, M, N) fp32 when split > 1; (split, M, npad) in the L2 handoff
   unsigned* counters;  // L2 handoff: arrival counter of tile t at counters[32 t]
   int tiles, npad;     // column tiles; tiles * 256
+  QLayout ql;          // where the weight words live (the MFMA kernel; rows for the VALU one)
 };
 
 __device__ __forceinline__ pk_half2 as_half2(uint32_t v) { return __builtin_bit_cast(pk_half2, v); }
@@ -303,15 +304,14 @@ void w4a16_gemv_mfma_kernel(GemvParams p) {
 
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.qw, (uint32_t)((int64_t)p.K * p.ldq * 4));
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda * 2));
-  const int ldq4 = (int)p.ldq * 4;
-  const int q_voff = rl * 8 * ldq4 + word0 * 4;
+  const int q_voff = rl * 8 * p.ql.row_bytes + (word0 >> 5) * p.ql.tile_bytes + (word0 & 31) * 4;
   pk_u4v xq[RB], w[RB][8];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     xq[rb] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(xrow * p.lda + rl * 8) * 2, (kb + 64 * rb) * 2, 0);
 #pragma unroll
     for (int r = 0; r < 8; ++r)
-      w[rb][r] = __builtin_amdgcn_raw_buffer_load_b128(rq, q_voff, (kb + 64 * rb + r) * ldq4, kPkLoadStream);
+      w[rb][r] = __builtin_amdgcn_raw_buffer_load_b128(rq, q_voff, (kb + 64 * rb + r) * p.ql.row_bytes, kPkLoadStream);
   }
 
   const pk_f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -568,10 +568,16 @@ static bool gemv_mfma_ready(const GemvPlan& pl, const void* a, int64_t lda, cons
          (int64_t)K * ldq * 4 < (1ll << 31) && (int64_t)M * lda * 2 < (1ll << 31);
 }
 
+bool gemv_tiled_ok(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
+                   int64_t ldq, const void* scales, int group, int M, int N, int K) {
+  return N % kGemvTileCols == 0 && ldq == N / 8 &&
+         gemv_mfma_ready(pl, a, lda, qw, ldq, scales, group, M, N, K);
+}
+
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
                 int64_t ldq, const void* scales, int group, OutEpi epi, void* c,
                 int c_dtype, int64_t ldc, int M, int N, int K, void* workspace,
-                hipStream_t s, bool partials_only) {
+                hipStream_t s, bool partials_only, bool tiled) {
   GemvParams p;
   p.a = reinterpret_cast<const pk_half*>(a);
   p.lda = lda;
@@ -594,8 +600,13 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
   p.counters = nullptr;
   p.tiles = pl.tiles;
   p.npad = pl.tiles * kGemvTileCols;
+  p.ql = qlayout(tiled, ldq, K);
   const int rb = pl.mfma;
   const bool mfma = gemv_mfma_ready(pl, a, lda, qw, ldq, scales, group, M, N, K);
+  if (tiled && !(mfma && N % kGemvTileCols == 0)) {
+    set_error("w4a16 gemv: column-tile weights need the MFMA kernel (N %% 256 == 0, K %% 256 == 0)");
+    return PK_EUNSUPPORTED;
+  }
   if (mfma) {
     // Slices hand off through L2 unless the caller wants the partials themselves.
     const bool l2split = pl.split > 1 && !partials_only && pl.tiles <= kWsMaxTiles &&

@@ -68,6 +68,7 @@ struct SkinnyParams {
   float* partials;  // (split, M, N) fp32 when split > 1; (split, M, npad) in the L2 handoff
   unsigned* counters;  // arrival counters of the L2 handoff, one 128-byte line per (tile, part)
   int npad;            // tiles * tile columns
+  QLayout ql;          // where the weight words live
 };
 
 template <int MB, int WPL>
@@ -118,8 +119,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
   const __amdgpu_buffer_rsrc_t rs =
       make_rsrc(HAS_GS ? (const void*)p.scales : (const void*)p.qw,
                 HAS_GS ? (uint32_t)((int64_t)(p.K / p.group) * p.N * 2) : 0u);
-  const int ldq4 = (int)p.ldq * 4;
-  const int q_voff = 8 * g * ldq4 + word0 * 4;
+  // a lane's words lie in one 256-column tile (word0 % 32 + WPL <= 32)
+  const int ldq4 = p.ql.row_bytes;
+  const int q_voff = 8 * g * ldq4 + (word0 >> 5) * p.ql.tile_bytes + (word0 & 31) * 4;
   int a_voff[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
@@ -509,7 +511,11 @@ size_t skinny_workspace_bytes(const SkinnyPlan& pl, int M, int N) {
 int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
                   int64_t ldq, const void* scales, int group, OutEpi epi, void* c,
                   int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
-                  bool partials_only) {
+                  bool partials_only, bool tiled) {
+  if (tiled && N % 256) {
+    set_error("w4a16 skinny: column-tile weights need N %% 256 == 0");
+    return PK_EUNSUPPORTED;
+  }
   SkinnyParams p;
   p.a = reinterpret_cast<const pk_half*>(a);
   p.lda = lda;
@@ -531,6 +537,7 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
   p.partials = pl.split > 1 ? split_partials(workspace, partials_only) : nullptr;
   p.counters = ws_counters(workspace);
   p.npad = pl.tiles * 16 * pl.cpl;
+  p.ql = qlayout(tiled, ldq, K);
   const bool l2 = !partials_only && skinny_l2(pl);
   if (scales) launch_skinny_cfg<true>(pl, p, l2, s);
   else launch_skinny_cfg<false>(pl, p, l2, s);

@@ -66,6 +66,7 @@ struct Tr4Params {
   int tiles_m, tiles_n;
   int kt_slice;     // k-tiles per split-K slice (all of K when unsplit)
   int64_t c_slice;  // elements between the slices' outputs (fp32 partial planes)
+  QLayout ql;       // where the weight words live
 };
 
 // global -> LDS DMA, 16 or 4 bytes per lane (lane L writes lds + 16 L / lds + 4 L)
@@ -144,9 +145,9 @@ void w4a16_tr4_kernel(Tr4Params p) {
 #pragma unroll
   for (int i = 0; i < B_DMA; ++i) {
     const int r = 8 * (2 * wave + i) + (lane >> 3);
-    b_off[i] = (int)((int64_t)r * p.ldb * 4) + n0 / 2 + tr4_bslot(r, lane & 7) * 16;
+    b_off[i] = r * p.ql.row_bytes + tn * p.ql.tile_bytes + tr4_bslot(r, lane & 7) * 16;
   }
-  const int ldb4 = (int)p.ldb * 4;
+  const int ldb4 = p.ql.row_bytes;
   // Scales: a 4-byte DMA per wave brings 128 column scales (lane L: columns 2 L, 2 L + 1) of
   // one k half's row; waves 0-3 fill both rows, waves 4-7 write the same bytes again, so every
   // wave issues the same loads.
@@ -454,7 +455,7 @@ bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ld
 // tensor scale (partials_only: the planes alone, at `workspace` itself).
 int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
                int group, OutEpi epi, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
-               int split, void* workspace, hipStream_t s, bool partials_only) {
+               int split, void* workspace, hipStream_t s, bool partials_only, bool tiled) {
   Tr4Params p;
   p.a = reinterpret_cast<const pk_half*>(a);
   p.lda = lda;
@@ -468,6 +469,7 @@ int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const voi
   p.tiles_m = (int)cdiv(M, 128);
   p.tiles_n = N / 256;
   p.kt_slice = K / 128 / split;
+  p.ql = qlayout(tiled, ldb, K);
   float* const partials = split > 1 ? split_partials(workspace, partials_only) : nullptr;
   if (split > 1) {
     p.epi = OutEpi(1.0f);

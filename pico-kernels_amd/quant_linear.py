@@ -27,6 +27,12 @@ file (no pickle) whose metadata records the format, its version and each layer's
 shape; ``load_quantized`` checks each tensor's shape and dtype before copying and raises
 ``ValueError`` on any mismatch.
 
+In memory, layers whose shape allows it (``in`` and ``out`` multiples of 256, groups of a
+multiple of 64 inputs or per-input scales: ``QuantLinear.tiled``) keep ``qweight`` in column
+tiles -- the words of each 256-output tile contiguous over all inputs (``_pk.tile_weights``) --
+which the kernels stream as whole DRAM pages (``pk_w4a16_gemm_tiled``). ``codes()`` /
+``set_codes()``, the state dict and the file format use ``pack_int4_n`` order either way.
+
 The output has the input's dtype (fp16, bf16 or fp32, as ``nn.Linear``); other inputs are
 computed in fp16. Weights need ``out % 8 == 0`` (whole int32 words) and ``in % 32 == 0``
 (the kernel's K), group layers ``in % group_size == 0``.
@@ -67,6 +73,8 @@ class QuantLinear(nn.Module):
             raise ValueError("in_features must be a multiple of group_size")
         self.in_features, self.out_features, self.scheme = in_features, out_features, scheme
         self.group_size = group_size if scheme == "group" else 0
+        # qweight in column tiles (see the module doc) where the shape allows
+        self.tiled = _pk.tiles_ok(in_features, out_features, self.group_size)
         self.register_buffer("qweight", torch.zeros(in_features, out_features // 8,
                                                     dtype=torch.int32, device=device))
         if scheme == "group":
@@ -112,7 +120,7 @@ class QuantLinear(nn.Module):
                 w.device)
         w_kn = w.to(_pk.gpu_device()).t().contiguous()  # (in, out): groups along the inputs
         qweight, scales = gemm_int4.quantize_int4_group(w_kn, group_size)
-        q.qweight.copy_(qweight)
+        q.set_codes(qweight)
         q.scales.copy_(scales)
         if linear.bias is not None:
             q.bias.copy_(linear.bias.detach().to(torch.float16))
@@ -143,19 +151,29 @@ class QuantLinear(nn.Module):
         s = torch.where(s > 0, s, torch.full_like(s, 1e-12 / qmax))
         layer = cls(in_f, out_f, bias is not None, 0, dev, scheme="per_input")
         codes = q.t().contiguous().to(torch.int8)       # (in, out)
-        layer.qweight.copy_(gemm_int4.pack_int4_n(codes).view(torch.int32))
+        layer.set_codes(gemm_int4.pack_int4_n(codes).view(torch.int32))
         layer.scales.copy_(s)
         layer._smax = float(s.max().item())
         if bias is not None:
             layer.bias.copy_(bias.to(torch.float16))
         return layer
 
+    # ---- codes ------------------------------------------------------------------------
+    def codes(self) -> torch.Tensor:
+        """The packed codes as ``(in, out/8)`` int32 words in ``pack_int4_n`` order."""
+        return _pk.untile_weights(self.qweight) if self.tiled else self.qweight
+
+    def set_codes(self, words: torch.Tensor) -> None:
+        """Store ``(in, out/8)`` int32 words given in ``pack_int4_n`` order."""
+        words = words.to(self.qweight.device)
+        self.qweight.copy_(_pk.tile_weights(words) if self.tiled else words)
+
     # ---- use ----------------------------------------------------------------------------
     def dequantized_weight(self) -> torch.Tensor:
         """``(out, in)`` fp32 ``q * scale`` (for inspection and tests)."""
         if self.scheme == "group":
-            return gemm_int4.dequantize_int4_group(self.qweight, self.scales, self.group_size).t()
-        q = gemm_int4.unpack_int4_n(self.qweight.contiguous().view(torch.uint8)).float()
+            return gemm_int4.dequantize_int4_group(self.codes(), self.scales, self.group_size).t()
+        q = gemm_int4.unpack_int4_n(self.codes().contiguous().view(torch.uint8)).float()
         return (q * self.scales.to(q.device)[:, None]).t()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -168,26 +186,36 @@ class QuantLinear(nn.Module):
             # x * s / max s in fp16 (the input cast in the same pass), then max s in the epilogue
             s = self.scales if self.scales.dtype == torch.float32 else self.scales.float()
             xp = _pk.w4a16_prep_activations(x2, s, 1.0 / self._smax)
-            y = _pk.w4a16_gemm(xp, self.qweight, None, 0, self._smax, out_dtype, bias=self.bias)
+            y = _pk.w4a16_gemm(xp, self.qweight, None, 0, self._smax, out_dtype, bias=self.bias,
+                               tiled=self.tiled)
         else:
             xp = x2 if x2.dtype == torch.float16 else _pk.w4a16_prep_activations(x2, None, 1.0)
             s = self.scales if self.scales.dtype == torch.float16 else self.scales.half()
             y = _pk.w4a16_gemm(xp, self.qweight, s, self.group_size, 1.0, out_dtype,
-                               bias=self.bias)
+                               bias=self.bias, tiled=self.tiled)
         return y.reshape(*lead, self.out_features)
 
     def _refresh(self) -> None:
         if self.scheme == "per_input":
             self._smax = float(self.scales.float().max().item())
 
-    def _load_from_state_dict(self, *args, **kwargs):
-        super()._load_from_state_dict(*args, **kwargs)
+    # the state dict holds the codes in pack_int4_n order, whatever the layout in memory
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        if self.tiled:
+            destination[prefix + "qweight"] = self.codes()
+
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
+        if self.tiled and prefix + "qweight" in state_dict:
+            self.qweight.copy_(_pk.tile_weights(self.qweight.clone()))
         self._refresh()
 
     def extra_repr(self) -> str:
         lay = f"group_size={self.group_size}" if self.scheme == "group" else "per-input scales"
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
-                f"bias={self.bias is not None}, {lay}, int4")
+                f"bias={self.bias is not None}, {lay}, int4"
+                + (", column tiles" if self.tiled else ""))
 
 
 def quantize_model_int4(model: nn.Module, group_size: int = 128, predicate=None,
@@ -231,7 +259,7 @@ def save_quantized(model: nn.Module, path: str) -> None:
     layers = _quant_layers(model)
     tensors, meta = {}, {}
     for name, q in layers.items():
-        tensors[f"{name}.qweight"] = q.qweight.detach().cpu().contiguous()
+        tensors[f"{name}.qweight"] = q.codes().detach().cpu().contiguous()
         tensors[f"{name}.scales"] = q.scales.detach().cpu().contiguous()
         if q.bias is not None:
             tensors[f"{name}.bias"] = q.bias.detach().cpu().contiguous()
@@ -287,7 +315,7 @@ def load_quantized(model: nn.Module, path: str) -> nn.Module:
             dev = cur.qweight.device if isinstance(cur, QuantLinear) else cur.weight.device
             q = QuantLinear(info["in_features"], info["out_features"], info["bias"],
                             info["group_size"] or 128, dev, scheme=info.get("scheme", "group"))
-            q.qweight.copy_(_read(f, f"{name}.qweight", q.qweight, path))
+            q.set_codes(_read(f, f"{name}.qweight", q.qweight, path))
             q.scales.copy_(_read(f, f"{name}.scales", q.scales, path))
             if info["bias"]:
                 q.bias.copy_(_read(f, f"{name}.bias", q.bias, path))

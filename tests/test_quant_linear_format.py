@@ -107,3 +107,38 @@ def test_shape_contract():
         ql.QuantLinear(100, 64, scheme="per_input")  # in_features not a multiple of 32
     with pytest.raises(ValueError):
         ql.QuantLinear(128, 64, scheme="per_row")
+
+
+def test_column_tiles_in_memory_pack_order_outside(tmp_path):
+    """Layers whose shape allows it keep qweight in column tiles (word j of input row k at
+    (j // 32) * 32 K + 32 k + j % 32); codes(), the state dict and the file hold pack_int4_n
+    order, and a round trip through either restores the same memory."""
+    import _pk
+
+    q = ql.QuantLinear(512, 768, True, 128)
+    assert q.tiled and not ql.QuantLinear(512, 776, True, 128).tiled
+    assert not ql.QuantLinear(512, 768, True, 32).tiled
+    assert ql.QuantLinear(512, 768, True, scheme="per_input").tiled
+    g = _gen(21)
+    words = torch.randint(-2**31, 2**31 - 1, (512, 96), generator=g, dtype=torch.int64).to(torch.int32)
+    q.set_codes(words)
+    flat = q.qweight.reshape(-1)
+    for k, j in ((0, 0), (5, 33), (511, 95), (100, 64), (257, 31)):
+        assert int(flat[(j // 32) * 32 * 512 + 32 * k + j % 32]) == int(words[k, j])
+    assert torch.equal(q.codes(), words)
+    assert torch.equal(_pk.untile_weights(_pk.tile_weights(words)), words)
+    sd = q.state_dict()
+    assert torch.equal(sd["qweight"], words)
+    q2 = ql.QuantLinear(512, 768, True, 128)
+    q2.load_state_dict(sd)
+    assert torch.equal(q2.qweight, q.qweight)
+    q.scales.copy_((torch.rand(q.scales.shape, generator=g) * 0.01).half())
+    path = str(tmp_path / "t.safetensors")
+    ql.save_quantized(nn.Sequential(q), path)
+    from safetensors import safe_open
+    with safe_open(path, framework="pt") as f:
+        assert torch.equal(f.get_tensor("0.qweight"), words)
+    dst = nn.Sequential(nn.Linear(512, 768))
+    ql.load_quantized(dst, path)
+    assert dst[0].tiled and torch.equal(dst[0].qweight, q.qweight)
+    assert torch.equal(dst[0].scales, q.scales)
