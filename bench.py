@@ -3,7 +3,10 @@
 
 Headline workload: W4A16 decode GEMV, M=1, K=4096, N=11008, int4 group
 128 with fp16 scales, fp16 activations N(0,1), weights N(0, 0.02), seeded CPU generator.
-A "step" is one ``w4a16_gemm`` call over one activation row. ``value`` is the whole-op HBM
+A "step" is one ``w4a16_gemm`` call over one activation row, on the weights in the layout
+``QuantLinear`` keeps in memory (``pk_w4a16_gemm_tiled``: the same codes in contiguous 16 KB
+blocks of 128 rows x 256 columns); the same call on ``pack_int4_n``'s row layout
+(``pk_w4a16_gemm``) is timed beside it. ``value`` is the whole-op HBM
 throughput (algorithmic bytes / step time), inputs resident in HBM. 40 distinct copies of the
 packed weights and scales (932 MB, more than twice the 256 MB Infinity Cache) are rotated:
 the W warm-up calls read copies 0..W-1, the timed graph starts at copy W and holds
@@ -138,6 +141,13 @@ def gemv_inputs(M: int, K: int, N: int, nrot: int, dev):
     return a, w, qws, scs
 
 
+def tiled_copies(qws: list) -> list:
+    """The weight copies in QuantLinear's in-memory layout (128 x 256 blocks)."""
+    import _pk
+
+    return [_pk.tile_weights(q) for q in qws]
+
+
 def unpack_codes(qw):
     """``(K, N//8)`` int32 words holding pack_int4_n bytes -> ``(K, N)`` int8 codes in [-8, 7],
     with plain torch ops (the reference's unpack, tests/test_gemm_int4.py:36-41)."""
@@ -215,12 +225,17 @@ def bench_gemv(args, dev) -> dict:
 
     M, K, N = 1, 4096, 11008
     a, w, qws, scs = gemv_inputs(M, K, N, N_ROTATE, dev)
+    qts = tiled_copies(qws)
     ag = a.to(dev)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     nbytes = w4a16_bytes(M, K, N)
     kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
 
-    def step(i):
+    def step(i):  # QuantLinear's layout: blocks
+        _pk.w4a16_gemm(ag, qts[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
+                       split_k=0, out=out, tiled=True)
+
+    def step_rows(i):  # pack_int4_n's row layout
         _pk.w4a16_gemm(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
                        split_k=0, out=out)
 
@@ -228,9 +243,19 @@ def bench_gemv(args, dev) -> dict:
         step(0)
         return out
 
+    def once_rows():
+        step_rows(0)
+        return out
+
     check = check_w4a16(once, ag, qws[0], scs[0])
+    y_tiles = out.clone()
+    check_rows = check_w4a16(once_rows, ag, qws[0], scs[0])
+    check["bitwise_equal_to_row_layout"] = bool(torch.equal(y_tiles, out))
+    if not check["bitwise_equal_to_row_layout"]:
+        raise RuntimeError("W4A16 GEMV: block and row layouts disagree")
     timed = max(args.steps, 2 * N_ROTATE)
     ms = GraphTimer(step, timed, args.warmup).run(reps=3)
+    ms_rows = GraphTimer(step_rows, timed, args.warmup).run(reps=3)
     launches = _pk.w4a16_launches(M, N, K, 128, 0)
 
     # The dominant kernel's average launch: back-to-back launches in one graph, HIP events
@@ -265,8 +290,9 @@ def bench_gemv(args, dev) -> dict:
         sweep[str(s)] = round(nbytes / (ms_s * 1e-3) / 1e9, 1)
     return {
         "M": M, "K": K, "N": N, "split": split, "kernel_id": kid, "launches": launches,
-        "bytes": nbytes, "steps_timed": timed, "check": check,
-        "ms_per_step": ms, "ms_kernel": ms_kernel, "ms_kernel_events": ms_kernel_events,
+        "bytes": nbytes, "steps_timed": timed, "check": check, "check_rows": check_rows,
+        "ms_per_step": ms, "ms_rows": ms_rows, "ms_kernel": ms_kernel,
+        "ms_kernel_events": ms_kernel_events,
         "split_sweep_GBs": sweep, "host": host_overhead(step),
         "inputs": (ag, qws[0], scs[0]),
     }
@@ -285,19 +311,30 @@ def bench_prefill(dev, iters: int = 50, M: int = 2048) -> dict:
     a = torch.randn(M, K, generator=_gen(2)).half().to(dev)
     w = (torch.randn(K, N, generator=_gen(3)) * 0.02).half().to(dev)
     qw, sc = gemm_int4.quantize_int4_group(w, 128)
+    qt = _pk.tile_weights(qw)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
 
-    def once():
+    def once():  # QuantLinear's layout: blocks
+        _pk.w4a16_gemm(a, qt, sc, 128, 1.0, torch.float16, out=out, tiled=True)
+        return out
+
+    def once_rows():
         _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, out=out)
         return out
 
     check = check_w4a16(once, a, qw, sc)
+    y_tiles = out.clone()
+    check_w4a16(once_rows, a, qw, sc)
+    check["bitwise_equal_to_row_layout"] = bool(torch.equal(y_tiles, out))
     kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
     ms = GraphTimer(lambda i: once(), iters, 2).run(reps=5)
+    ms_rows = GraphTimer(lambda i: once_rows(), iters, 2).run(reps=5)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return {"workload": "w4a16_prefill_gemm" if M == 2048 else "w4a16_gemm_4096^3", "M": M, "K": K,
             "N": N, "ms": round(ms, 4), "kernel_id": kid, "split": split,
             "value": round(tflops, 1), "unit": "TFLOP/s", "dtype": "fp16 MFMA, fp32 acc",
+            "weights": "128x256 blocks (QuantLinear's layout, pk_w4a16_gemm_tiled)",
+            "row_layout_TFLOP/s": round(2.0 * M * N * K / (ms_rows * 1e-3) / 1e12, 1),
             "check": check,
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -373,12 +410,17 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
         del w
         nrot = max(2, min(N_ROTATE, (600 << 20) // (K * N // 2) + 1))
         qws = [qw] + [qw.clone() for _ in range(nrot - 1)]
+        qts = tiled_copies(qws)
         scs = [sc] + [sc.clone() for _ in range(nrot - 1)]
         for M in (1, 8, 32, 128):
             a = torch.randn(M, K, generator=_gen(7)).half().to(dev)
             out = torch.empty((M, N), dtype=torch.float16, device=dev)
 
-            def step(i):
+            def step(i):  # QuantLinear's layout: blocks
+                _pk.w4a16_gemm(a, qts[i % nrot], scs[i % nrot], 128, 1.0, torch.float16,
+                               out=out, tiled=True)
+
+            def step_rows(i):
                 _pk.w4a16_gemm(a, qws[i % nrot], scs[i % nrot], 128, 1.0, torch.float16,
                                out=out)
 
@@ -388,12 +430,14 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
 
             check = check_w4a16(once, a, qw, sc)
             ms = GraphTimer(step, max(iters, 2 * nrot), 2).run(reps=3)
+            ms_rows = GraphTimer(step_rows, max(iters, 2 * nrot), 2).run(reps=3)
             by = w4a16_bytes(M, K, N)
             flop = 2.0 * M * N * K
             t_hbm = by / (HBM_PEAK_GBS * 1e9)
             t_mfma = flop / (MFMA_F16_PEAK_TFLOPS * 1e12)
             kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
             rows.append({"layer": name, "M": M, "K": K, "N": N, "us": round(ms * 1e3, 2),
+                         "us_row_layout": round(ms_rows * 1e3, 2),
                          "GB/s": round(by / (ms * 1e-3) / 1e9, 1),
                          "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
                          "bound": "hbm" if t_hbm >= t_mfma else "mfma",
@@ -401,7 +445,7 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
                          "kernel_id": kid, "split": split,
                          "launches": _pk.w4a16_launches(M, N, K, 128, 0), "copies": nrot,
                          "rel_fro": check["rel_fro_vs_fp32_expr"]})
-        del qws, scs
+        del qws, qts, scs
     return rows
 
 
@@ -639,9 +683,9 @@ COPY_PROBE_BYTES = 256 << 20
 
 def traffic_probe(dev) -> int:
     """Short run for the rocprofv3 --pmc passes: 50 launches of the GEMV's dominant kernel
-    on rotating weights (the whole op when its slices add up in L2, else the slice kernel),
-    then 50 launches of the slices alone writing their partials (pk_w4a16_gemm_partials: the
-    same loads and partial stores, no handoff reads), then 10 device copies of
+    on rotating weights in blocks (the whole op when its slices add up in L2), then 50
+    launches of the slices alone writing their partials (pk_w4a16_gemm_partials on the row
+    layout: the same loads and partial stores, no handoff reads), then 10 device copies of
     COPY_PROBE_BYTES (the calibration kernel: it must read and write exactly that many
     bytes)."""
     import torch
@@ -650,13 +694,14 @@ def traffic_probe(dev) -> int:
 
     M, K, N = 1, 4096, 11008
     a, w, qws, scs = gemv_inputs(M, K, N, N_ROTATE, dev)
+    qts = tiled_copies(qws)
     ag = a.to(dev)
     kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
     if _pk.w4a16_launches(M, N, K, 128, 0) == 1:
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
-        for i in range(50):
-            _pk.w4a16_gemm(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
-                           out=out)
+        for i in range(50):  # the headline's call: blocks
+            _pk.w4a16_gemm(ag, qts[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
+                           out=out, tiled=True)
     parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
     for i in range(50):
         _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
@@ -878,13 +923,19 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int4 weights (group 128, fp16 scales) x fp16 activations, fp32 accumulate",
         "data": "synthetic: seeded CPU generator, A ~ N(0,1) fp16, W ~ N(0,0.02) int4-quantized "
-                f"(group 128); {N_ROTATE} copies of the packed weights and scales rotated "
+                "(group 128), the codes in QuantLinear's in-memory layout (128x256 blocks; the "
+                f"row layout of pack_int4_n: {g['bytes'] / (g['ms_rows'] * 1e-3) / 1e9:.1f} GB/s); "
+                f"{N_ROTATE} copies of the packed weights and scales rotated "
                 f"({N_ROTATE * g['bytes'] / 1e6:.0f} MB > 2x the 256 MB Infinity Cache): warm-up "
                 f"reads copies 0..{args.warmup - 1}, the timed graph {g['steps_timed']} calls "
                 f"from copy {max(args.warmup, 1) % N_ROTATE} on, best of 3 replays",
         "config": {"workload": "w4a16_decode_gemv", "M": g["M"], "K": g["K"], "N": g["N"],
                    "group_size": 128, "split_k": g["split"], "out_dtype": "fp16",
-                   "split_k_sweep_GBs": g["split_sweep_GBs"]},
+                   "weights": "128x256 blocks (QuantLinear's layout, pk_w4a16_gemm_tiled)",
+                   "row_layout_GBs": round(g["bytes"] / (g["ms_rows"] * 1e-3) / 1e9, 1),
+                   "split_k_sweep_GBs": g["split_sweep_GBs"],
+                   "split_k_sweep_weights": "row layout (pk_w4a16_gemm; splits 1, 2, 4 run the "
+                                            "VALU GEMV, which reads rows only)"},
         "steps_timed": g["steps_timed"],
         "check": g["check"],
         "host": g["host"],

@@ -157,19 +157,21 @@ int pk_w4a16_gemm_bias(const void* a, int64_t lda, const uint32_t* qweight, int6
                        int bias_dtype, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
                        int split_k, void* workspace, size_t workspace_bytes, void* stream);
 
-/* pk_w4a16_gemm_bias on weights stored in column tiles: the same codes as pk_w4a16_gemm's
- * (K, N/8) words, reordered so that the 32 words (256 columns) of each column tile are
- * contiguous over all K rows -- word j of row k at (j / 32) * 32 K + 32 k + j % 32, i.e.
- * torch's qweight.view(K, N/256, 32).permute(1, 0, 2). Each workgroup then streams whole
- * DRAM pages instead of one 128-byte line per 5.5 KB row (measured on MI355X: the M=1
- * 4096x11008 GEMV 4.5% faster, Llama-3-8B layers at M = 1..32 up to 12%). Same scales,
- * bias, output, split_k, plan, workspace (pk_w4a16_workspace_bytes) and bits as
- * pk_w4a16_gemm_bias with ldq = N/8. Requires N % 256 == 0, K % 256 == 0, group_size % 64 ==
- * 0 with scales, 16-byte aligned operands, and a plan on a kernel that reads column tiles
- * (M <= 4, the register-dequant kernel, or the packed-B GEMM; the automatic split always
- * is): otherwise PK_EUNSUPPORTED. Has no counterpart in the reference, whose int4 weights
- * exist only in pack_int4_n order (gemm_int4.py:65-72); it is the layout QuantLinear keeps
- * in memory (its file format stays pack_int4_n order). */
+/* pk_w4a16_gemm_bias on weights stored in blocks: the same codes as pk_w4a16_gemm's (K, N/8)
+ * words, reordered into blocks of 128 rows x 256 columns (16 KB, row-major inside), the
+ * blocks ordered by row block and then column tile -- word j of row k at
+ * ((k / 128) * (N / 256) + j / 32) * 4096 + (k % 128) * 32 + j % 32, i.e. torch's
+ * qweight.view(K/128, 128, N/256, 32).permute(0, 2, 1, 3). A workgroup then streams 16 KB
+ * runs instead of one 128-byte line per 5.5 KB row, while the column tiles that a GEMM works
+ * on at the same k stay adjacent (measured on MI355X: the M=1 4096x11008 GEMV 4% faster,
+ * Llama-3-8B layers at M = 1..32 up to 12%, the large GEMMs within 2%). Same scales, bias,
+ * output, split_k, plan, workspace (pk_w4a16_workspace_bytes) and bits as pk_w4a16_gemm_bias
+ * with ldq = N/8. Requires N % 256 == 0, K % 256 == 0, group_size % 64 == 0 with scales,
+ * 16-byte aligned operands, and a plan on a kernel that reads blocks (M <= 4, the
+ * register-dequant kernel, or the packed-B GEMM; the automatic split always is): otherwise
+ * PK_EUNSUPPORTED. Has no counterpart in the reference, whose int4 weights exist only in
+ * pack_int4_n order (gemm_int4.py:65-72); it is the layout QuantLinear keeps in memory (its
+ * file format stays pack_int4_n order). */
 int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* qtiled, const void* scales,
                         int group_size, float tensor_scale, const void* bias, int bias_dtype,
                         void* c, int c_dtype, int64_t ldc, int M, int N, int K, int split_k,

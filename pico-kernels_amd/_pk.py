@@ -298,25 +298,28 @@ _ws_bytes: dict[tuple[int, int, int, int, int], int] = {}
 
 
 def tiles_ok(K: int, N: int, group_size: int) -> bool:
-    """Shapes whose weights pk_w4a16_gemm_tiled reads in column tiles (group 0: per-tensor)."""
+    """Shapes whose weights pk_w4a16_gemm_tiled reads in blocks (group 0: per-tensor)."""
     return N % 256 == 0 and K % 256 == 0 and group_size % 64 == 0
 
 
 def tile_weights(qweight: torch.Tensor) -> torch.Tensor:
-    """(K, N/8) int32 words in pack_int4_n order -> the same codes in column tiles: the 32
-    words of each 256-column tile contiguous over all K rows (still shaped (K, N/8))."""
+    """(K, N/8) int32 words in pack_int4_n order -> the same codes in 128 x 256 blocks: each
+    block's 128 rows of 32 words contiguous (16 KB), the blocks ordered by row block and then
+    column tile (still shaped (K, N/8))."""
     K, W = qweight.shape
-    if W % 32:
-        raise ValueError(f"tile_weights: N = {8 * W} is not a multiple of 256")
-    return qweight.reshape(K, W // 32, 32).permute(1, 0, 2).contiguous().view(K, W)
+    if W % 32 or K % 128:
+        raise ValueError(f"tile_weights: K = {K} must be a multiple of 128 and N = {8 * W} of 256")
+    return (qweight.reshape(K // 128, 128, W // 32, 32).permute(0, 2, 1, 3).contiguous()
+            .view(K, W))
 
 
 def untile_weights(qtiled: torch.Tensor) -> torch.Tensor:
-    """Inverse of tile_weights: column tiles -> (K, N/8) words in pack_int4_n order."""
+    """Inverse of tile_weights: blocks -> (K, N/8) words in pack_int4_n order."""
     K, W = qtiled.shape
-    if W % 32:
-        raise ValueError(f"untile_weights: N = {8 * W} is not a multiple of 256")
-    return qtiled.contiguous().view(W // 32, K, 32).permute(1, 0, 2).contiguous().view(K, W)
+    if W % 32 or K % 128:
+        raise ValueError(f"untile_weights: K = {K} must be a multiple of 128 and N = {8 * W} of 256")
+    return (qtiled.contiguous().view(K // 128, W // 32, 128, 32).permute(0, 2, 1, 3)
+            .contiguous().view(K, W))
 
 
 def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | None,
@@ -325,7 +328,7 @@ def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | No
                bias: torch.Tensor | None = None, tiled: bool = False) -> torch.Tensor:
     """out = tensor_scale * (a @ dequant(qweight, scales)) (+ bias, N values of fp32 / fp16 /
     bf16 added in the kernels' epilogue: pk_w4a16_gemm_bias). ``tiled``: qweight holds the
-    codes in column tiles (tile_weights; pk_w4a16_gemm_tiled)."""
+    codes in 128 x 256 blocks (tile_weights; pk_w4a16_gemm_tiled)."""
     M, K = a.shape
     N = qweight.shape[1] * 8
     if bias is not None and (bias.numel() != N or bias.dtype not in _TORCH_TO_PK
@@ -354,7 +357,7 @@ def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | No
     ws = workspace(dev, nbytes, stream) if nbytes else None
     if tiled:
         if not qweight.is_contiguous():
-            raise ValueError("w4a16_gemm: column-tile weights must be contiguous")
+            raise ValueError("w4a16_gemm: block-layout weights must be contiguous")
         rc = L.pk_w4a16_gemm_tiled(
             a.data_ptr(), a.stride(0), qweight.data_ptr(),
             None if scales is None else scales.data_ptr(), g, float(tensor_scale),

@@ -21,17 +21,26 @@ inline float* split_partials(void* ws, bool partials_only) {
   return partials_only ? reinterpret_cast<float*>(ws) : ws_partials(ws);
 }
 // Where the packed int4 weight words live. Rows (gemm_int4.pack_int4_n's layout viewed as a
-// (K, ldq) int32 array): word w of row k at k * ldq + w. Column tiles (pk_w4a16_gemm_tiled):
-// the 32 words (256 columns) of tile t = w / 32 are contiguous over all K rows, word w of row
-// k at (w / 32) * 32 K + 32 k + w % 32. A kernel reads a 16-byte chunk (four words of one
-// tile) at byte (w / 32) * tile_bytes + k * row_bytes + (w % 32) * 4, which is k * ldq * 4 +
-// w * 4 for rows.
+// (K, ldq) int32 array): word w of row k at k * ldq + w. Blocks (pk_w4a16_gemm_tiled): 128 rows
+// x 256 columns (32 words) per 16 KB block, row-major inside, the blocks ordered by row block
+// and then column tile -- word w of row k at ((k / 128) * T + w / 32) * 4096 + (k % 128) * 32 +
+// w % 32, T = N / 256. A kernel reads a 16-byte chunk (four words of one column tile) at byte
+//   (w / 32) * tile_bytes + (k / 128) * kblock_bytes + (k % 128) * row_bytes + (w % 32) * 4,
+// which is k * ldq * 4 + w * 4 for rows. Every kernel's rows per address base stay inside one
+// aligned 128-row block (the GEMV's 64-row wave groups, the register-dequant kernel's 32-row
+// k-steps, the packed-B GEMM's 128-row k-tiles).
 struct QLayout {
-  int row_bytes;   // between consecutive rows of one tile: ldq * 4, or 128
-  int tile_bytes;  // between consecutive 256-column tiles: 128, or K * 128
+  int row_bytes;     // between consecutive rows inside a block: ldq * 4, or 128
+  int tile_bytes;    // between consecutive 256-column tiles: 128, or 16 KB
+  int kblock_bytes;  // between consecutive 128-row blocks: 128 * ldq * 4, or T * 16 KB
 };
-inline QLayout qlayout(bool tiled, int64_t ldq, int K) {
-  return tiled ? QLayout{128, K * 128} : QLayout{(int)(ldq * 4), 128};
+inline QLayout qlayout(bool tiled, int64_t ldq, int N) {
+  return tiled ? QLayout{128, 16384, (N / 256) * 16384}
+               : QLayout{(int)(ldq * 4), 128, (int)(128 * ldq * 4)};
+}
+// Byte offset of row k's words within its column tile.
+__host__ __device__ __forceinline__ int qrow_off(const QLayout& q, int k) {
+  return (k >> 7) * q.kblock_bytes + (k & 127) * q.row_bytes;
 }
 
 // Host: split-K slices may hand off through one XCD's L2 on the current device (its XCC count
@@ -55,12 +64,12 @@ bool gemv_plan(int M, int N, int K, int group, bool has_gs, int split_req, GemvP
 size_t gemv_workspace_bytes(const GemvPlan& pl, int M, int N);
 // Launches the GEMV; with split > 1 the slices' partials go to `workspace` and, unless
 // partials_only, the ordered reduction into C follows.
-// `tiled`: the weights are in column tiles (QLayout; the MFMA kernel only, see gemv_tiled_ok).
+// `tiled`: the weights are in blocks (QLayout; the MFMA kernel only, see gemv_tiled_ok).
 int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw, int64_t ldq,
                 const void* scales, int group, OutEpi epi, void* c, int c_dtype,
                 int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                 bool partials_only = false, bool tiled = false);
-// The plan and operands run the MFMA kernel, the one that reads column tiles.
+// The plan and operands run the MFMA kernel, the one that reads blocks.
 bool gemv_tiled_ok(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
                    int64_t ldq, const void* scales, int group, int M, int N, int K);
 

@@ -94,7 +94,7 @@ size_t plan_ws(const W4Plan& pl, int M, int N) {
   return k > g ? k : g;
 }
 
-// The kernel the plan runs reads column-tile weights (the GEMV's MFMA form, the register-
+// The kernel the plan runs reads block-layout weights (the GEMV's MFMA form, the register-
 // dequant kernel, the packed-B GEMM) and its launch conditions hold, so no fallback to a
 // rows-only kernel can happen.
 bool plan_reads_tiles(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw,
@@ -122,7 +122,7 @@ int plan_launch(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw
     return tr4_launch(a, lda, qw, ldq, scales, group, epi, c, c_dtype, ldc, M, N, K,
                       pl.tr4_split, workspace, s, partials_only, tiled);
   if (tiled) {
-    set_error("pk_w4a16_gemm_tiled: no kernel reads column-tile weights for M=%d N=%d K=%d", M, N, K);
+    set_error("pk_w4a16_gemm_tiled: no kernel reads block-layout weights for M=%d N=%d K=%d", M, N, K);
     return PK_EUNSUPPORTED;
   }
   return gemm_launch(pl.gemm, 1, a, lda, qw, ldq, scales, group, epi, c, c_dtype, ldc,
@@ -193,7 +193,7 @@ int w4a16_gemm_ws(const char* name, const void* a, int64_t lda, const uint32_t* 
     return PK_EINVAL;
   }
   if (tiled && !plan_reads_tiles(pl, a, lda, qweight, ldq, scales, group, c, c_dtype, ldc, M, N, K)) {
-    set_error("%s: no kernel reads column-tile weights for M=%d N=%d K=%d split_k=%d (the plan "
+    set_error("%s: no kernel reads block-layout weights for M=%d N=%d K=%d split_k=%d (the plan "
               "picked kernel %d, or its operands are misaligned)", name, M, N, K, split_k, pl.kernel);
     return PK_EUNSUPPORTED;
   }
@@ -222,7 +222,7 @@ extern "C" int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* q
                                    int64_t ldc, int M, int N, int K, int split_k,
                                    void* workspace, size_t workspace_bytes, void* stream) {
   PK_REQUIRE(N % 256 == 0 && K % 256 == 0,
-             "pk_w4a16_gemm_tiled: column tiles need N %% 256 == 0 and K %% 256 == 0 (N=%d K=%d)",
+             "pk_w4a16_gemm_tiled: blocks need N %% 256 == 0 and K %% 256 == 0 (N=%d K=%d)",
              N, K);
   PK_REQUIRE(scales == nullptr || group_size % 64 == 0,
              "pk_w4a16_gemm_tiled: group_size=%d must be a multiple of 64", group_size);

@@ -311,7 +311,7 @@ void w4a16_gemv_mfma_kernel(GemvParams p) {
     xq[rb] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(xrow * p.lda + rl * 8) * 2, (kb + 64 * rb) * 2, 0);
 #pragma unroll
     for (int r = 0; r < 8; ++r)
-      w[rb][r] = __builtin_amdgcn_raw_buffer_load_b128(rq, q_voff, (kb + 64 * rb + r) * p.ql.row_bytes, kPkLoadStream);
+      w[rb][r] = __builtin_amdgcn_raw_buffer_load_b128(rq, q_voff, qrow_off(p.ql, kb + 64 * rb + r), kPkLoadStream);
   }
 
   const pk_f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -600,11 +600,11 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
   p.counters = nullptr;
   p.tiles = pl.tiles;
   p.npad = pl.tiles * kGemvTileCols;
-  p.ql = qlayout(tiled, ldq, K);
+  p.ql = qlayout(tiled, ldq, N);
   const int rb = pl.mfma;
   const bool mfma = gemv_mfma_ready(pl, a, lda, qw, ldq, scales, group, M, N, K);
   if (tiled && !(mfma && N % kGemvTileCols == 0)) {
-    set_error("w4a16 gemv: column-tile weights need the MFMA kernel (N %% 256 == 0, K %% 256 == 0)");
+    set_error("w4a16 gemv: block-layout weights need the MFMA kernel (N %% 256 == 0, K %% 256 == 0)");
     return PK_EUNSUPPORTED;
   }
   if (mfma) {

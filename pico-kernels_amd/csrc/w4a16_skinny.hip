@@ -120,8 +120,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
       make_rsrc(HAS_GS ? (const void*)p.scales : (const void*)p.qw,
                 HAS_GS ? (uint32_t)((int64_t)(p.K / p.group) * p.N * 2) : 0u);
   // a lane's words lie in one 256-column tile (word0 % 32 + WPL <= 32)
-  const int ldq4 = p.ql.row_bytes;
-  const int q_voff = 8 * g * ldq4 + (word0 >> 5) * p.ql.tile_bytes + (word0 & 31) * 4;
+  const int q_voff = 8 * g * p.ql.row_bytes + (word0 >> 5) * p.ql.tile_bytes + (word0 & 31) * 4;
   int a_voff[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
@@ -142,11 +141,11 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       if constexpr (WPL == 2) {
-        const pk_u2v v = __builtin_amdgcn_raw_buffer_load_b64(rq, q_voff, (k0 + d) * ldq4, 0);
+        const pk_u2v v = __builtin_amdgcn_raw_buffer_load_b64(rq, q_voff, qrow_off(p.ql, k0 + d), 0);
         b.w[d][0] = v[0];
         b.w[d][1] = v[1];
       } else {
-        b.w[d][0] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_voff, (k0 + d) * ldq4, 0);
+        b.w[d][0] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_voff, qrow_off(p.ql, k0 + d), 0);
       }
     }
 #pragma unroll
@@ -513,7 +512,7 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
                   int c_dtype, int64_t ldc, int M, int N, int K, void* workspace, hipStream_t s,
                   bool partials_only, bool tiled) {
   if (tiled && N % 256) {
-    set_error("w4a16 skinny: column-tile weights need N %% 256 == 0");
+    set_error("w4a16 skinny: block-layout weights need N %% 256 == 0");
     return PK_EUNSUPPORTED;
   }
   SkinnyParams p;
@@ -537,7 +536,7 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
   p.partials = pl.split > 1 ? split_partials(workspace, partials_only) : nullptr;
   p.counters = ws_counters(workspace);
   p.npad = pl.tiles * 16 * pl.cpl;
-  p.ql = qlayout(tiled, ldq, K);
+  p.ql = qlayout(tiled, ldq, N);
   const bool l2 = !partials_only && skinny_l2(pl);
   if (scales) launch_skinny_cfg<true>(pl, p, l2, s);
   else launch_skinny_cfg<false>(pl, p, l2, s);

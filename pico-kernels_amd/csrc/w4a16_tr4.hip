@@ -147,7 +147,6 @@ void w4a16_tr4_kernel(Tr4Params p) {
     const int r = 8 * (2 * wave + i) + (lane >> 3);
     b_off[i] = r * p.ql.row_bytes + tn * p.ql.tile_bytes + tr4_bslot(r, lane & 7) * 16;
   }
-  const int ldb4 = p.ql.row_bytes;
   // Scales: a 4-byte DMA per wave brings 128 column scales (lane L: columns 2 L, 2 L + 1) of
   // one k half's row; waves 0-3 fill both rows, waves 4-7 write the same bytes again, so every
   // wave issues the same loads.
@@ -160,7 +159,7 @@ void w4a16_tr4_kernel(Tr4Params p) {
 #pragma unroll
     for (int i = 0; i < A_DMA; ++i) tr4_dma16(ra, sA + (4 * wave + i) * 1024, a_off[i], k0 * 2);
 #pragma unroll
-    for (int i = 0; i < B_DMA; ++i) tr4_dma16(rb, sB + (2 * wave + i) * 1024, b_off[i], k0 * ldb4);
+    for (int i = 0; i < B_DMA; ++i) tr4_dma16(rb, sB + (2 * wave + i) * 1024, b_off[i], qrow_off(p.ql, k0));
     if constexpr (GS)
       tr4_dma4(rs, sS + 512 * s_half + 256 * s_part, s_off, ((k0 + 64 * s_half) / p.group) * p.N * 2);
   };
@@ -469,7 +468,7 @@ int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const voi
   p.tiles_m = (int)cdiv(M, 128);
   p.tiles_n = N / 256;
   p.kt_slice = K / 128 / split;
-  p.ql = qlayout(tiled, ldb, K);
+  p.ql = qlayout(tiled, ldb, N);
   float* const partials = split > 1 ? split_partials(workspace, partials_only) : nullptr;
   if (split > 1) {
     p.epi = OutEpi(1.0f);

@@ -28,10 +28,10 @@ shape; ``load_quantized`` checks each tensor's shape and dtype before copying an
 ``ValueError`` on any mismatch.
 
 In memory, layers whose shape allows it (``in`` and ``out`` multiples of 256, groups of a
-multiple of 64 inputs or per-input scales: ``QuantLinear.tiled``) keep ``qweight`` in column
-tiles -- the words of each 256-output tile contiguous over all inputs (``_pk.tile_weights``) --
-which the kernels stream as whole DRAM pages (``pk_w4a16_gemm_tiled``). ``codes()`` /
-``set_codes()``, the state dict and the file format use ``pack_int4_n`` order either way.
+multiple of 64 inputs or per-input scales: ``QuantLinear.tiled``) keep ``qweight`` in blocks
+of 128 inputs x 256 outputs, each 16 KB block contiguous (``_pk.tile_weights``), which the
+kernels stream in long runs (``pk_w4a16_gemm_tiled``). ``codes()`` / ``set_codes()``, the
+state dict and the file format use ``pack_int4_n`` order either way.
 
 The output has the input's dtype (fp16, bf16 or fp32, as ``nn.Linear``); other inputs are
 computed in fp16. Weights need ``out % 8 == 0`` (whole int32 words) and ``in % 32 == 0``
@@ -73,7 +73,7 @@ class QuantLinear(nn.Module):
             raise ValueError("in_features must be a multiple of group_size")
         self.in_features, self.out_features, self.scheme = in_features, out_features, scheme
         self.group_size = group_size if scheme == "group" else 0
-        # qweight in column tiles (see the module doc) where the shape allows
+        # qweight in 128 x 256 blocks (see the module doc) where the shape allows
         self.tiled = _pk.tiles_ok(in_features, out_features, self.group_size)
         self.register_buffer("qweight", torch.zeros(in_features, out_features // 8,
                                                     dtype=torch.int32, device=device))
@@ -215,7 +215,7 @@ class QuantLinear(nn.Module):
         lay = f"group_size={self.group_size}" if self.scheme == "group" else "per-input scales"
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"bias={self.bias is not None}, {lay}, int4"
-                + (", column tiles" if self.tiled else ""))
+                + (", 128x256 blocks" if self.tiled else ""))
 
 
 def quantize_model_int4(model: nn.Module, group_size: int = 128, predicate=None,

@@ -110,9 +110,10 @@ def test_shape_contract():
 
 
 def test_column_tiles_in_memory_pack_order_outside(tmp_path):
-    """Layers whose shape allows it keep qweight in column tiles (word j of input row k at
-    (j // 32) * 32 K + 32 k + j % 32); codes(), the state dict and the file hold pack_int4_n
-    order, and a round trip through either restores the same memory."""
+    """Layers whose shape allows it keep qweight in 128 x 256 blocks (word j of input row k at
+    ((k // 128) * T + j // 32) * 4096 + (k % 128) * 32 + j % 32, T = out / 256); codes(), the
+    state dict and the file hold pack_int4_n order, and a round trip through either restores
+    the same memory."""
     import _pk
 
     q = ql.QuantLinear(512, 768, True, 128)
@@ -123,8 +124,8 @@ def test_column_tiles_in_memory_pack_order_outside(tmp_path):
     words = torch.randint(-2**31, 2**31 - 1, (512, 96), generator=g, dtype=torch.int64).to(torch.int32)
     q.set_codes(words)
     flat = q.qweight.reshape(-1)
-    for k, j in ((0, 0), (5, 33), (511, 95), (100, 64), (257, 31)):
-        assert int(flat[(j // 32) * 32 * 512 + 32 * k + j % 32]) == int(words[k, j])
+    for k, j in ((0, 0), (5, 33), (511, 95), (100, 64), (257, 31), (128, 0), (127, 32)):
+        assert int(flat[((k // 128) * 3 + j // 32) * 4096 + (k % 128) * 32 + j % 32]) == int(words[k, j])
     assert torch.equal(q.codes(), words)
     assert torch.equal(_pk.untile_weights(_pk.tile_weights(words)), words)
     sd = q.state_dict()

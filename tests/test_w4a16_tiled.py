@@ -1,6 +1,7 @@
-"""W4A16 on weights in column tiles (pk_w4a16_gemm_tiled, the layout QuantLinear keeps in
-memory): the same codes as pack_int4_n's (K, N/8) words, the 32 words of each 256-column tile
-contiguous over all K rows. Through the C ABI, every kernel that reads the layout -- the GEMV
+"""W4A16 on weights in blocks (pk_w4a16_gemm_tiled, the layout QuantLinear keeps in memory):
+the same codes as pack_int4_n's (K, N/8) words in 16 KB blocks of 128 rows x 256 columns,
+ordered by row block and then column tile. Through the C ABI, every kernel that reads the
+layout -- the GEMV
 (M <= 4, 256- and 512-row slices), the register-dequant kernel (5 <= M <= 128) and the
 packed-B GEMM (M > 64, unsplit and split-K) -- must give bitwise the result of pk_w4a16_gemm
 on the rows layout (itself checked against the oracle), for group sizes 64 / 128 / 256, the
