@@ -32,7 +32,8 @@ metric also names, split-KV decode attention, GPTQ of one layer, the eager host 
 cores: dequantize, then matmul, each the median of 5 runs after a warm-up).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-sweep]
-       python bench.py --only {prefill,gemm4096,fp8,flash_decode,gptq,sweep}   (one line)
+       python bench.py --only {gemv,prefill,gemm4096,fp8,fp8_2048,flash_decode,gptq,sweep}
+       [--no-row-layout: time the W4A16 lines on the block layout only, for kernel traces]
 """
 
 from __future__ import annotations
@@ -52,6 +53,10 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2516.6  # dense fp16 (256 CU x 2.4 GHz x 4096 FLOP/clk)
 MFMA_F8_PEAK_TFLOPS = 5033.2   # dense fp8
 N_ROTATE = 40
+# Time the row layout (pack_int4_n order, pk_w4a16_gemm) beside QuantLinear's block layout;
+# --no-row-layout turns it off, so a kernel trace holds the block layout's launches alone
+# (both layouts run the same kernels).
+ROW_LAYOUT = True
 KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v3_f16_kernel", 3: "w4a16_skinny_kernel"}
 
 
@@ -255,7 +260,7 @@ def bench_gemv(args, dev) -> dict:
         raise RuntimeError("W4A16 GEMV: block and row layouts disagree")
     timed = max(args.steps, 2 * N_ROTATE)
     ms = GraphTimer(step, timed, args.warmup).run(reps=3)
-    ms_rows = GraphTimer(step_rows, timed, args.warmup).run(reps=3)
+    ms_rows = GraphTimer(step_rows, timed, args.warmup).run(reps=3) if ROW_LAYOUT else None
     launches = _pk.w4a16_launches(M, N, K, 128, 0)
 
     # The dominant kernel's average launch: back-to-back launches in one graph, HIP events
@@ -276,7 +281,7 @@ def bench_gemv(args, dev) -> dict:
         ms_kernel_events = per_launch_ms(step_partials, min(timed, 500))
 
     sweep = {}
-    for s in (1, 2, 4, 8, 16):
+    for s in ((1, 2, 4, 8, 16) if getattr(args, "split_sweep", True) else ()):
         def step_s(i, s=s):
             _pk.w4a16_gemm(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
                            split_k=s, out=out)
@@ -328,13 +333,13 @@ def bench_prefill(dev, iters: int = 50, M: int = 2048) -> dict:
     check["bitwise_equal_to_row_layout"] = bool(torch.equal(y_tiles, out))
     kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
     ms = GraphTimer(lambda i: once(), iters, 2).run(reps=5)
-    ms_rows = GraphTimer(lambda i: once_rows(), iters, 2).run(reps=5)
+    ms_rows = GraphTimer(lambda i: once_rows(), iters, 2).run(reps=5) if ROW_LAYOUT else None
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return {"workload": "w4a16_prefill_gemm" if M == 2048 else "w4a16_gemm_4096^3", "M": M, "K": K,
             "N": N, "ms": round(ms, 4), "kernel_id": kid, "split": split,
             "value": round(tflops, 1), "unit": "TFLOP/s", "dtype": "fp16 MFMA, fp32 acc",
             "weights": "128x256 blocks (QuantLinear's layout, pk_w4a16_gemm_tiled)",
-            "row_layout_TFLOP/s": round(2.0 * M * N * K / (ms_rows * 1e-3) / 1e12, 1),
+            "row_layout_TFLOP/s": round(2.0 * M * N * K / (ms_rows * 1e-3) / 1e12, 1) if ms_rows else None,
             "check": check,
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -430,14 +435,14 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
 
             check = check_w4a16(once, a, qw, sc)
             ms = GraphTimer(step, max(iters, 2 * nrot), 2).run(reps=3)
-            ms_rows = GraphTimer(step_rows, max(iters, 2 * nrot), 2).run(reps=3)
+            ms_rows = GraphTimer(step_rows, max(iters, 2 * nrot), 2).run(reps=3) if ROW_LAYOUT else None
             by = w4a16_bytes(M, K, N)
             flop = 2.0 * M * N * K
             t_hbm = by / (HBM_PEAK_GBS * 1e9)
             t_mfma = flop / (MFMA_F16_PEAK_TFLOPS * 1e12)
             kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
             rows.append({"layer": name, "M": M, "K": K, "N": N, "us": round(ms * 1e3, 2),
-                         "us_row_layout": round(ms_rows * 1e3, 2),
+                         "us_row_layout": round(ms_rows * 1e3, 2) if ms_rows else None,
                          "GB/s": round(by / (ms * 1e-3) / 1e9, 1),
                          "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
                          "bound": "hbm" if t_hbm >= t_mfma else "mfma",
@@ -855,8 +860,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true", help="skip the GEMM lines")
     ap.add_argument("--no-sweep", action="store_true", help="skip the Llama-3-8B layer sweep")
-    ap.add_argument("--only", choices=("prefill", "gemm4096", "fp8", "fp8_2048", "flash_decode",
-                                       "gptq", "sweep"),
+    ap.add_argument("--no-row-layout", action="store_true",
+                    help="time the W4A16 lines on QuantLinear's block layout only (for kernel traces)")
+    ap.add_argument("--only", choices=("gemv", "prefill", "gemm4096", "fp8", "fp8_2048",
+                                       "flash_decode", "gptq", "sweep"),
                     help="run one secondary workload alone and print its JSON (for profiling)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only run eager GEMM calls for rocprofv3 --pmc MFMA utilisation")
@@ -886,6 +893,8 @@ def main() -> int:
         return 1
     _pk.lib()
     dev = torch.device("cuda", 0)
+    global ROW_LAYOUT
+    ROW_LAYOUT = not args.no_row_layout
     if args.traffic_probe:
         return traffic_probe(dev)
     if args.mfma_probe:
@@ -898,6 +907,13 @@ def main() -> int:
         return 0
     if args.hbm_ceiling:
         print(json.dumps(hbm_ceiling(dev)), flush=True)
+        return 0
+    if args.only == "gemv":  # the headline call alone: its timing, no split sweep
+        args.split_sweep = False
+        g = bench_gemv(args, dev)
+        g.pop("inputs")
+        g["GB/s"] = round(g["bytes"] / (g["ms_per_step"] * 1e-3) / 1e9, 1)
+        print(json.dumps(g), flush=True)
         return 0
     if args.only:
         fn = {"prefill": bench_prefill, "gemm4096": lambda d: bench_prefill(d, M=4096),
@@ -923,8 +939,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int4 weights (group 128, fp16 scales) x fp16 activations, fp32 accumulate",
         "data": "synthetic: seeded CPU generator, A ~ N(0,1) fp16, W ~ N(0,0.02) int4-quantized "
-                "(group 128), the codes in QuantLinear's in-memory layout (128x256 blocks; the "
-                f"row layout of pack_int4_n: {g['bytes'] / (g['ms_rows'] * 1e-3) / 1e9:.1f} GB/s); "
+                "(group 128), the codes in QuantLinear's in-memory layout (128x256 blocks"
+                + (f"; the row layout of pack_int4_n: {g['bytes'] / (g['ms_rows'] * 1e-3) / 1e9:.1f} GB/s"
+                   if g["ms_rows"] else "") + "); "
                 f"{N_ROTATE} copies of the packed weights and scales rotated "
                 f"({N_ROTATE * g['bytes'] / 1e6:.0f} MB > 2x the 256 MB Infinity Cache): warm-up "
                 f"reads copies 0..{args.warmup - 1}, the timed graph {g['steps_timed']} calls "
@@ -932,7 +949,8 @@ def main() -> int:
         "config": {"workload": "w4a16_decode_gemv", "M": g["M"], "K": g["K"], "N": g["N"],
                    "group_size": 128, "split_k": g["split"], "out_dtype": "fp16",
                    "weights": "128x256 blocks (QuantLinear's layout, pk_w4a16_gemm_tiled)",
-                   "row_layout_GBs": round(g["bytes"] / (g["ms_rows"] * 1e-3) / 1e9, 1),
+                   "row_layout_GBs": (round(g["bytes"] / (g["ms_rows"] * 1e-3) / 1e9, 1)
+                                      if g["ms_rows"] else None),
                    "split_k_sweep_GBs": g["split_sweep_GBs"],
                    "split_k_sweep_weights": "row layout (pk_w4a16_gemm; splits 1, 2, 4 run the "
                                             "VALU GEMV, which reads rows only)"},
