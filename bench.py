@@ -13,9 +13,10 @@ the W warm-up calls read copies 0..W-1, the timed graph starts at copy W and hol
 max(K, 80) calls, so it reads every copy at least twice and never starts on a copy the
 warm-up has just read.
 
-Timing: W eager warm-up steps, then max(K, 80) steps captured in one HIP graph, replayed 3
-times between HIP events on the graph's stream (device synchronisation around each replay);
-the best replay gives ``ms_per_step``. On MI355X the GEMV's split-K slices add up in L2 inside
+Timing: W eager warm-up steps, then max(K, 80) steps captured in one HIP graph; untimed
+replays for 250 ms (the clocks settle under load), then 3 replays between HIP events on the
+graph's stream (device synchronisation around each replay); the best replay gives
+``ms_per_step``. Every timed line gets the same settling replays. On MI355X the GEMV's split-K slices add up in L2 inside
 the one kernel, so the op is the dominant kernel and the roofline fraction uses its time;
 where a second (reduce) launch is needed, the slice kernel is timed on its own through
 ``pk_w4a16_gemm_partials``.
@@ -57,6 +58,7 @@ N_ROTATE = 40
 # --no-row-layout turns it off, so a kernel trace holds the block layout's launches alone
 # (both layouts run the same kernels).
 ROW_LAYOUT = True
+WARM_MS = 250.0  # untimed graph replays before each timed measurement (GraphTimer.run)
 KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v3_f16_kernel", 3: "w4a16_skinny_kernel"}
 
 
@@ -95,12 +97,18 @@ class GraphTimer:
                 fn(start + i)
         torch.cuda.synchronize()
 
-    def run(self, reps: int = 1) -> float:
-        """Milliseconds per step (best of `reps` replays)."""
+    def run(self, reps: int = 1, warm_ms: float = WARM_MS) -> float:
+        """Milliseconds per step (best of `reps` replays), after untimed replays for at least
+        `warm_ms` of wall time: the GPU's clocks settle under load over a few hundred
+        milliseconds, and without this the first configuration timed reads ~3% slow."""
         import torch
 
         best = float("inf")
         with torch.cuda.stream(self.stream):
+            t_end = time.perf_counter() + warm_ms * 1e-3
+            while time.perf_counter() < t_end:
+                self.graph.replay()
+                torch.cuda.synchronize()
             for _ in range(reps):
                 e0 = torch.cuda.Event(enable_timing=True)
                 e1 = torch.cuda.Event(enable_timing=True)

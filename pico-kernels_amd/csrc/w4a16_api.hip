@@ -49,7 +49,8 @@ struct W4Plan {
   SkinnyPlan skinny;
 };
 
-bool make_plan(int M, int N, int K, int group_size, bool has_gs, int split_k, W4Plan* pl) {
+bool make_plan(int M, int N, int K, int group_size, bool has_gs, int split_k, W4Plan* pl,
+               bool tiled = false) {
   if (M <= 4 && gemv_plan(M, N, K, group_size, has_gs, split_k, &pl->gemv)) {
     pl->kernel = kKernelGemv;
     return true;
@@ -67,7 +68,7 @@ bool make_plan(int M, int N, int K, int group_size, bool has_gs, int split_k, W4
   }
   // The skinny kernel's split must also be one the GEMM accepts: the GEMM is its fallback
   // when a buffer exceeds 32-bit offsets, and the workspace size is the same (split*M*N*4).
-  if (skinny_plan(M, N, K, group_size, has_gs, split_k, &pl->skinny) &&
+  if (skinny_plan(M, N, K, group_size, has_gs, split_k, &pl->skinny, tiled) &&
       gemm_plan(M, N, K, group_size, has_gs, pl->skinny.split, &pl->gemm)) {
     pl->kernel = kKernelSkinny;
     return true;
@@ -172,8 +173,16 @@ extern "C" int pk_w4a16_launches(int M, int N, int K, int group_size, int split_
 extern "C" size_t pk_w4a16_workspace_bytes(int M, int N, int K, int group_size, int split_k) {
   W4Plan pl;
   const bool has_gs = group_size > 0;
-  if (!make_plan(M, N, K, has_gs ? group_size : K, has_gs, split_k, &pl)) return 0;
-  return plan_ws(pl, M, N);
+  const int group = has_gs ? group_size : K;
+  if (!make_plan(M, N, K, group, has_gs, split_k, &pl)) return 0;
+  size_t need = plan_ws(pl, M, N);
+  // enough for pk_w4a16_gemm_tiled's plan as well, where blocks are possible
+  W4Plan pt;
+  if (N % 256 == 0 && K % 256 == 0 && make_plan(M, N, K, group, has_gs, split_k, &pt, true)) {
+    const size_t t = plan_ws(pt, M, N);
+    if (t > need) need = t;
+  }
+  return need;
 }
 
 namespace {
@@ -187,7 +196,7 @@ int w4a16_gemm_ws(const char* name, const void* a, int64_t lda, const uint32_t* 
   const bool has_gs = scales != nullptr;
   const int group = has_gs ? group_size : K;
   W4Plan pl;
-  if (!make_plan(M, N, K, group, has_gs, split_k, &pl)) {
+  if (!make_plan(M, N, K, group, has_gs, split_k, &pl, tiled)) {
     set_error("%s: split_k=%d does not divide K=%d into slices of whole groups "
               "(group %d, multiple of 32 rows)", name, split_k, K, group);
     return PK_EINVAL;

@@ -424,7 +424,8 @@ bool skinny_layout_set(int cpl, int nw) {
   return true;
 }
 
-bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out) {
+bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, SkinnyPlan* out,
+                 bool tiled) {
   if (M < kSkinnyMinM || M > kSkinnyMaxM || N % 16 || K % 128) return false;
   // Above 64 rows every weight is read by two row parts; that beat the LDS-tiled GEMM only
   // on layers of at most 4096 x 4096 weights (measured at M = 96 and 128).
@@ -438,9 +439,12 @@ bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, Ski
     return skinny_plan_nw(M, N, K, group, has_gs, split_req, w, M > 32 ? 8 : c, out);
   }
   // 8 waves (half the slices for the same waves in flight); 4 where slices of 8 k-steps do
-  // not fit K, the group or the requested split.
-  return skinny_plan_nw(M, N, K, group, has_gs, split_req, 8, 0, out) ||
-         skinny_plan_nw(M, N, K, group, has_gs, split_req, 4, 0, out);
+  // not fit K, the group or the requested split. Block-layout weights with one 16-row block:
+  // 128-column tiles, whose two halves of each 256-byte block row go to two workgroups of one
+  // XCD (faster there on the larger layers; 256-column tiles on the row layout).
+  const int c = tiled && M <= 16 ? 8 : 0;
+  return skinny_plan_nw(M, N, K, group, has_gs, split_req, 8, c, out) ||
+         skinny_plan_nw(M, N, K, group, has_gs, split_req, 4, c, out);
 }
 
 // Buffer offsets are 32-bit: weights, scales and activations must each stay below 2 GiB.
