@@ -343,7 +343,9 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
           const pk_u4v val = *reinterpret_cast<const pk_u4v*>(sW + r * RB + ((ch ^ (r % NCH)) << 4));
           const int gm = m0 + wm0 + 32 * HF * h + r, gn = n0 + wn0 + ch * (16 / E);
           if (gm < p.M && gn < p.N)  // N % 16 == 0: a chunk is all in or all out
-            *PK_GLOBAL(pk_u4v, reinterpret_cast<char*>(p.c) + ((int64_t)gm * p.ldc + gn) * E) = val;
+            // non-temporal: written once, read by no later part of this kernel (measured on
+            // MI355X: 2048x4096x4096 2-4% faster, 4096^3 +0.5%)
+            __builtin_nontemporal_store(val, PK_GLOBAL(pk_u4v, reinterpret_cast<char*>(p.c) + ((int64_t)gm * p.ldc + gn) * E));
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next half is staged
       }
