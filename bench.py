@@ -803,6 +803,7 @@ def vendor_compare(dev) -> dict:
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
         w = (torch.randn(K, N, generator=_gen(6)) * 0.02).half().to(dev)
         qw, sc = gemm_int4.quantize_int4_group(w, 128)
+        qt = _pk.tile_weights(qw)
         a8, sa = gemm_fp8.quantize(a)
         b8, sb = gemm_fp8.quantize(b)
         b8t = b8.t().contiguous().t()
@@ -816,10 +817,12 @@ def vendor_compare(dev) -> dict:
                      "hipblaslt_f16_nn": tf(lambda i: torch.matmul(a, b, out=out)),
                      "hipblaslt_f16_nt": tf(lambda i: torch.matmul(a, bt.t(), out=out)),
                      "pk_w4a16_g128": tf(lambda i: _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, out=out)),
+                     "pk_w4a16_g128_blocks": tf(lambda i: _pk.w4a16_gemm(a, qt, sc, 128, 1.0, torch.float16,
+                                                                       out=out, tiled=True)),
                      "hipblaslt_fp8_scaled_mm": tf(lambda i: torch._scaled_mm(a8, b8t, one, one, out_dtype=torch.float16)),
                      "pk_fp8": tf(lambda i: _pk.fp8_gemm(a8, b8, 1.0, torch.float16, out=out)),
                      "unit": "TFLOP/s"})
-        del a, b, bt, out, w, qw, sc, a8, b8, b8t
+        del a, b, bt, out, w, qw, qt, sc, a8, b8, b8t
     return {"vendor_compare": rows}
 
 
