@@ -55,6 +55,16 @@ bool make_plan(int M, int N, int K, int group_size, bool has_gs, int split_k, W4
     pl->kernel = kKernelGemv;
     return true;
   }
+  // 65..128 rows of a layer of 1024^2 .. 4096^2 weights: two row parts of the register-dequant
+  // kernel where its automatic plan needs at most 8 slices (measured on MI355X at M = 72, 96
+  // and 128 against the packed-B GEMM: 4096 x 4096 18.8 -> 15.6 us at M = 128, the 1024..4096
+  // layers 5-21% faster; with 16 slices, K = 4096 x N = 1024, 21-27% slower).
+  if (M > 64 && split_k == 0 && (int64_t)K * N >= 1024ll * 1024 &&
+      skinny_plan(M, N, K, group_size, has_gs, 0, &pl->skinny, tiled) && pl->skinny.split <= 8 &&
+      gemm_plan(M, N, K, group_size, has_gs, pl->skinny.split, &pl->gemm)) {
+    pl->kernel = kKernelSkinny;
+    return true;
+  }
   // Above the skinny kernel's 64 rows: the packed-B GEMM where its shape rules hold, with the
   // GEMM that dequantises into LDS at the same split as its fallback (operands misaligned for
   // it, or beyond its 32-bit offsets), so the workspace covers both.

@@ -89,12 +89,17 @@ def test_w4a16_plans_by_row_count():
     # ineligible shapes (N % 16, K % 128) stay on the GEMM
     assert _pk.w4a16_plan(8, 520, 1024, 32, 0)[0] == C
     assert _pk.w4a16_plan(8, 512, 1056, 32, 0)[0] == C
-    # M > 64: the GEMM that keeps B packed in LDS where its shape rules hold (N % 256,
-    # K % 128, group % 64), 128 x 256 tiles with the most equal k-slices (at most 16) that keep
-    # tiles x slices <= 224, unsplit where the tiles alone reach that
+    # 65 <= M <= 128 on layers of 1024^2 .. 4096^2 weights: two row parts of the
+    # register-dequant kernel when its automatic plan needs at most 8 slices
     T = _pk.KERNEL_GEMM_TR4
-    assert _pk.w4a16_plan(128, 4096, 4096, 128, 0) == (T, 8)      # 16 tiles x 8
-    assert _pk.w4a16_plan(96, 4096, 4096, 128, 0) == (T, 8)
+    assert _pk.w4a16_plan(128, 4096, 4096, 128, 0) == (S, 4)      # 32 tiles x 2 parts x 4
+    assert _pk.w4a16_plan(96, 4096, 4096, 128, 0) == (S, 4)
+    assert _pk.w4a16_plan(72, 1024, 1024, 128, 0) == (S, 4)
+    assert _pk.w4a16_plan(128, 1024, 4096, 128, 0) == (T, 16)     # its plan would need 16
+    assert _pk.w4a16_plan(128, 768, 1024, 128, 0) == (T, 8)       # below 1024^2 weights
+    # otherwise above 64 rows: the GEMM that keeps B packed in LDS where its shape rules hold
+    # (N % 256, K % 128, group % 64), 128 x 256 tiles with the most equal k-slices (at most
+    # 16) that keep tiles x slices <= 224, unsplit where the tiles alone reach that
     assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (T, 8)      # 24 tiles x 8
     assert _pk.w4a16_plan(128, 14336, 4096, 128, 0) == (T, 4)     # 56 tiles x 4
     assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (T, 14)    # 16 tiles x 14 (112 k-tiles)

@@ -37,7 +37,7 @@ PATHS = [
     (8, 4096, 2048, 0, _pk.KERNEL_SKINNY),    # register-dequant, slices added in L2
     (32, 4096, 2048, 0, _pk.KERNEL_SKINNY),   # register-dequant + reduce launch
     (100, 2048, 1040, 0, _pk.KERNEL_SKINNY),  # two row parts
-    (128, 2048, 1024, 0, _pk.KERNEL_GEMM_TR4),  # packed-B split-K + reduce launch
+    (128, 1024, 768, 0, _pk.KERNEL_GEMM_TR4),  # packed-B split-K + reduce launch
     (256, 512, 512, 1, _pk.KERNEL_GEMM_TR4),  # packed-B unsplit (staged epilogue)
     (256, 1024, 1152, 0, _pk.KERNEL_GEMM),    # LDS-dequant large tiles, split-K
     (300, 512, 1160, 1, _pk.KERNEL_GEMM),     # LDS-dequant large tiles, unsplit, ragged
