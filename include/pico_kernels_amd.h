@@ -180,7 +180,9 @@ int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* qtiled, cons
 /* Which kernel pk_w4a16_gemm would run and its split factor (for reporting/benchmarks):
  * writes kernel id (1 = GEMV for M <= 4, 2 = LDS-tiled MFMA GEMM that dequantises B into LDS,
  * 3 = register-dequant MFMA kernel for 5 <= M <= 64, and M <= 128 on layers of at most
- * 4096 x 4096 weights the next kernel does not take, 4 = MFMA GEMM that keeps B packed in
+ * 4096 x 4096 weights: with an automatic split where the layer has at least 1024 x 1024
+ * weights and the kernel's plan needs at most 8 slices, else where the next kernel does not
+ * take the shape, 4 = MFMA GEMM that keeps B packed in
  * LDS, for M > 64 with N % 256 == 0, K % 128 == 0, group % 64 == 0 (split-K with a reduce
  * launch where its tiles leave CUs idle), assuming 16-byte aligned operands) and the
  * effective split. */
