@@ -82,6 +82,7 @@ struct SkinnyPlan {
   int cpl, nw;    // columns per lane (16 or 8), waves per workgroup (4 or 8)
   int row_parts;  // workgroups along M per (column tile, slice)
   int split, k_slice, tiles;
+  bool mg;        // a wave's rows span several 128-row groups (folded at each boundary)
 };
 // `tiled`: the plan for block-layout weights (QLayout): one 16-row block (M <= 16) takes
 // 128-column tiles there (measured on MI355X: down M=8 15.3 -> 13.7 us, gate_up 13.1 -> 12.7).

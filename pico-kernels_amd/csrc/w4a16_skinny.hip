@@ -79,8 +79,9 @@ struct SkStep {
 
 // MB: 16-row activation blocks per workgroup; CPL: columns per lane (16: 8-byte weight loads,
 // 256-column tiles; 8: 4-byte loads, 128-column tiles, half the accumulators per block);
-// NW: waves per workgroup, each taking 1/NW of the slice's rows.
-template <int MB, int CPL, int NW, bool HAS_GS, int PD, int OCC, bool L2>
+// NW: waves per workgroup, each taking 1/NW of the slice's rows. MG: the wave's rows span
+// several 128-row groups; its sums are scaled and added up at every group boundary.
+template <int MB, int CPL, int NW, bool HAS_GS, int PD, int OCC, bool L2, bool MG>
 __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams p) {
   constexpr int TC = 16 * CPL;  // tile columns
   constexpr int WPL = CPL / 8;  // words per lane and row
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
     a_voff[mb] = (int)(min(m0 + mb * 16 + j, p.M - 1) * p.lda + 8 * g) * 2;
-  // The wave's rows lie in group kb / group: its CPL column scales, requested first.
+  // The wave's (first) group kb / group: its CPL column scales, requested first.
   pk_u4v sraw[WPL];
 #pragma unroll
   for (int i = 0; i < WPL; ++i) sraw[i] = pk_u4v{0u, 0u, 0u, 0u};
@@ -194,27 +195,10 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
     }
   };
 
-  // ---- k-steps: a ring of PD buffers, each refilled PD steps ahead -----------------------
-  SkStep<MB, WPL> ring[PD];
-#pragma unroll
-  for (int i = 0; i < PD; ++i)
-    if (i < nsteps) load(ring[i], i);
-  for (int s0 = 0; s0 < nsteps; s0 += PD) {
-#pragma unroll
-    for (int i = 0; i < PD; ++i) {
-      const int s = s0 + i;
-      if (s < nsteps) {
-        compute(ring[i]);
-        if (s + PD < nsteps) load(ring[i], s + PD);
-      }
-    }
-  }
-  mfma_drain();
-
   // ---- per column: remove the +8 offset, apply 2^24 / 2^20 and the group scale ------------
   // acc[mb][c] holds rows m0 + mb*16 + 4g + r of the lane's column c.
   pk_f4 acc[MB][CPL];
-  {
+  auto fold = [&](bool first) {
     float sc[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -229,9 +213,63 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int by = 0; by < CPL / 2; ++by) {
-        acc[mb][2 * by] = (accL[mb][by] - off[mb]) * sc[2 * by];
-        acc[mb][2 * by + 1] = (accR[mb][by] - accL[mb][by] - off[mb] * 16.0f) * sc[2 * by + 1];
+        const pk_f4 lo = (accL[mb][by] - off[mb]) * sc[2 * by];
+        const pk_f4 hi = (accR[mb][by] - accL[mb][by] - off[mb] * 16.0f) * sc[2 * by + 1];
+        acc[mb][2 * by] = first ? lo : acc[mb][2 * by] + lo;
+        acc[mb][2 * by + 1] = first ? hi : acc[mb][2 * by + 1] + hi;
       }
+  };
+
+  // ---- k-steps: a ring of PD buffers, each refilled PD steps ahead -----------------------
+  SkStep<MB, WPL> ring[PD];
+#pragma unroll
+  for (int i = 0; i < PD; ++i)
+    if (i < nsteps) load(ring[i], i);
+  if constexpr (MG) {
+    // 128-row groups of 4 k-steps (the plan makes the wave's rows a whole number of them);
+    // at each boundary the group's sums are scaled into acc and the accumulators restart,
+    // while the ring's loads for the next group stay in flight.
+    static_assert(HAS_GS && PD <= 4 && 4 % PD == 0, "MG: whole groups of 4 k-steps");
+    const int groups = nsteps >> 2;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) acc[mb][c] = pk_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int gi = 0; gi < groups; ++gi) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int s = 4 * gi + i;
+        compute(ring[i % PD]);
+        if (s + PD < nsteps) load(ring[i % PD], s + PD);
+      }
+      mfma_drain();
+      fold(gi == 0);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        off[mb] = pk_f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int b = 0; b < CPL / 2; ++b) accL[mb][b] = accR[mb][b] = off[mb];
+      }
+      if (gi + 1 < groups) {
+        const int srow = (kb / p.group + gi + 1) * p.N * 2;
+#pragma unroll
+        for (int i = 0; i < WPL; ++i)
+          sraw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16 + 16 * i, srow, 0);
+      }
+    }
+  } else {
+    for (int s0 = 0; s0 < nsteps; s0 += PD) {
+#pragma unroll
+      for (int i = 0; i < PD; ++i) {
+        const int s = s0 + i;
+        if (s < nsteps) {
+          compute(ring[i]);
+          if (s + PD < nsteps) load(ring[i], s + PD);
+        }
+      }
+    }
+    mfma_drain();
+    fold(true);
   }
 
   // ---- add the waves' tiles in LDS: waves NB.. store, waves 0..NB-1 add their own, and the
@@ -372,23 +410,28 @@ constexpr int kSkWaveTarget = 1536;
 // The plan for nw waves per workgroup, cpl_fixed columns per lane (0: chosen here).
 static bool skinny_plan_nw(int M, int N, int K, int group, bool has_gs, int split_req, int nw,
                            int cpl_fixed, SkinnyPlan* out) {
-  // A wave takes k_slice / nw rows, a multiple of the 32-row k-step lying in one group.
-  auto ok = [&](int s) {
-    if (s < 1 || K % s || (K / s) % (nw * kSkStep)) return false;
-    const int rows_w = K / s / nw;
-    return !has_gs || group % rows_w == 0;
-  };
   // 16 columns per lane (256-column tiles) hold at most two 16-row blocks; 8 columns per lane
   // (128-column tiles) up to four, with two row parts above 64 rows.
   const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
   const int rp = (int)cdiv(M, mb * 16);
+  // A wave takes k_slice / nw rows, a multiple of the 32-row k-step lying in one group; with
+  // two 16-row blocks and 8 columns per lane (the registers for a second set of sums), also a
+  // whole number of 128-row groups, folded at each boundary -- half the slices of down and
+  // gate_up at M = 32 (measured on MI355X: 22.6 -> 18.5 and 19.3 -> 17.8 us with group-256
+  // weights, which take those slices without folds).
+  const bool mg_ok = has_gs && group == 128 && mb == 2;
+  auto ok = [&](int s, int cpl) {
+    if (s < 1 || K % s || (K / s) % (nw * kSkStep)) return false;
+    const int rows_w = K / s / nw;
+    return !has_gs || group % rows_w == 0 || (mg_ok && cpl == 8 && rows_w % group == 0);
+  };
   auto waves = [&](int cpl, int s) {
     return (int64_t)cdiv(N, 16 * cpl) * rp * s * nw;
   };
   auto pick = [&](int cpl) {  // fewest slices reaching the wave target, else the most
     int last = 0;
     for (int s = 1; s <= K / (nw * kSkStep); ++s)
-      if (ok(s)) {
+      if (ok(s, cpl)) {
         last = s;
         if (waves(cpl, s) >= kSkWaveTarget) return s;
       }
@@ -396,27 +439,30 @@ static bool skinny_plan_nw(int M, int N, int K, int group, bool has_gs, int spli
   };
   int cpl = 8, split = 0;
   if (split_req > 0) {
-    if (!ok(split_req)) return false;
-    split = split_req;
     if (cpl_fixed) cpl = cpl_fixed;
-    else if (M <= 32 && waves(16, split) >= kSkWaveTarget) cpl = 16;
+    else if (M <= 32 && waves(16, split_req) >= kSkWaveTarget && ok(split_req, 16)) cpl = 16;
+    if (!ok(split_req, cpl)) return false;
+    split = split_req;
   } else if (cpl_fixed) {
     cpl = cpl_fixed;
     split = pick(cpl);
   } else {
-    // 256-column tiles when they reach the wave target without extra slices
+    // 256-column tiles when they reach the wave target without extra slices, unless
+    // group-spanning waves on 128-column tiles need fewer slices
     int first = 0;
     for (int s = 1; s <= K / (nw * kSkStep) && !first; ++s)
-      if (ok(s)) first = s;
-    if (first && M <= 32 && waves(16, first) >= kSkWaveTarget) {
+      if (ok(s, 16)) first = s;
+    const int s8 = pick(8);
+    if (first && M <= 32 && waves(16, first) >= kSkWaveTarget && !(mg_ok && s8 && s8 < first)) {
       cpl = 16;
       split = first;
     } else {
-      split = pick(8);
+      split = s8;
     }
   }
   if (!split) return false;
-  *out = {mb, cpl, nw, rp, split, K / split, (int)cdiv(N, 16 * cpl)};
+  *out = {mb, cpl, nw, rp, split, K / split, (int)cdiv(N, 16 * cpl),
+          has_gs && K / split / nw > group};
   return true;
 }
 
@@ -474,28 +520,29 @@ bool skinny_fits(int M, int N, int K, int64_t lda, int64_t ldq, int group, bool 
          (!has_gs || (int64_t)(K / group) * N * 2 < (1ll << 31));
 }
 
-template <int MB, int CPL, int NW, bool GS>
+template <int MB, int CPL, int NW, bool GS, bool MG>
 static void launch_skinny_t(const SkinnyParams& p, bool l2, hipStream_t s) {
   // k-steps in flight per wave, measured on the Llama-3-8B shapes: 3 for one 16-row block of
   // 16 columns per lane (162 VGPRs, three waves per SIMD; 2-3% faster than 4 at two waves),
-  // 2 for two blocks; 8 columns per lane halve the weight registers.
-  constexpr int PD = CPL == 16 ? (MB == 1 ? 3 : 2) : (MB == 1 ? 4 : MB == 2 ? 3 : 2);
+  // 2 for two blocks; 8 columns per lane halve the weight registers. Group-spanning waves
+  // keep a divisor of the group's 4 k-steps.
+  constexpr int PD = MG ? 2 : CPL == 16 ? (MB == 1 ? 3 : 2) : (MB == 1 ? 4 : MB == 2 ? 3 : 2);
   constexpr int OCC = NW == 4 ? 2 : 1;
   // tiles rounded up to whole groups of 8 XCDs (of pairs with 8 columns per lane)
   const unsigned slots = (unsigned)(cdiv(p.tiles, CPL == 8 ? 16 : 8) * (CPL == 8 ? 16 : 8));
   if (l2) {
-    w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, true>
+    w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, true, MG>
         <<<slots * p.split * p.row_parts, 64 * NW, 0, s>>>(p);
     return;
   }
-  w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, false>
+  w4a16_skinny_kernel<MB, CPL, NW, GS, PD, OCC, false, MG>
       <<<dim3(slots * p.row_parts, p.split), 64 * NW, 0, s>>>(p);
 }
 
-template <int MB, int CPL, bool GS>
+template <int MB, int CPL, bool GS, bool MG = false>
 static void launch_skinny_nw(const SkinnyParams& p, int nw, bool l2, hipStream_t s) {
-  if (nw == 8) launch_skinny_t<MB, CPL, 8, GS>(p, l2, s);
-  else launch_skinny_t<MB, CPL, 4, GS>(p, l2, s);
+  if (nw == 8) launch_skinny_t<MB, CPL, 8, GS, MG>(p, l2, s);
+  else launch_skinny_t<MB, CPL, 4, GS, MG>(p, l2, s);
 }
 
 template <bool GS>
@@ -505,7 +552,12 @@ static void launch_skinny_cfg(const SkinnyPlan& pl, const SkinnyParams& p, bool 
     else launch_skinny_nw<2, 16, GS>(p, pl.nw, l2, s);
   } else {
     if (pl.mb == 1) launch_skinny_nw<1, 8, GS>(p, pl.nw, l2, s);
-    else if (pl.mb == 2) launch_skinny_nw<2, 8, GS>(p, pl.nw, l2, s);
+    else if (pl.mb == 2) {
+      if constexpr (GS) {
+        if (pl.mg) return launch_skinny_nw<2, 8, GS, true>(p, pl.nw, l2, s);
+      }
+      launch_skinny_nw<2, 8, GS>(p, pl.nw, l2, s);
+    }
     else launch_skinny_nw<4, 8, GS>(p, pl.nw, l2, s);
   }
 }
@@ -517,10 +569,11 @@ static void launch_skinny_cfg(const SkinnyPlan& pl, const SkinnyParams& p, bool 
 // workgroup's gather of 32 * split partial rows per tile pays on the smaller layers (qkv
 // 13.85 -> 13.1, o_proj 12.1 -> 10.6 us) but not on the larger (gate_up 22.1 -> 22.8, down
 // 22.7 -> 26.1), and with four blocks it was slower everywhere, so those keep the reduce
-// launch.
+// launch. Group-spanning plans (half the slices, 128-column tiles) gather a quarter of those
+// bytes per tile and hand off in L2 on every layer (down M = 32 with 7 slices: 19.5 -> 18.5).
 bool skinny_l2(const SkinnyPlan& pl) {
   const int64_t weights = (int64_t)pl.split * pl.k_slice * pl.tiles * 16 * pl.cpl;
-  const bool blocks_ok = pl.mb == 1 || (pl.mb == 2 && weights <= 4096ll * 6144);
+  const bool blocks_ok = pl.mb == 1 || (pl.mb == 2 && (weights <= 4096ll * 6144 || pl.mg));
   return pl.split > 1 && blocks_ok && pl.tiles * pl.row_parts <= kWsMaxTiles &&
          splitk_in_l2_ok();
 }

@@ -73,14 +73,15 @@ def test_gemv_l2_handoff_matches_two_phase(M, K, N, cuda):
 @pytest.mark.parametrize("M,K,N", [(8, 4096, 6144), (12, 4096, 11008), (32, 4096, 4096),
                                    (17, 2048, 528), (8, 14336, 4096), (128, 4096, 4000),
                                    (100, 2048, 1040), (48, 4096, 2048), (5, 1024, 4112),
-                                   (16, 4096, 1024)])
+                                   (16, 4096, 1024), (32, 14336, 4096), (24, 4096, 14336)])
 def test_skinny_one_call_matches_two_phase(M, K, N, cuda):
     a, qw, sc, codes, s16 = _case(M, K, N, 1100 + M + N % 89, cuda)
     ag = a.to(cuda)
     kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
     assert kid == _pk.KERNEL_SKINNY and split > 1
     # one launch for one 16-row block, and for two on layers of at most 4096 x 6144 weights
-    single = M <= 16 or (M <= 32 and K * N <= 4096 * 6144)
+    # or with wave rows spanning several groups (half the slices)
+    single = M <= 16 or (M <= 32 and (K * N <= 4096 * 6144 or K // split // 8 > 128))
     assert _pk.w4a16_launches(M, N, K, 128, 0) == (1 if single else 2)
     one = gemm_int4.w4a16_gemm(ag, qw, sc, 128, out_dtype=torch.float32)
     assert torch.equal(one, _two_phase(ag, qw, sc, split, cuda))

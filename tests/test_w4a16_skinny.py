@@ -58,15 +58,18 @@ def test_skinny_group_sizes(G, cuda):
 @pytest.mark.parametrize("M", [8, 32])
 def test_skinny_split_k_deterministic(M, cuda):
     """Every explicit split whose wave rows (K / split / waves) fit in one group is bitwise
-    reproducible, and splits agree up to fp32 reassociation; other splits go to the GEMM.
+    reproducible, and splits agree up to fp32 reassociation; other splits go to the GEMM, except
+    that two 16-row blocks (M = 32) take wave rows of whole 128-row groups (split 1: 256 rows).
     Splits 4 and 8 run 8 waves per workgroup, 16 (128-row slices) 4 waves."""
     K, N = 2048, 1024
     a, qw, sc, codes, s16 = _case(M, K, N, 60 + M, cuda)
     ag = a.to(cuda)
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
-    assert _pk.w4a16_plan(M, N, K, 128, 1)[0] == _pk.KERNEL_GEMM
+    spanning = M > 16
+    assert _pk.w4a16_plan(M, N, K, 128, 1) == ((_pk.KERNEL_SKINNY, 1) if spanning
+                                               else (_pk.KERNEL_GEMM, 1))
     base = None
-    for s in (4, 8, 16):
+    for s in ((1, 4, 8, 16) if spanning else (4, 8, 16)):
         assert _pk.w4a16_plan(M, N, K, 128, s) == (_pk.KERNEL_SKINNY, s)
         o1 = gemm_int4.w4a16_gemm(ag, qw, sc, 128, split_k=s, out_dtype=torch.float32)
         o2 = gemm_int4.w4a16_gemm(ag, qw, sc, 128, split_k=s, out_dtype=torch.float32)
@@ -75,6 +78,34 @@ def test_skinny_split_k_deterministic(M, cuda):
         base = o1 if base is None else base
         # fp32 reassociation, amplified ~10x by removing the +8 offset (as in the GEMV test)
         assert oracle.rel_fro(o1.cpu().numpy(), base.cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("M,K,N,split", [(32, 4096, 14336, 0), (24, 14336, 4096, 0),
+                                         (17, 2048, 1024, 1), (20, 4096, 512, 1),
+                                         (32, 4096, 768, 2), (30, 8192, 1280, 4)])
+def test_skinny_group_spanning_waves(M, K, N, split, cuda):
+    """Two 16-row blocks whose waves take several 128-row groups (gate_up and down at M = 32
+    halve their slices this way; 2, 4 and 8 groups per wave here): each group's sums are
+    scaled and added at its boundary. Within the oracle's tolerance, bitwise repeatable, the
+    one-launch handoff bitwise equal to the partials plus the ordered reduce, and the block
+    layout bitwise equal to the rows."""
+    kid, used = _pk.w4a16_plan(M, N, K, 128, split)
+    assert kid == _pk.KERNEL_SKINNY and K // used // 8 > 128, (kid, used)
+    a, qw, sc, codes, s16 = _case(M, K, N, 500 + M + N % 97, cuda)
+    ag = a.to(cuda)
+    out = _pk.w4a16_gemm(ag, qw, sc, 128, 1.0, torch.float32, split_k=split)
+    assert torch.equal(out, _pk.w4a16_gemm(ag, qw, sc, 128, 1.0, torch.float32, split_k=split))
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
+    assert oracle.rel_fro(out.cpu().numpy(), ref) <= W4A16_TOL
+    if used > 1:
+        parts = _pk.w4a16_gemm_partials(ag, qw, sc, 128, used)
+        two = torch.empty((M, N), dtype=torch.float32, device=cuda)
+        _pk.splitk_reduce(parts, 1.0, two)
+        assert torch.equal(out, two)
+    if N % 256 == 0:
+        tiles = _pk.w4a16_gemm(ag, _pk.tile_weights(qw), sc, 128, 1.0, torch.float32,
+                               split_k=split, tiled=True)
+        assert torch.equal(out, tiles)
 
 
 @pytest.mark.parametrize("M,split", [(8, 4), (20, 8)])
