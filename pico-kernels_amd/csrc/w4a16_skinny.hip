@@ -29,7 +29,9 @@
 // and with O = sum x * 8 * 2^-24 (one more MFMA per k-step against a constant operand)
 //   sum x * v_lo = (L - O) * 2^24,   sum x * v_hi = (R - L - 16 O) * 2^20.
 // A wave's rows lie in one quantisation group, so its fp32 result is scaled once per column
-// at the end (exact powers of two folded into the scale).
+// at the end (exact powers of two folded into the scale); with two 16-row blocks and 8 columns
+// per lane a wave may instead take several whole 128-row groups, scaling and adding each
+// group's sums at its boundary (fewer slices on deep or wide layers).
 //
 // Reduction: the waves' tiles are added in LDS in a fixed order. With split-K and one 16-row
 // block the slices of a column tile hand off through one XCD's L2 inside the launch, as the
