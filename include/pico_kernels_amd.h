@@ -183,7 +183,8 @@ int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* qtiled, cons
  * 4096 x 4096 weights: with an automatic split where the layer has at least 1024 x 1024
  * weights and the kernel's plan needs at most 8 slices, else where the next kernel does not
  * take the shape, 4 = MFMA GEMM that keeps B packed in
- * LDS, for M > 64 with N % 256 == 0, K % 128 == 0, group % 64 == 0 (split-K with a reduce
+ * LDS, for M > 64, and with an automatic split for M > 32 on layers of more than 4096 x 8192
+ * weights, with N % 256 == 0, K % 128 == 0, group % 64 == 0 (split-K with a reduce
  * launch where its tiles leave CUs idle), assuming 16-byte aligned operands) and the
  * effective split. */
 int pk_w4a16_plan(int M, int N, int K, int group_size, int split_k, int* kernel_id,

@@ -2,10 +2,11 @@
 // dense fp16 split-K matmul (gemm_splitk.triton_gemm_splitk).
 //
 // Dispatch: M <= 4 runs the HBM-bound GEMV (w4a16_gemv.hip); up to 64 rows the register-dequant
-// MFMA kernel (w4a16_skinny.hip); larger M the GEMM that keeps B packed in LDS
-// (w4a16_tr4.hip, split-K where its tiles leave CUs idle) where its shape rules hold, else the
-// register-dequant kernel (up to 128 rows of layers of at most 4096 x 4096 weights) or the
-// GEMMs that dequantise into LDS. All honour an explicit split_k.
+// MFMA kernel (w4a16_skinny.hip), except from 33 rows on layers of more than 4096 x 8192
+// weights; larger M the GEMM that keeps B packed in LDS (w4a16_tr4.hip, split-K where its
+// tiles leave CUs idle) where its shape rules hold, else the register-dequant kernel (up to
+// 128 rows of layers of at most 4096 x 4096 weights) or the GEMMs that dequantise into LDS. All
+// honour an explicit split_k. make_plan gives the measured rules.
 #include "pk_internal.h"
 
 #include <atomic>
@@ -65,10 +66,14 @@ bool make_plan(int M, int N, int K, int group_size, bool has_gs, int split_k, W4
     pl->kernel = kKernelSkinny;
     return true;
   }
-  // Above the skinny kernel's 64 rows: the packed-B GEMM where its shape rules hold, with the
+  // Above the skinny kernel's 64 rows, and from 33 rows on layers of more than 4096 x 8192
+  // weights with an automatic split: the packed-B GEMM where its shape rules hold, with the
   // GEMM that dequantises into LDS at the same split as its fallback (operands misaligned for
-  // it, or beyond its 32-bit offsets), so the workspace covers both.
-  if (M > 64 && tr4_shape_ok(M, N, K, group_size, has_gs)) {
+  // it, or beyond its 32-bit offsets), so the workspace covers both. (33..64 rows, measured on
+  // MI355X: 4096 x 11008, 4096 x 14336 and 14336 x 4096 3-16% faster on the packed-B GEMM;
+  // 4096 x 6144, 4096 x 8192, 8192 x 4096 and 14336 x 2048 9-35% faster on the skinny kernel.)
+  const bool tr4_rows = M > 64 || (M > 32 && split_k == 0 && (int64_t)K * N > 4096ll * 8192);
+  if (tr4_rows && tr4_shape_ok(M, N, K, group_size, has_gs)) {
     const int s = split_k > 0 ? split_k : tr4_pick_split(M, N, K);
     if (tr4_split_ok(K, s) && gemm_plan(M, N, K, group_size, has_gs, s, &pl->gemm)) {
       pl->kernel = kKernelGemmTr4;

@@ -80,7 +80,11 @@ def test_w4a16_plans_by_row_count():
         assert _pk.w4a16_plan(M, 6144, 4096, 128, 0) == (S, 4)       # 48 tiles x 4 x 8 waves
     assert _pk.w4a16_plan(8, 4096, 4096, 128, 0) == (S, 8)           # 32 tiles x 8 x 8
     assert _pk.w4a16_plan(8, 4096, 14336, 128, 0) == (S, 14)         # 16 wide tiles x 14 x 8
-    assert _pk.w4a16_plan(48, 4096, 14336, 128, 0) == (S, 14)
+    # 33..64 rows of layers of more than 4096 x 8192 weights: the packed-B GEMM
+    assert _pk.w4a16_plan(48, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 14)
+    assert _pk.w4a16_plan(40, 11008, 4096, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
+    assert _pk.w4a16_plan(64, 8192, 4096, 128, 0) == (S, 4)
+    assert _pk.w4a16_plan(48, 4096, 14336, 128, 14) == (S, 14)      # explicit split
     # short K: 384 rows fit no 8-wave slice -> 4 waves, 3 slices of one 32-row k-step each
     assert _pk.w4a16_plan(8, 528, 384, 128, 0) == (S, 3)
     # explicit splits whose wave rows exceed a group go to the GEMM

@@ -141,3 +141,20 @@ def test_tr4_split_k_per_tensor_strided_out(cuda):
     _pk.w4a16_gemm(ag, packed, None, 0, 0.037, torch.float16, out=big[:, 128:128 + N])
     assert torch.equal(big[:, 128:128 + N], dense)
     assert torch.all(big[:, :128] == 3.0) and torch.all(big[:, 128 + N:] == 3.0)
+
+
+@pytest.mark.parametrize("M", [33, 48, 64])
+@pytest.mark.parametrize("K,N", [(4096, 11008), (14336, 4096)])
+def test_tr4_mid_rows_on_large_layers(M, K, N, cuda):
+    """33..64 rows of layers of more than 4096 x 8192 weights run the packed-B GEMM with an
+    automatic split: one 128-row tile, most of it past M, split-K partials and the ordered
+    reduce; against the oracle, bitwise repeatable, and on the block layout bitwise equal."""
+    a, codes, s16, qw, sc = _case(M, K, N, 128, 900 + M + K % 97, cuda)
+    kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
+    assert kid == _pk.KERNEL_GEMM_TR4 and split > 1
+    ag = a.to(cuda)
+    out = _pk.w4a16_gemm(ag, qw, sc, 128, 1.0, torch.float32)
+    assert torch.equal(out, _pk.w4a16_gemm(ag, qw, sc, 128, 1.0, torch.float32))
+    assert oracle.rel_fro(out.cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, 128)) <= 1e-3
+    tiles = _pk.w4a16_gemm(ag, _pk.tile_weights(qw), sc, 128, 1.0, torch.float32, tiled=True)
+    assert torch.equal(out, tiles)
