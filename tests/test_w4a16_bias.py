@@ -42,6 +42,9 @@ PATHS = [
     (256, 1024, 1152, 0, _pk.KERNEL_GEMM),    # LDS-dequant large tiles, split-K
     (300, 512, 1160, 1, _pk.KERNEL_GEMM),     # LDS-dequant large tiles, unsplit, ragged
     (40, 1024, 520, 0, _pk.KERNEL_GEMM),      # small-tile GEMM (N % 16 != 0)
+    (24, 4096, 3072, 1, _pk.KERNEL_SKINNY),   # group-spanning waves (4 groups), unsplit
+    (32, 8192, 1280, 4, _pk.KERNEL_SKINNY),   # group-spanning waves, slices added in L2
+    (40, 4096, 11008, 0, _pk.KERNEL_GEMM_TR4),  # 33..64 rows of a large layer: packed-B
 ]
 
 

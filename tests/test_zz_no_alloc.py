@@ -41,6 +41,7 @@ def _noalloc(a, qw, sc, split, out):
     [(1, 4096, 11008, 0), (1, 1024, 512, 4)],       # GEMV, slices added through the scratch
     [(4, 4096, 4096, 16), (2, 2048, 1024, 8)],
     [(32, 4096, 6144, 0), (8, 1024, 2048, 2)],      # register-dequant kernel + reduce launch
+    [(32, 14336, 4096, 0), (24, 4096, 1024, 2)],    # group-spanning waves, slices in L2
     [(256, 4096, 1024, 4), (128, 2048, 512, 2)],    # packed-B GEMM, split-K + reduce launch
     [(256, 4096, 1152, 4), (128, 2048, 520, 2)],    # LDS-tiled GEMM, split-K
     [(2048, 512, 2048, 0), (256, 512, 512, 1)],     # unsplit: no scratch used
