@@ -891,7 +891,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the kernel is "
-              "benchmarked at its single-GPU shape; see the sharding notes in DESIGN.md).",
+              "benchmarked at its single-GPU shape, one GPU's share of a sharded layer).",
               file=sys.stderr)
         return 2
 
