@@ -177,6 +177,14 @@ int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* qtiled, cons
                         void* c, int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Rows per kernel call of pk_w4a16_gemm_tiled for M activation rows of stride lda elements:
+ * M itself while the activations span less than 2 GiB (M * lda * 2 bytes); beyond that the
+ * call runs equal chunks of this many rows (a multiple of 128), since the kernels that read
+ * block-layout weights at large M address their operands with 32-bit buffer offsets; 0 when
+ * even 128 rows exceed that. No device work. No counterpart in the reference (a Triton launch
+ * addresses its operands with 64-bit pointers). */
+int64_t pk_w4a16_tiled_rows_per_call(int64_t M, int64_t lda);
+
 /* Which kernel pk_w4a16_gemm would run and its split factor (for reporting/benchmarks):
  * writes kernel id (1 = GEMV for M <= 4, 2 = LDS-tiled MFMA GEMM that dequantises B into LDS,
  * 3 = register-dequant MFMA kernel for 5 <= M <= 64, and M <= 128 on layers of at most

@@ -58,6 +58,7 @@ _SIGNATURES = {
     "pk_w4a16_gemm_tiled": (_i32, [_vp, _i64, _vp, _vp, _i32, _f32, _vp, _i32, _vp, _i32, _i64,
                                    _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
     "pk_w4a16_noalloc_scratch_bytes": (_sz, []),
+    "pk_w4a16_tiled_rows_per_call": (_i64, [_i64, _i64]),
     "pk_w4a16_skinny_layout": (_i32, [_i32, _i32]),
     "pk_w4a16_prep_activations": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _vp]),
     "pk_w4a16_gemm_noalloc": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
@@ -280,6 +281,25 @@ def w4a16_launches(M: int, N: int, K: int, group_size: int, split_k: int) -> int
     n = lib().pk_w4a16_launches(M, N, K, group_size, split_k)
     _check(min(n, 0), "pk_w4a16_launches")
     return n
+
+
+FP16_MAX = 65504.0
+
+
+def check_fp16_range(x: torch.Tensor, what: str, converted: torch.Tensor | None = None) -> None:
+    """Raise ``ValueError`` when a finite element of ``x`` (bf16 / fp32 activations the W4A16
+    kernels take as fp16) lies beyond fp16's largest finite value 65504, where the fp16 cast
+    would turn it into an infinity -- or, given ``converted`` (the fp16 tensor made from
+    ``x``), when a finite element of ``x`` became infinite in it. One device reduction and a
+    synchronisation; skipped while the stream is being captured into a graph (no
+    synchronisation is allowed there)."""
+    if x.dtype == torch.float16 or (x.is_cuda and torch.cuda.is_current_stream_capturing()):
+        return
+    bad = torch.isinf(converted) if converted is not None else x.abs() > FP16_MAX
+    if bool((bad & torch.isfinite(x)).any()):
+        big = x[torch.isfinite(x)].abs().max().item()
+        raise ValueError(f"{what}: {x.dtype} activations up to |x| = {big:g} exceed fp16's range "
+                         f"(65504); the W4A16 kernels compute in fp16")
 
 
 def _rows_ok(t: torch.Tensor) -> torch.Tensor:

@@ -130,8 +130,8 @@ int v2_f8_launch(const uint8_t* a8, int64_t lda, const uint8_t* b8, int64_t ldb,
 bool tr4_shape_ok(int M, int N, int K, int group, bool has_gs);
 bool tr4_split_ok(int K, int split);
 int tr4_pick_split(int M, int N, int K);
-bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ldb, int64_t ldc,
-            int c_dtype, const void* c, int split);
+bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, const void* b, int64_t ldb,
+            int64_t ldc, int c_dtype, const void* c, int split);
 int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const void* scales,
                int group, OutEpi epi, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
                int split, void* workspace, hipStream_t s, bool partials_only, bool tiled = false);

@@ -119,7 +119,7 @@ bool plan_reads_tiles(const W4Plan& pl, const void* a, int64_t lda, const uint32
   if (pl.kernel == kKernelGemv) return gemv_tiled_ok(pl.gemv, a, lda, qw, ldq, scales, group, M, N, K);
   if (pl.kernel == kKernelSkinny) return skinny_fits(M, N, K, lda, ldq, group, scales != nullptr);
   if (pl.kernel == kKernelGemmTr4)
-    return tr4_ok(M, N, K, group, scales != nullptr, lda, ldq, ldc, c_dtype, c, pl.tr4_split);
+    return tr4_ok(M, N, K, group, scales != nullptr, lda, qw, ldq, ldc, c_dtype, c, pl.tr4_split);
   return false;
 }
 
@@ -134,7 +134,7 @@ int plan_launch(const W4Plan& pl, const void* a, int64_t lda, const uint32_t* qw
     return skinny_launch(pl.skinny, a, lda, qw, ldq, scales, group, epi, c, c_dtype,
                          ldc, M, N, K, workspace, s, partials_only, tiled);
   if (pl.kernel == kKernelGemmTr4 &&
-      tr4_ok(M, N, K, group, scales != nullptr, lda, ldq, ldc, c_dtype, c, pl.tr4_split))
+      tr4_ok(M, N, K, group, scales != nullptr, lda, qw, ldq, ldc, c_dtype, c, pl.tr4_split))
     return tr4_launch(a, lda, qw, ldq, scales, group, epi, c, c_dtype, ldc, M, N, K,
                       pl.tr4_split, workspace, s, partials_only, tiled);
   if (tiled) {
@@ -201,6 +201,18 @@ extern "C" size_t pk_w4a16_workspace_bytes(int M, int N, int K, int group_size, 
 }
 
 namespace {
+// Activations whose rows span 2 GiB or more exceed the 32-bit buffer offsets of the kernels
+// that read block-layout weights at large M (the packed-B GEMM). Such calls run as equal
+// chunks of rows, each a whole multiple of 128 rows below that limit (0: lda too large).
+constexpr int64_t kBufferBytes = 1ll << 31;
+int64_t tiled_rows_per_call(int64_t M, int64_t lda) {
+  if (M * lda * 2 < kBufferBytes) return M;
+  const int64_t cap = ((kBufferBytes - 1) / (lda * 2)) / 128 * 128;
+  if (cap < 128) return 0;
+  const int64_t chunks = cdiv(M, cap);
+  return cdiv(cdiv(M, chunks), 128) * 128;
+}
+
 int w4a16_gemm_ws(const char* name, const void* a, int64_t lda, const uint32_t* qweight,
                   int64_t ldq, const void* scales, int group_size, OutEpi epi, void* c,
                   int c_dtype, int64_t ldc, int M, int N, int K, int split_k, void* workspace,
@@ -208,6 +220,21 @@ int w4a16_gemm_ws(const char* name, const void* a, int64_t lda, const uint32_t* 
   int rc = check_w4a16(a, lda, qweight, ldq, scales, group_size, c, c_dtype, ldc, M, N, K,
                        split_k);
   if (rc != PK_OK) return rc;
+  if (tiled && (int64_t)M * lda * 2 >= kBufferBytes) {
+    const int64_t rows = tiled_rows_per_call(M, lda);
+    PK_REQUIRE(rows > 0, "%s: activation rows of %lld elements are beyond the block-layout "
+               "kernels' 2 GiB buffers", name, (long long)lda);
+    const int esz = c_dtype == PK_F32 ? 4 : 2;
+    for (int64_t r0 = 0; r0 < M; r0 += rows) {
+      const int m = (int)(M - r0 < rows ? M - r0 : rows);
+      rc = w4a16_gemm_ws(name, static_cast<const char*>(a) + r0 * lda * 2, lda, qweight, ldq,
+                         scales, group_size, epi, static_cast<char*>(c) + r0 * ldc * esz,
+                         c_dtype, ldc, m, N, K, split_k, workspace, workspace_bytes, stream,
+                         true);
+      if (rc != PK_OK) return rc;
+    }
+    return PK_OK;
+  }
   const bool has_gs = scales != nullptr;
   const int group = has_gs ? group_size : K;
   W4Plan pl;
@@ -238,6 +265,10 @@ extern "C" int pk_w4a16_gemm(const void* a, int64_t lda, const uint32_t* qweight
   return w4a16_gemm_ws("pk_w4a16_gemm", a, lda, qweight, ldq, scales, group_size,
                        OutEpi(tensor_scale), c, c_dtype, ldc, M, N, K, split_k, workspace,
                        workspace_bytes, stream);
+}
+
+extern "C" int64_t pk_w4a16_tiled_rows_per_call(int64_t M, int64_t lda) {
+  return M >= 1 && lda >= 1 ? tiled_rows_per_call(M, lda) : 0;
 }
 
 extern "C" int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* qtiled,

@@ -436,10 +436,12 @@ int tr4_pick_split(int M, int N, int K) {
   return best;
 }
 
-bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, int64_t ldb, int64_t ldc,
-            int c_dtype, const void* c, int split) {
+bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, const void* b, int64_t ldb,
+            int64_t ldc, int c_dtype, const void* c, int split) {
   if (!tr4_shape_ok(M, N, K, group, has_gs) || !tr4_split_ok(K, split)) return false;
   if (lda % 8) return false;
+  // B is DMA'd in 16-byte chunks at k * ldb * 4 + 16 * j: 16-byte aligned base and rows
+  if ((reinterpret_cast<uintptr_t>(b) & 15) || ldb % 4) return false;
   // unsplit: the epilogue stores 16-byte chunks of the output itself
   const int esz = c_dtype == PK_F32 ? 4 : 2;
   if (split == 1 && ((ldc * esz) % 16 || (reinterpret_cast<uintptr_t>(c) & 15))) return false;

@@ -65,43 +65,57 @@ def eager_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Ten
     return (torch.softmax(s, dim=-1) @ vf).to(q.dtype)
 
 
-def check_correctness(N: int = 2048, D: int = 64, split_size: int = 256) -> None:
-    """The reference's self-check (flash_decoding.py:128-138): split-KV decode against
-    eager_decode, max abs error and allclose at 1e-2."""
-    torch.manual_seed(0)
-    B, H = 2, 4
-    q = torch.randn(B, H, 1, D, device="cuda", dtype=torch.float16)
-    k = torch.randn(B, H, N, D, device="cuda", dtype=torch.float16)
-    v = torch.randn(B, H, N, D, device="cuda", dtype=torch.float16)
-    o = flash_decoding(q, k, v, split_size=split_size)
-    ref = eager_decode(q, k, v)
-    err = (o.float() - ref.float()).abs().max().item()
-    print(f"flash-decoding vs eager (N={N}): max abs err {err:.3e} | "
-          f"allclose {torch.allclose(o.float(), ref.float(), atol=1e-2, rtol=1e-2)}")
+def _harness_checks() -> list:
+    """Self-check at the reference's check shape (flash_decoding.py:128-138: B2 H4 N2048 D64,
+    split 256): split-KV decode against ``eager_decode``, max absolute error and
+    torch.allclose at atol = rtol = 1e-2."""
+    from _timing import Check
+
+    def measure():
+        g = torch.Generator(device="cuda").manual_seed(0)
+        q, k, v = (torch.randn(2, 4, n, 64, device="cuda", dtype=torch.float16, generator=g)
+                   for n in (1, 2048, 2048))
+        o = flash_decoding(q, k, v, split_size=256).float()
+        ref = eager_decode(q, k, v).float()
+        return {"max_abs_err": (o - ref).abs().max().item(),
+                "allclose_1e-2": bool(torch.allclose(o, ref, atol=1e-2, rtol=1e-2))}
+
+    return [Check("split256_B2H4N2048D64", measure, {"allclose_1e-2": (True, True)})]
+
+
+def _harness_rows() -> list:
+    """The reference's benchmark cases (flash_decoding.py:141-152: B2 H4 D64, split 256,
+    N = 1K..8K): ``eager_decode`` against ``flash_decoding``, in milliseconds."""
+    from _timing import Row
+
+    def build(n):
+        def make():
+            q, k, v = (torch.randn(2, 4, m, 64, device="cuda", dtype=torch.float16)
+                       for m in (1, n, n))
+            return {"eager": lambda: eager_decode(q, k, v),
+                    "flash_decoding": lambda: flash_decoding(q, k, v, split_size=256)}
+        return make
+
+    return [Row(f"B=2,H=4,N={n},D=64", build(n)) for n in (1024, 2048, 4096, 8192)]
+
+
+def check_correctness() -> bool:
+    """Run and print the module's self-check (see ``_harness_checks``)."""
+    from _timing import run_checks
+
+    return run_checks("flash_decoding", _harness_checks())
 
 
 def bench() -> None:
-    """The reference's benchmark table (flash_decoding.py:141-152): eager decode against
-    split-KV decode at B=2, H=4, D=64, split 256, N = 1K..8K (milliseconds)."""
-    from _timing import do_bench
+    """Time and print the module's benchmark rows (see ``_harness_rows``)."""
+    from _timing import run_rows
 
-    B, H, D = 2, 4, 64
-    print(f"{'N':>7} {'eager decode':>13} {'flash-decoding':>15} {'speedup':>8}")
-    print("-" * 46)
-    for N in (1024, 2048, 4096, 8192):
-        q = torch.randn(B, H, 1, D, device="cuda", dtype=torch.float16)
-        k = torch.randn(B, H, N, D, device="cuda", dtype=torch.float16)
-        v = torch.randn(B, H, N, D, device="cuda", dtype=torch.float16)
-        ms_eager = do_bench(lambda: eager_decode(q, k, v))
-        ms_fd = do_bench(lambda: flash_decoding(q, k, v, split_size=256))
-        print(f"{N:>7} {ms_eager:>12.3f}m {ms_fd:>12.3f}m {ms_eager / ms_fd:>7.2f}x")
+    run_rows("flash_decoding", _harness_rows())
 
 
 if __name__ == "__main__":
-    from _timing import banner
+    import sys
 
-    print(banner())
-    print("=== correctness ===")
-    check_correctness()
-    print("=== benchmark (decode, M=1) ===")
-    bench()
+    from _timing import main
+
+    sys.exit(main("flash_decoding", _harness_checks(), _harness_rows()))

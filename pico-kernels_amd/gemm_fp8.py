@@ -58,43 +58,58 @@ def fp8_gemm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return fp8_gemm_precast(a8, a_scale, b8, b_scale)
 
 
-def check_correctness(M: int = 1024, K: int = 1024, N: int = 1024) -> None:
-    """The reference's self-check (gemm_fp8.py:127-136): fp8_gemm against the fp32 product."""
-    torch.manual_seed(0)
-    a = torch.randn(M, K, device="cuda", dtype=torch.float16)
-    b = torch.randn(K, N, device="cuda", dtype=torch.float16)
-    c = fp8_gemm(a, b)
-    ref = a.float() @ b.float()
-    rel_fro = torch.norm(c - ref) / torch.norm(ref)
-    print(f"fp8 vs fp32: rel Frobenius err {rel_fro.item():.4%} | "
-          f"max abs err {(c - ref).abs().max().item():.3e}")
+def _harness_checks() -> list:
+    """Self-check at the reference's check shape (gemm_fp8.py:127-136: 1024^3, N(0,1) fp16):
+    ``fp8_gemm`` against the fp32 product. Its relative Frobenius error is the e4m3 rounding
+    of both operands, ~3.7% for N(0,1) data (the reference reports 3.74%)."""
+    from _timing import Check
+
+    def measure():
+        g = torch.Generator(device="cuda").manual_seed(0)
+        a = torch.randn(1024, 1024, device="cuda", dtype=torch.float16, generator=g)
+        b = torch.randn(1024, 1024, device="cuda", dtype=torch.float16, generator=g)
+        y = fp8_gemm(a, b)
+        exact = a.float() @ b.float()
+        return {"rel_fro": (torch.linalg.norm(y - exact) / torch.linalg.norm(exact)).item(),
+                "max_abs_err": (y - exact).abs().max().item()}
+
+    return [Check("fp8_gemm_1024^3", measure, {"rel_fro": (0.02, 0.06)})]
+
+
+def _harness_rows() -> list:
+    """The reference's benchmark sizes (gemm_fp8.py:139-156): square fp16 matmul through torch
+    (hipBLASLt) against ``fp8_gemm_precast`` on operands cast once, outside the timing."""
+    from _timing import Row
+
+    def build(n):
+        def make():
+            a = torch.randn(n, n, device="cuda", dtype=torch.float16)
+            b = torch.randn(n, n, device="cuda", dtype=torch.float16)
+            (a8, sa), (b8, sb) = quantize(a), quantize(b)
+            return {"torch_fp16": lambda: a @ b,
+                    "fp8_gemm_precast": lambda: fp8_gemm_precast(a8, sa, b8, sb)}
+        return make
+
+    return [Row(f"M=N=K={n}", build(n), 2.0 * n ** 3) for n in (512, 1024, 2048, 4096)]
+
+
+def check_correctness() -> bool:
+    """Run and print the module's self-check (see ``_harness_checks``)."""
+    from _timing import run_checks
+
+    return run_checks("gemm_fp8", _harness_checks())
 
 
 def bench() -> None:
-    """The reference's benchmark table (gemm_fp8.py:139-156): GFLOPS of the fp16 matmul
-    (hipBLASLt through torch) and of fp8_gemm_precast (cast done once, untimed)."""
-    from _timing import do_bench
+    """Time and print the module's benchmark rows (see ``_harness_rows``)."""
+    from _timing import run_rows
 
-    print(f"{'size':>7} {'fp16 hipBLASLt':>14} {'fp8 HIP':>12} {'speedup':>8}")
-    print("-" * 46)
-    for size in (512, 1024, 2048, 4096):
-        a = torch.randn(size, size, device="cuda", dtype=torch.float16)
-        b = torch.randn(size, size, device="cuda", dtype=torch.float16)
-        a8, a_scale = quantize(a)
-        b8, b_scale = quantize(b)
-        flops = 2 * size**3 / 1e9
-        ms_fp16 = do_bench(lambda: a @ b)
-        ms_fp8 = do_bench(lambda: fp8_gemm_precast(a8, a_scale, b8, b_scale))
-        g_fp16 = flops / (ms_fp16 / 1e3)
-        g_fp8 = flops / (ms_fp8 / 1e3)
-        print(f"{size:>7} {g_fp16:>11.0f} G {g_fp8:>9.0f} G {g_fp8 / g_fp16:>7.2f}x")
+    run_rows("gemm_fp8", _harness_rows())
 
 
 if __name__ == "__main__":
-    from _timing import banner
+    import sys
 
-    print(banner())
-    print("=== correctness (fp8 vs fp32 reference) ===")
-    check_correctness()
-    print("=== benchmark (GFLOPS - higher is better; cast is pre-done) ===")
-    bench()
+    from _timing import main
+
+    sys.exit(main("gemm_fp8", _harness_checks(), _harness_rows()))

@@ -80,13 +80,15 @@ def int4_gemm(a: torch.Tensor, w_packed: torch.Tensor, scale: float,
     fp16 in one pass (``pk_w4a16_prep_activations``) and run on the fp16 kernels: the
     conversion is exact for 2^-17 <= |x| <= 65504 (and 0), so there the products with the
     exact integer codes, and the fp32 sums, are those of a bf16 dot; smaller magnitudes keep
-    fp16's subnormal precision and larger ones overflow.
+    fp16's subnormal precision. A finite bf16 activation above 65504 raises ``ValueError``
+    (checked with one device reduction, except while a graph is being captured).
     """
     assert a.is_cuda and a.dtype in (torch.float16, torch.bfloat16)
     M, K = a.shape
     K2, N_half = w_packed.shape
     assert K2 == K, "int4_gemm: w_packed must be (K, N//2) for a of shape (M, K)"
     if a.dtype == torch.bfloat16:
+        _pk.check_fp16_range(a, "int4_gemm")
         a = _pk.w4a16_prep_activations(a, None, 1.0)
     N = N_half * 2
     assert N % 8 == 0, "int4_gemm: N must be a multiple of 8 (whole int32 words)"
@@ -147,52 +149,62 @@ def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
                           split_k=0 if split_k is None else int(split_k))
 
 
-def check_correctness(M: int = 128, K: int = 256, N: int = 256) -> None:
-    """The reference's self-check (gemm_int4.py:95-104): per-tensor int4 GEMM against the
-    fp32 product of the dequantised weights, relative Frobenius error printed."""
-    torch.manual_seed(0)
-    a = torch.randn(M, K, device="cuda", dtype=torch.float16)
-    w = torch.randn(K, N, device="cuda", dtype=torch.float16)
-    w_q, scale = quantize_int4(w)
-    w_packed = pack_int4_n(w_q)
-    c = int4_gemm(a, w_packed, scale)
-    ref = a.float() @ (w_q.float() * scale)
-    rel = torch.norm(c - ref) / torch.norm(ref)
-    print(f"int4 vs fp16-quantized ref: rel Frobenius err {rel.item():.4%}")
+def _harness_checks() -> list:
+    """Self-check of the per-tensor path at the reference's check shape (gemm_int4.py:95-104:
+    128 x 256 x 256, N(0,1) fp16): the relative Frobenius error of ``int4_gemm`` against the
+    fp32 product of the dequantised weights, which the fused kernel reproduces to fp32
+    rounding."""
+    from _timing import Check
+
+    def measure():
+        g = torch.Generator(device="cuda").manual_seed(0)
+        a = torch.randn(128, 256, device="cuda", dtype=torch.float16, generator=g)
+        w = torch.randn(256, 256, device="cuda", dtype=torch.float16, generator=g)
+        codes, s = quantize_int4(w)
+        y = int4_gemm(a, pack_int4_n(codes), s)
+        exact = a.float() @ (codes.float() * s)
+        return {"rel_fro": (torch.linalg.norm(y - exact) / torch.linalg.norm(exact)).item()}
+
+    return [Check("int4_gemm_per_tensor_128x256x256", measure, {"rel_fro": (None, 1e-4)})]
+
+
+def _harness_rows() -> list:
+    """The reference's four benchmark shapes (gemm_int4.py:107-130), rates of torch's fp16
+    matmul (hipBLASLt) and of ``int4_gemm`` on the same operands."""
+    from _timing import Row
+
+    def build(M, N, K):
+        def make():
+            a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+            codes, s = quantize_int4(torch.randn(K, N, device="cuda", dtype=torch.float16))
+            wp = pack_int4_n(codes)
+            wd = codes.half() * s
+            return {"torch_fp16": lambda: a @ wd, "int4_gemm": lambda: int4_gemm(a, wp, s)}
+        return make
+
+    shapes = ((16, 4096, 4096, "decode"), (16, 8192, 8192, "decode"),
+              (1024, 4096, 4096, "mixed"), (4096, 4096, 4096, "compute"))
+    return [Row(f"M={M},N={N},K={K}", build(M, N, K), 2.0 * M * N * K, note)
+            for M, N, K, note in shapes]
+
+
+def check_correctness() -> bool:
+    """Run and print the module's self-check (see ``_harness_checks``)."""
+    from _timing import run_checks
+
+    return run_checks("gemm_int4", _harness_checks())
 
 
 def bench() -> None:
-    """The reference's benchmark table (gemm_int4.py:107-130): GFLOPS of the fp16 matmul
-    (hipBLASLt through torch) and of int4_gemm at its four shapes, HIP-event timed."""
-    from _timing import do_bench
+    """Time and print the module's benchmark rows (see ``_harness_rows``)."""
+    from _timing import run_rows
 
-    print(f"{'shape (M,N,K)':>16} {'fp16':>12} {'int4':>12} {'speedup':>8}  regime")
-    print("-" * 60)
-    cases = [
-        (16, 4096, 4096, "memory-bound (decode)"),
-        (16, 8192, 8192, "memory-bound (decode)"),
-        (1024, 4096, 4096, "mixed"),
-        (4096, 4096, 4096, "compute-bound"),
-    ]
-    for M, N, K, label in cases:
-        a = torch.randn(M, K, device="cuda", dtype=torch.float16)
-        w = torch.randn(K, N, device="cuda", dtype=torch.float16)
-        w_q, scale = quantize_int4(w)
-        w_packed = pack_int4_n(w_q)
-        flops = 2 * M * N * K / 1e9
-        ms_fp16 = do_bench(lambda: a @ w)
-        ms_int4 = do_bench(lambda: int4_gemm(a, w_packed, scale))
-        g_fp16 = flops / (ms_fp16 / 1e3)
-        g_int4 = flops / (ms_int4 / 1e3)
-        print(f"{(M, N, K)!s:>16} {g_fp16:>9.0f} G {g_int4:>9.0f} G "
-              f"{g_int4 / g_fp16:>7.2f}x  {label}")
+    run_rows("gemm_int4", _harness_rows())
 
 
 if __name__ == "__main__":
-    from _timing import banner
+    import sys
 
-    print(banner())
-    print("=== correctness (int4 vs quantized fp16 ref) ===")
-    check_correctness()
-    print("=== benchmark (GFLOPS - memory-bound is the win) ===")
-    bench()
+    from _timing import main
+
+    sys.exit(main("gemm_int4", _harness_checks(), _harness_rows()))

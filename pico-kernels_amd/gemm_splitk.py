@@ -31,47 +31,62 @@ def triton_gemm_splitk(a: torch.Tensor, b: torch.Tensor, split_k: int = 4,
     return _pk.gemm_dense(a, b, torch.float32, split_k)
 
 
-def check_correctness(M: int = 1024, K: int = 1024, N: int = 1024) -> None:
-    """The reference's self-check (gemm_splitk.py:83-91): split-K 4 against the fp32 product."""
-    torch.manual_seed(0)
-    a = torch.randn(M, K, device="cuda", dtype=torch.float16)
-    b = torch.randn(K, N, device="cuda", dtype=torch.float16)
-    c = triton_gemm_splitk(a, b, split_k=4)
-    ref = a.float() @ b.float()
-    print(f"split-K vs fp32: max abs err {(c - ref).abs().max().item():.3e} | "
-          f"allclose {torch.allclose(c, ref, atol=1e-2, rtol=1e-2)}")
+def _harness_checks() -> list:
+    """Self-check at the reference's check shape (gemm_splitk.py:83-91: 1024^3, split 4):
+    the split-K product against the fp32 product, max absolute error and torch.allclose at
+    atol = rtol = 1e-2."""
+    from _timing import Check
+
+    def measure():
+        g = torch.Generator(device="cuda").manual_seed(0)
+        a = torch.randn(1024, 1024, device="cuda", dtype=torch.float16, generator=g)
+        b = torch.randn(1024, 1024, device="cuda", dtype=torch.float16, generator=g)
+        y = triton_gemm_splitk(a, b, split_k=4)
+        exact = a.float() @ b.float()
+        return {"max_abs_err": (y - exact).abs().max().item(),
+                "allclose_1e-2": bool(torch.allclose(y, exact, atol=1e-2, rtol=1e-2))}
+
+    return [Check("splitk4_1024^3", measure, {"allclose_1e-2": (True, True)})]
+
+
+def _harness_rows() -> list:
+    """The reference's benchmark shapes and splits (gemm_splitk.py:94-113): torch's fp16
+    matmul (hipBLASLt), the unsplit ``gemm.triton_gemm`` and ``triton_gemm_splitk``."""
+    from _timing import Row
+
+    def build(M, N, K, sk):
+        def make():
+            import gemm
+
+            a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+            b = torch.randn(K, N, device="cuda", dtype=torch.float16)
+            return {"torch_fp16": lambda: a @ b, "unsplit": lambda: gemm.triton_gemm(a, b),
+                    f"split{sk}": lambda: triton_gemm_splitk(a, b, split_k=sk)}
+        return make
+
+    shapes = ((512, 512, 8192, 4, "tall-skinny"), (512, 512, 16384, 8, "tall-skinny"),
+              (1024, 1024, 4096, 4, "square"), (4096, 4096, 4096, 4, "square"))
+    return [Row(f"M={M},N={N},K={K}", build(M, N, K, sk), 2.0 * M * N * K, note)
+            for M, N, K, sk, note in shapes]
+
+
+def check_correctness() -> bool:
+    """Run and print the module's self-check (see ``_harness_checks``)."""
+    from _timing import run_checks
+
+    return run_checks("gemm_splitk", _harness_checks())
 
 
 def bench() -> None:
-    """The reference's benchmark table (gemm_splitk.py:94-113): GFLOPS of the fp16 matmul
-    (hipBLASLt through torch), the unsplit GEMM (gemm.triton_gemm) and split-K."""
-    import gemm
-    from _timing import do_bench
+    """Time and print the module's benchmark rows (see ``_harness_rows``)."""
+    from _timing import run_rows
 
-    print(f"{'shape (M,N,K)':>16} {'hipBLASLt':>10} {'unsplit':>10} {'split-K':>10}  note")
-    print("-" * 64)
-    cases = [
-        (512, 512, 8192, 4, "tall-skinny"),
-        (512, 512, 16384, 8, "tall-skinny"),
-        (1024, 1024, 4096, 4, "square"),
-        (4096, 4096, 4096, 4, "square"),
-    ]
-    for M, N, K, sk, note in cases:
-        a = torch.randn(M, K, device="cuda", dtype=torch.float16)
-        b = torch.randn(K, N, device="cuda", dtype=torch.float16)
-        flops = 2 * M * N * K / 1e9
-        ms_blas = do_bench(lambda: a @ b)
-        ms_auto = do_bench(lambda: gemm.triton_gemm(a, b))
-        ms_split = do_bench(lambda: triton_gemm_splitk(a, b, split_k=sk))
-        fmt = lambda ms: f"{flops / (ms / 1e3):>7.0f} G"
-        print(f"{(M, N, K)!s:>16} {fmt(ms_blas):>10} {fmt(ms_auto):>10} {fmt(ms_split):>10}  {note}")
+    run_rows("gemm_splitk", _harness_rows())
 
 
 if __name__ == "__main__":
-    from _timing import banner
+    import sys
 
-    print(banner())
-    print("=== correctness ===")
-    check_correctness()
-    print("=== benchmark (GFLOPS) ===")
-    bench()
+    from _timing import main
+
+    sys.exit(main("gemm_splitk", _harness_checks(), _harness_rows()))

@@ -34,7 +34,11 @@ kernels stream in long runs (``pk_w4a16_gemm_tiled``). ``codes()`` / ``set_codes
 state dict and the file format use ``pack_int4_n`` order either way.
 
 The output has the input's dtype (fp16, bf16 or fp32, as ``nn.Linear``); other inputs are
-computed in fp16. Weights need ``out % 8 == 0`` (whole int32 words) and ``in % 32 == 0``
+computed in fp16. A finite bf16 / fp32 activation whose fp16 form would be infinite (beyond
+65504, after the per-input scales for that scheme) raises ``ValueError``: one device reduction
+and synchronisation per call on such inputs, skipped under graph capture and when
+``QuantLinear.range_check`` is False (then such values become infinities, as torch's own fp16
+cast makes them). Weights need ``out % 8 == 0`` (whole int32 words) and ``in % 32 == 0``
 (the kernel's K), group layers ``in % group_size == 0``.
 """
 
@@ -58,6 +62,9 @@ _OUT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 class QuantLinear(nn.Module):
     """``y = x @ W^T + b`` with ``W`` stored as int4 codes and scales (see the module doc)."""
+
+    # bf16 / fp32 inputs: raise ValueError when the fp16 cast would overflow (see the module doc)
+    range_check: bool = True
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True,
                  group_size: int = 128, device: torch.device | str | None = None,
@@ -186,10 +193,14 @@ class QuantLinear(nn.Module):
             # x * s / max s in fp16 (the input cast in the same pass), then max s in the epilogue
             s = self.scales if self.scales.dtype == torch.float32 else self.scales.float()
             xp = _pk.w4a16_prep_activations(x2, s, 1.0 / self._smax)
+            if self.range_check:
+                _pk.check_fp16_range(x2, "QuantLinear", xp)
             y = _pk.w4a16_gemm(xp, self.qweight, None, 0, self._smax, out_dtype, bias=self.bias,
                                tiled=self.tiled)
         else:
             xp = x2 if x2.dtype == torch.float16 else _pk.w4a16_prep_activations(x2, None, 1.0)
+            if self.range_check and xp is not x2:
+                _pk.check_fp16_range(x2, "QuantLinear", xp)
             s = self.scales if self.scales.dtype == torch.float16 else self.scales.half()
             y = _pk.w4a16_gemm(xp, self.qweight, s, self.group_size, 1.0, out_dtype,
                                bias=self.bias, tiled=self.tiled)
@@ -208,7 +219,9 @@ class QuantLinear(nn.Module):
     def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
         super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
         if self.tiled and prefix + "qweight" in state_dict:
-            self.qweight.copy_(_pk.tile_weights(self.qweight.clone()))
+            # A new tensor, never an in-place rewrite: under load_state_dict(assign=True) the
+            # buffer is the caller's own state-dict tensor, which must keep pack_int4_n order.
+            self.qweight = _pk.tile_weights(self.qweight)
         self._refresh()
 
     def extra_repr(self) -> str:

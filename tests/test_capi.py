@@ -184,3 +184,20 @@ def test_product_modules_never_import_the_oracle():
     for f in (ROOT / "pico-kernels_amd").glob("*.py"):
         src = f.read_text()
         assert not re.search(r"^\s*(import|from)\s+oracle\b", src, re.M), f.name
+
+
+def test_tiled_rows_per_call():
+    """Block-layout calls whose activations span 2 GiB or more (the packed-B GEMM's 32-bit
+    buffer offsets) run as equal chunks of whole 128-row multiples below that limit."""
+    f = _pk.lib().pk_w4a16_tiled_rows_per_call
+    assert f(2048, 4096) == 2048
+    assert f(262143, 4096) == 262143                    # 2 GiB - 8 KB: one call
+    for M, lda in ((262144, 4096), (75000, 14336), (131072, 14336), (1 << 20, 4096),
+                   (300000, 8192)):
+        rows = f(M, lda)
+        chunks = -(-M // rows)
+        assert rows % 128 == 0 and rows * lda * 2 < 2 ** 31, (M, lda, rows)
+        assert (chunks - 1) * rows < M <= chunks * rows
+        assert rows - M / chunks < 128                   # equal chunks, no small tail call
+    assert f(75000, 14336) == 37504
+    assert f(100, 1 << 24) == 0                          # even 128 rows exceed 2 GiB

@@ -66,8 +66,12 @@ def test_gptq_golden(golden, cuda):
             continue
         out = gptq_layer(W.to(cuda), X.to(cuda), case["bits"], act_order=case["act_order"],
                          group_size=case["group_size"])
-        close = np.isclose(out.cpu().numpy(), arrays[name + "_out"], atol=1e-4, rtol=1e-4)
-        assert close.mean() > 0.99, f"{name}: {(~close).sum()} of {close.size} differ"
+        got, ref = out.cpu().numpy(), arrays[name + "_out"]
+        close = np.isclose(got, ref, atol=1e-4, rtol=1e-4)
+        # Measured on MI355X: no element outside the tolerance in any case (max |diff|
+        # 1.7e-6: fp32 linear algebra in another library, no code flipped across a tie).
+        assert (~close).sum() == 0, f"{name}: {(~close).sum()} of {close.size} differ"
+        assert np.abs(got - ref).max() <= 1e-5, name
 
 
 def test_gptq_act_order_is_permutation_consistent(cuda):

@@ -138,3 +138,27 @@ def test_tiled_repeatable(cuda):
     first = _pk.w4a16_gemm(a, qt, sc, 128, 1.0, torch.float16, tiled=True)
     for _ in range(3):
         assert torch.equal(first, _pk.w4a16_gemm(a, qt, sc, 128, 1.0, torch.float16, tiled=True))
+
+
+def test_tiled_rows_beyond_32bit_offsets(cuda):
+    """A block-layout call whose activations span more than 2 GiB (a ~75k-token prefill on the
+    14336-deep down projection) runs in equal row chunks: each chunk bitwise the call on those
+    rows alone, sample rows against the oracle."""
+    M, K, N = 75000, 14336, 256
+    assert M * K * 2 >= 2 ** 31
+    g = torch.Generator(device=cuda).manual_seed(7)
+    a = torch.randn(M, K, device=cuda, dtype=torch.float16, generator=g)
+    w = (torch.randn(K, N, generator=_gen(8)) * 0.02).half()
+    codes, _, s16 = oracle.rtn_group_codes(w.numpy(), 4, 128)
+    qw = torch.from_numpy(oracle.pack_int4_n(codes).view(np.int32).copy()).to(cuda)
+    sc = torch.from_numpy(s16).to(cuda)
+    qt = _pk.tile_weights(qw)
+    y = _pk.w4a16_gemm(a, qt, sc, 128, 1.0, torch.float16, tiled=True)
+    rows = _pk.lib().pk_w4a16_tiled_rows_per_call(M, K)
+    assert 0 < rows < M
+    for r0 in range(0, M, rows):
+        part = _pk.w4a16_gemm(a[r0:r0 + rows], qt, sc, 128, 1.0, torch.float16, tiled=True)
+        assert torch.equal(y[r0:r0 + rows], part), r0
+    pick = [0, 1, rows - 1, rows, M - 1]
+    ref = oracle.w4a16_ref(a[pick].cpu().numpy(), codes, s16, 128)
+    assert oracle.rel_fro(y[pick].float().cpu().numpy(), ref) <= 1e-3
