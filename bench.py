@@ -3,10 +3,12 @@
 
 Headline workload: W4A16 decode GEMV, M=1, K=4096, N=11008, int4 group
 128 with fp16 scales, fp16 activations N(0,1), weights N(0, 0.02), seeded CPU generator.
-A "step" is one ``w4a16_gemm`` call over one activation row, on the weights in the layout
-``QuantLinear`` keeps in memory (``pk_w4a16_gemm_tiled``: the same codes in contiguous 16 KB
-blocks of 128 rows x 256 columns); the same call on ``pack_int4_n``'s row layout
-(``pk_w4a16_gemm``) is timed beside it. ``value`` is the whole-op HBM
+A "step" is one call over one activation row on the copy of the weights ``QuantLinear`` runs
+decode (at most ``DECODE_MAX_ROWS`` rows) on: the strip layout (``pk_w4a16_gemm_strips``: each
+16-column strip's K rows contiguous, one workgroup per strip over the whole of K, one launch).
+The same call on ``QuantLinear``'s block layout (``pk_w4a16_gemm_tiled``, 128 x 256 blocks:
+the split-K GEMV, slices added in L2) and on ``pack_int4_n``'s row layout (``pk_w4a16_gemm``)
+is timed beside it. ``value`` is the whole-op HBM
 throughput (algorithmic bytes / step time), inputs resident in HBM. 40 distinct copies of the
 packed weights and scales (932 MB, more than twice the 256 MB Infinity Cache) are rotated:
 the W warm-up calls read copies 0..W-1, the timed graph starts at copy W and holds
@@ -16,10 +18,8 @@ warm-up has just read.
 Timing: W eager warm-up steps, then max(K, 80) steps captured in one HIP graph; untimed
 replays for 250 ms (the clocks settle under load), then 3 replays between HIP events on the
 graph's stream (device synchronisation around each replay); the best replay gives
-``ms_per_step``. Every timed line gets the same settling replays. On MI355X the GEMV's split-K slices add up in L2 inside
-the one kernel, so the op is the dominant kernel and the roofline fraction uses its time;
-where a second (reduce) launch is needed, the slice kernel is timed on its own through
-``pk_w4a16_gemm_partials``.
+``ms_per_step``. Every timed line gets the same settling replays. The strip GEMV is one kernel
+launch, so the op is the dominant kernel and the roofline fraction uses its time.
 
 Correctness comes first: before any timing each GPU line checks its own output against the
 reference's test-path expression in fp32 torch on the GPU (unpack, multiply by the repeated
@@ -59,7 +59,8 @@ N_ROTATE = 40
 # (both layouts run the same kernels).
 ROW_LAYOUT = True
 WARM_MS = 250.0  # untimed graph replays before each timed measurement (GraphTimer.run)
-KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v3_f16_kernel", 3: "w4a16_skinny_kernel"}
+KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v3_f16_kernel", 3: "w4a16_skinny_kernel",
+                4: "w4a16_tr4_kernel", "strips": "w4a16_strip_kernel"}
 
 
 def _gen(seed: int):
@@ -161,6 +162,13 @@ def tiled_copies(qws: list) -> list:
     return [_pk.tile_weights(q) for q in qws]
 
 
+def strip_copies(qws: list, scs: list) -> tuple[list, list]:
+    """The weight and scale copies in QuantLinear's decode layout (16-column strips)."""
+    import _pk
+
+    return [_pk.strip_weights(q) for q in qws], [_pk.strip_scales(s) for s in scs]
+
+
 def unpack_codes(qw):
     """``(K, N//8)`` int32 words holding pack_int4_n bytes -> ``(K, N)`` int8 codes in [-8, 7],
     with plain torch ops (the reference's unpack, tests/test_gemm_int4.py:36-41)."""
@@ -239,12 +247,17 @@ def bench_gemv(args, dev) -> dict:
     M, K, N = 1, 4096, 11008
     a, w, qws, scs = gemv_inputs(M, K, N, N_ROTATE, dev)
     qts = tiled_copies(qws)
+    qss, sss = strip_copies(qws, scs)
     ag = a.to(dev)
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     nbytes = w4a16_bytes(M, K, N)
     kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
 
-    def step(i):  # QuantLinear's layout: blocks
+    def step(i):  # QuantLinear's decode layout: strips
+        _pk.w4a16_gemm_strips(ag, qss[i % N_ROTATE], sss[i % N_ROTATE], 128, 1.0,
+                              torch.float16, out=out)
+
+    def step_blocks(i):  # QuantLinear's layout above DECODE_MAX_ROWS rows: blocks
         _pk.w4a16_gemm(ag, qts[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
                        split_k=0, out=out, tiled=True)
 
@@ -252,41 +265,30 @@ def bench_gemv(args, dev) -> dict:
         _pk.w4a16_gemm(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
                        split_k=0, out=out)
 
-    def once():
-        step(0)
-        return out
+    def once(fn):
+        def call():
+            fn(0)
+            return out
+        return call
 
-    def once_rows():
-        step_rows(0)
-        return out
-
-    check = check_w4a16(once, ag, qws[0], scs[0])
-    y_tiles = out.clone()
-    check_rows = check_w4a16(once_rows, ag, qws[0], scs[0])
-    check["bitwise_equal_to_row_layout"] = bool(torch.equal(y_tiles, out))
-    if not check["bitwise_equal_to_row_layout"]:
+    check = check_w4a16(once(step), ag, qws[0], scs[0])
+    check_blocks = check_w4a16(once(step_blocks), ag, qws[0], scs[0])
+    y_blocks = out.clone()
+    check_rows = check_w4a16(once(step_rows), ag, qws[0], scs[0])
+    check_blocks["bitwise_equal_to_row_layout"] = bool(torch.equal(y_blocks, out))
+    if not check_blocks["bitwise_equal_to_row_layout"]:
         raise RuntimeError("W4A16 GEMV: block and row layouts disagree")
     timed = max(args.steps, 2 * N_ROTATE)
     ms = GraphTimer(step, timed, args.warmup).run(reps=3)
+    ms_blocks = GraphTimer(step_blocks, timed, args.warmup).run(reps=3) if ROW_LAYOUT else None
     ms_rows = GraphTimer(step_rows, timed, args.warmup).run(reps=3) if ROW_LAYOUT else None
-    launches = _pk.w4a16_launches(M, N, K, 128, 0)
 
-    # The dominant kernel's average launch: back-to-back launches in one graph, HIP events
-    # around the replay on the launch stream (agrees with rocprof's kernel-trace average);
-    # single launches bracketed by their own events read ~1.5 us longer (event overhead).
-    # With the slices added in L2 the op is that one kernel; otherwise time the slice kernel
-    # alone (it writes the fp32 partials that a second launch adds).
-    if launches == 1:
-        ms_kernel = ms
-        ms_kernel_events = per_launch_ms(step, min(timed, 500))
-    else:
-        parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
-
-        def step_partials(i):
-            _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
-
-        ms_kernel = GraphTimer(step_partials, timed, args.warmup).run(reps=3)
-        ms_kernel_events = per_launch_ms(step_partials, min(timed, 500))
+    # The op is one launch of the strip kernel: the graph's per-step time is that kernel's
+    # average launch duration (HIP events around the replay on the launch stream; agrees with
+    # rocprof's kernel-trace average). Single launches bracketed by their own events read
+    # ~1.5 us longer (event overhead) and are reported beside it.
+    ms_kernel = ms
+    ms_kernel_events = per_launch_ms(step, min(timed, 500))
 
     sweep = {}
     for s in ((1, 2, 4, 8, 16) if getattr(args, "split_sweep", True) else ()):
@@ -294,21 +296,37 @@ def bench_gemv(args, dev) -> dict:
             _pk.w4a16_gemm(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
                            split_k=s, out=out)
 
-        def once_s(s=s):
-            step_s(0)
-            return out
-
-        check_w4a16(once_s, ag, qws[0], scs[0])
+        check_w4a16(once(step_s), ag, qws[0], scs[0])
         ms_s = GraphTimer(step_s, max(min(args.steps, 400), 2 * N_ROTATE), 2).run(reps=3)
         sweep[str(s)] = round(nbytes / (ms_s * 1e-3) / 1e9, 1)
     return {
-        "M": M, "K": K, "N": N, "split": split, "kernel_id": kid, "launches": launches,
-        "bytes": nbytes, "steps_timed": timed, "check": check, "check_rows": check_rows,
-        "ms_per_step": ms, "ms_rows": ms_rows, "ms_kernel": ms_kernel,
-        "ms_kernel_events": ms_kernel_events,
-        "split_sweep_GBs": sweep, "host": host_overhead(step),
+        "M": M, "K": K, "N": N, "split": 1, "kernel_id": "strips", "launches": 1,
+        "blocks_layout_plan": {"kernel_id": kid, "split": split,
+                               "launches": _pk.w4a16_launches(M, N, K, 128, 0)},
+        "bytes": nbytes, "steps_timed": timed, "check": check, "check_blocks": check_blocks,
+        "check_rows": check_rows, "ms_per_step": ms, "ms_blocks": ms_blocks, "ms_rows": ms_rows,
+        "ms_kernel": ms_kernel, "ms_kernel_events": ms_kernel_events,
+        "split_sweep_GBs": sweep, "host": host_times(ag, qws[0], scs[0], qss[0], sss[0], out, step),
         "inputs": (ag, qws[0], scs[0]),
     }
+
+
+def host_times(ag, qw, sc, qs, ss, out, step) -> dict:
+    """Eager host cost of one decode call at M = 1 (see host_overhead), three ways: the generic
+    binding (``_pk.w4a16_gemm_strips``, the timed step), the prepared call QuantLinear keeps per
+    layer (``_pk.PreparedStrips``, output given), and ``QuantLinear.forward`` itself (its output
+    allocated per call)."""
+    import _pk
+    import quant_linear
+
+    K, N = qw.shape[0], qw.shape[1] * 8
+    call = _pk.PreparedStrips(qs, ss, 128, 1.0, out.dtype)
+    layer = quant_linear.QuantLinear(K, N, bias=False, group_size=128, device=ag.device)
+    layer.set_codes(qw)
+    layer.scales.copy_(sc)
+    layer._refresh()
+    return {"binding": host_overhead(step), "prepared_call": host_overhead(lambda i: call(ag, out)),
+            "quant_linear_forward": host_overhead(lambda i: layer(ag))}
 
 
 def bench_prefill(dev, iters: int = 50, M: int = 2048) -> dict:
@@ -415,6 +433,7 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
 
     import _pk
     import gemm_int4
+    import quant_linear
 
     rows = []
     for name, K, N in SWEEP_LAYERS:
@@ -425,13 +444,19 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
         qws = [qw] + [qw.clone() for _ in range(nrot - 1)]
         qts = tiled_copies(qws)
         scs = [sc] + [sc.clone() for _ in range(nrot - 1)]
+        qss, sss = strip_copies(qws, scs)
         for M in (1, 8, 32, 128):
             a = torch.randn(M, K, generator=_gen(7)).half().to(dev)
             out = torch.empty((M, N), dtype=torch.float16, device=dev)
+            strips = M <= quant_linear.DECODE_MAX_ROWS
 
-            def step(i):  # QuantLinear's layout: blocks
-                _pk.w4a16_gemm(a, qts[i % nrot], scs[i % nrot], 128, 1.0, torch.float16,
-                               out=out, tiled=True)
+            def step(i):  # what QuantLinear runs: the strip copy for decode rows, else blocks
+                if strips:
+                    _pk.w4a16_gemm_strips(a, qss[i % nrot], sss[i % nrot], 128, 1.0,
+                                          torch.float16, out=out)
+                else:
+                    _pk.w4a16_gemm(a, qts[i % nrot], scs[i % nrot], 128, 1.0, torch.float16,
+                                   out=out, tiled=True)
 
             def step_rows(i):
                 _pk.w4a16_gemm(a, qws[i % nrot], scs[i % nrot], 128, 1.0, torch.float16,
@@ -455,10 +480,12 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
                          "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
                          "bound": "hbm" if t_hbm >= t_mfma else "mfma",
                          "frac": round(max(t_hbm, t_mfma) / (ms * 1e-3), 4),
-                         "kernel_id": kid, "split": split,
-                         "launches": _pk.w4a16_launches(M, N, K, 128, 0), "copies": nrot,
+                         "layout": "strips" if strips else "blocks",
+                         "kernel_id": "strips" if strips else kid, "split": 1 if strips else split,
+                         "launches": 1 if strips else _pk.w4a16_launches(M, N, K, 128, 0),
+                         "copies": nrot,
                          "rel_fro": check["rel_fro_vs_fp32_expr"]})
-        del qws, qts, scs
+        del qws, qts, scs, qss, sss
     return rows
 
 
@@ -695,29 +722,21 @@ COPY_PROBE_BYTES = 256 << 20
 
 
 def traffic_probe(dev) -> int:
-    """Short run for the rocprofv3 --pmc passes: 50 launches of the GEMV's dominant kernel
-    on rotating weights in blocks (the whole op when its slices add up in L2), then 50
-    launches of the slices alone writing their partials (pk_w4a16_gemm_partials on the row
-    layout: the same loads and partial stores, no handoff reads), then 10 device copies of
-    COPY_PROBE_BYTES (the calibration kernel: it must read and write exactly that many
-    bytes)."""
+    """Short run for the rocprofv3 --pmc passes: 50 launches of the headline's kernel (the
+    strip GEMV, the whole op) on rotating weights, then 10 device copies of COPY_PROBE_BYTES
+    (the calibration kernel: it must read and write exactly that many bytes)."""
     import torch
 
     import _pk
 
     M, K, N = 1, 4096, 11008
     a, w, qws, scs = gemv_inputs(M, K, N, N_ROTATE, dev)
-    qts = tiled_copies(qws)
+    qss, sss = strip_copies(qws, scs)
     ag = a.to(dev)
-    kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
-    if _pk.w4a16_launches(M, N, K, 128, 0) == 1:
-        out = torch.empty((M, N), dtype=torch.float16, device=dev)
-        for i in range(50):  # the headline's call: blocks
-            _pk.w4a16_gemm(ag, qts[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
-                           out=out, tiled=True)
-    parts = torch.empty((split, M, N), dtype=torch.float32, device=dev)
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
     for i in range(50):
-        _pk.w4a16_gemm_partials(ag, qws[i % N_ROTATE], scs[i % N_ROTATE], 128, 0, parts)
+        _pk.w4a16_gemm_strips(ag, qss[i % N_ROTATE], sss[i % N_ROTATE], 128, 1.0,
+                              torch.float16, out=out)
     torch.cuda.synchronize()
     src = torch.empty(COPY_PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
@@ -725,7 +744,7 @@ def traffic_probe(dev) -> int:
     for _ in range(10):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"traffic probe done: split={split} copy_bytes={COPY_PROBE_BYTES}", flush=True)
+    print(f"traffic probe done: launches=50 copy_bytes={COPY_PROBE_BYTES}", flush=True)
     return 0
 
 
@@ -950,16 +969,19 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int4 weights (group 128, fp16 scales) x fp16 activations, fp32 accumulate",
         "data": "synthetic: seeded CPU generator, A ~ N(0,1) fp16, W ~ N(0,0.02) int4-quantized "
-                "(group 128), the codes in QuantLinear's in-memory layout (128x256 blocks"
-                + (f"; the row layout of pack_int4_n: {g['bytes'] / (g['ms_rows'] * 1e-3) / 1e9:.1f} GB/s"
-                   if g["ms_rows"] else "") + "); "
+                "(group 128), the codes in QuantLinear's decode layout (16-column strips, each "
+                "strip's K rows contiguous); "
                 f"{N_ROTATE} copies of the packed weights and scales rotated "
                 f"({N_ROTATE * g['bytes'] / 1e6:.0f} MB > 2x the 256 MB Infinity Cache): warm-up "
                 f"reads copies 0..{args.warmup - 1}, the timed graph {g['steps_timed']} calls "
                 f"from copy {max(args.warmup, 1) % N_ROTATE} on, best of 3 replays",
         "config": {"workload": "w4a16_decode_gemv", "M": g["M"], "K": g["K"], "N": g["N"],
-                   "group_size": 128, "split_k": g["split"], "out_dtype": "fp16",
-                   "weights": "128x256 blocks (QuantLinear's layout, pk_w4a16_gemm_tiled)",
+                   "group_size": 128, "split_k": 1, "out_dtype": "fp16",
+                   "weights": "16-column strips (QuantLinear's decode copy, pk_w4a16_gemm_strips): "
+                              "one workgroup per strip over the whole of K, one launch",
+                   "blocks_layout_GBs": (round(g["bytes"] / (g["ms_blocks"] * 1e-3) / 1e9, 1)
+                                         if g["ms_blocks"] else None),
+                   "blocks_layout_plan": g["blocks_layout_plan"],
                    "row_layout_GBs": (round(g["bytes"] / (g["ms_rows"] * 1e-3) / 1e9, 1)
                                       if g["ms_rows"] else None),
                    "split_k_sweep_GBs": g["split_sweep_GBs"],
@@ -971,9 +993,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": KERNEL_NAMES.get(g["kernel_id"], "?") + (
-                         " (split-K slices added in L2: the whole op)" if g["launches"] == 1
-                         else " (split-K slices)"),
+                     "kernel": KERNEL_NAMES[g["kernel_id"]] + " (one launch: the whole op)",
                      "kernel_us": round(g["ms_kernel"] * 1e3, 3),
                      "kernel_us_single_launch_events": round(g["ms_kernel_events"] * 1e3, 3),
                      "bytes_per_launch": g["bytes"]},

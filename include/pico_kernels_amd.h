@@ -177,6 +177,29 @@ int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* qtiled, cons
                         void* c, int c_dtype, int64_t ldc, int M, int N, int K, int split_k,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* W4A16 decode matmul (1 <= M <= 8) on weights in the strip layout: C = tensor_scale * A @
+ * dequant(q, S) (+ bias), the arithmetic of pk_w4a16_gemm_bias (gemm_int4.py:21-55, 75-92 with
+ * group scales), in ONE launch with no split-K partials: one workgroup per 16-column strip
+ * adds the whole of K in LDS, in a fixed order (bitwise reproducible). The strip layout is a
+ * byte permutation of pack_int4_n's (K, N/2) bytes (gemm_int4.py:65-72): byte (k, c), with
+ * k = 128b + 32rs + 8g + e and c = 8s + 2cps + h (b block, rs, g, cps in 0..3, e in 0..7,
+ * h in 0..1), sits at byte ((((s * K/128 + b) * 4 + g) * 4 + rs) * 4 + cps) * 16 + 8h + e, both
+ * nibbles XOR 8 (the code biased to 0..15): each strip's K rows contiguous, in 1 KB blocks of
+ * 128 rows. Scales (group mode, sstrips non-null):
+ * the (K/G, N) fp16 group scales reordered as (N/16, K/G, 16). Requires N % 16 == 0,
+ * K % 128 == 0, G a multiple of 32 dividing K that divides 128 or is a multiple of it,
+ * 16-byte aligned A rows and weights, 8-byte aligned scales; fp32/fp16/bf16 output and bias.
+ * Replaces gemm_int4.int4_gemm (gemm_int4.py:75-92) at M = 1 and the split-K GEMV
+ * (gemm_splitk.py:26-80) for decode: the reference has no weight layout other than
+ * pack_int4_n's. */
+int pk_w4a16_gemm_strips(const void* a, int64_t lda, const uint8_t* qstrips, const void* sstrips,
+                         int group_size, float tensor_scale, const void* bias, int bias_dtype,
+                         void* c, int c_dtype, int64_t ldc, int M, int N, int K, void* stream);
+
+/* Fix the strip GEMV's 1 KB blocks per wave (2, 4 or 8) for later calls, or 0 for the
+ * automatic choice; for measurements. No counterpart in the reference. */
+int pk_w4a16_strips_config(int blocks_per_wave);
+
 /* Rows per kernel call of pk_w4a16_gemm_tiled for M activation rows of stride lda elements:
  * M itself while the activations span less than 2 GiB (M * lda * 2 bytes); beyond that the
  * call runs equal chunks of this many rows (a multiple of 128), since the kernels that read

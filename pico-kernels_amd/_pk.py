@@ -59,6 +59,9 @@ _SIGNATURES = {
                                    _i32, _i32, _i32, _i32, _vp, _sz, _vp]),
     "pk_w4a16_noalloc_scratch_bytes": (_sz, []),
     "pk_w4a16_tiled_rows_per_call": (_i64, [_i64, _i64]),
+    "pk_w4a16_gemm_strips": (_i32, [_vp, _i64, _vp, _vp, _i32, _f32, _vp, _i32, _vp, _i32, _i64,
+                                    _i32, _i32, _i32, _vp]),
+    "pk_w4a16_strips_config": (_i32, [_i32]),
     "pk_w4a16_skinny_layout": (_i32, [_i32, _i32]),
     "pk_w4a16_prep_activations": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _vp]),
     "pk_w4a16_gemm_noalloc": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
@@ -340,6 +343,122 @@ def untile_weights(qtiled: torch.Tensor) -> torch.Tensor:
         raise ValueError(f"untile_weights: K = {K} must be a multiple of 128 and N = {8 * W} of 256")
     return (qtiled.contiguous().view(K // 128, W // 32, 128, 32).permute(0, 2, 1, 3)
             .contiguous().view(K, W))
+
+
+def strips_ok(K: int, N: int, group_size: int) -> bool:
+    """Shapes pk_w4a16_gemm_strips takes (group 0: per-tensor): N % 16 == 0, K % 128 == 0, and
+    a group of a multiple of 32 that divides 128 or is a multiple of it."""
+    if N % 16 or K % 128 or K < 128:
+        return False
+    g = int(group_size)
+    return g == 0 or (g % 32 == 0 and K % g == 0 and (128 % g == 0 or g % 128 == 0))
+
+
+def strip_weights(qweight: torch.Tensor) -> torch.Tensor:
+    """(K, N/8) int32 words in pack_int4_n order -> the same bytes in the strip layout of
+    pk_w4a16_gemm_strips (still shaped (K, N/8) int32): byte (k, c) of the (K, N/2) packed
+    bytes, k = 128b + 32rs + 8g + e and c = 8s + 2cps + h, moves to
+    ((((s * K/128 + b) * 4 + g) * 4 + rs) * 4 + cps) * 16 + 8h + e, with both nibbles XOR 8
+    (u = v + 8, the code biased to 0..15)."""
+    K, W = qweight.shape
+    N = 8 * W
+    if N % 16 or K % 128:
+        raise ValueError(f"strip_weights: K = {K} must be a multiple of 128 and N = {N} of 16")
+    b = qweight.contiguous().view(torch.uint8).view(K // 128, 4, 4, 8, N // 16, 4, 2)
+    return (b.permute(4, 0, 2, 1, 5, 6, 3).contiguous() ^ 0x88).view(torch.int32).view(K, W)
+
+
+def unstrip_weights(qstrips: torch.Tensor) -> torch.Tensor:
+    """Inverse of strip_weights: the strip layout -> (K, N/8) words in pack_int4_n order."""
+    K, W = qstrips.shape
+    N = 8 * W
+    if N % 16 or K % 128:
+        raise ValueError(f"unstrip_weights: K = {K} must be a multiple of 128 and N = {N} of 16")
+    b = qstrips.contiguous().view(torch.uint8).view(N // 16, K // 128, 4, 4, 4, 2, 8) ^ 0x88
+    return b.permute(1, 3, 2, 6, 0, 4, 5).contiguous().view(K, N // 2).view(torch.int32)
+
+
+def strip_scales(scales: torch.Tensor) -> torch.Tensor:
+    """(K/G, N) group scales -> (N/16, K/G, 16), each strip's scales contiguous (still
+    shaped (K/G, N))."""
+    KG, N = scales.shape
+    return scales.contiguous().view(KG, N // 16, 16).permute(1, 0, 2).contiguous().view(KG, N)
+
+
+def unstrip_scales(sstrips: torch.Tensor) -> torch.Tensor:
+    """Inverse of strip_scales."""
+    KG, N = sstrips.shape
+    return sstrips.contiguous().view(N // 16, KG, 16).permute(1, 0, 2).contiguous().view(KG, N)
+
+
+def w4a16_gemm_strips(a: torch.Tensor, qstrips: torch.Tensor, sstrips: torch.Tensor | None,
+                      group_size: int, tensor_scale: float, out_dtype: torch.dtype,
+                      out: torch.Tensor | None = None,
+                      bias: torch.Tensor | None = None) -> torch.Tensor:
+    """out = tensor_scale * (a @ dequant(q, s)) (+ bias) for 1..8 rows of fp16 activations on
+    strip-layout codes and scales (strip_weights / strip_scales; pk_w4a16_gemm_strips)."""
+    M, K = a.shape
+    N = qstrips.shape[1] * 8
+    a = _rows_ok(a)
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    g = int(group_size) if sstrips is not None else 0
+    L = _lib if _lib is not None else lib()
+    rc = L.pk_w4a16_gemm_strips(
+        a.data_ptr(), a.stride(0), qstrips.data_ptr(),
+        None if sstrips is None else sstrips.data_ptr(), g, float(tensor_scale),
+        None if bias is None else bias.data_ptr(),
+        _TORCH_TO_PK[bias.dtype] if bias is not None else PK_F16, out.data_ptr(),
+        _TORCH_TO_PK[out.dtype], out.stride(0), M, N, K,
+        torch.cuda.current_stream(a.device).cuda_stream)
+    if rc != PK_OK:
+        _check(rc, "pk_w4a16_gemm_strips")
+    return out
+
+
+class PreparedStrips:
+    """``pk_w4a16_gemm_strips`` bound to one strip-layout weight copy: the weight, scale and bias
+    pointers, group, tensor scale and output dtype are converted once, so a call converts only
+    the activations, the output and the stream (what an eager decode loop pays per layer). The
+    tensors must stay alive and in place while the object is used (QuantLinear drops it when
+    its buffers move or change)."""
+
+    __slots__ = ("q", "s", "g", "scale", "b", "bd", "od", "out_dtype", "N", "K", "dev", "fn",
+                 "_keep")
+
+    def __init__(self, qstrips: torch.Tensor, sstrips: torch.Tensor | None, group_size: int,
+                 tensor_scale: float, out_dtype: torch.dtype, bias: torch.Tensor | None = None):
+        self.K, W = qstrips.shape
+        self.N = 8 * W
+        self.q = qstrips.data_ptr()
+        self.s = None if sstrips is None else sstrips.data_ptr()
+        self.g = int(group_size) if sstrips is not None else 0
+        self.scale = float(tensor_scale)
+        self.b = None if bias is None else bias.data_ptr()
+        self.bd = _TORCH_TO_PK[bias.dtype] if bias is not None else PK_F16
+        self.od = _TORCH_TO_PK[out_dtype]
+        self.out_dtype = out_dtype
+        self.dev = qstrips.device.index
+        self.fn = lib().pk_w4a16_gemm_strips
+        self._keep = (qstrips, sstrips, bias)
+
+    def __call__(self, a: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        M = a.shape[0]
+        if a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16:
+            a = _rows_ok(a)
+        if out is None:
+            out = torch.empty((M, self.N), dtype=self.out_dtype, device=a.device)
+        rc = self.fn(a.data_ptr(), a.stride(0), self.q, self.s, self.g, self.scale, self.b,
+                     self.bd, out.data_ptr(), self.od, out.stride(0), M, self.N, self.K,
+                     torch._C._cuda_getCurrentRawStream(self.dev))
+        if rc != PK_OK:
+            _check(rc, "pk_w4a16_gemm_strips")
+        return out
+
+
+def w4a16_strips_config(blocks_per_wave: int) -> None:
+    """Fix the strip GEMV's 1 KB blocks per wave (2, 4 or 8; 0: automatic)."""
+    _check(lib().pk_w4a16_strips_config(int(blocks_per_wave)), "pk_w4a16_strips_config")
 
 
 def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | None,

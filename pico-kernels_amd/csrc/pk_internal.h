@@ -73,6 +73,14 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
 bool gemv_tiled_ok(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
                    int64_t ldq, const void* scales, int group, int M, int N, int K);
 
+// W4A16 decode GEMV on strip-layout weights (w4a16_strips.hip): 1 <= M <= 8, one workgroup
+// per 16-column strip over the whole of K, one launch.
+bool strips_shape_ok(int M, int N, int K, int group, bool has_gs);
+int strips_launch(const void* a, int64_t lda, const uint8_t* qs, const void* ss, int group,
+                  OutEpi epi, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                  hipStream_t stream);
+bool strips_config_set(int blocks_per_wave);
+
 // W4A16 for kSkinnyMinM <= M <= kSkinnyMaxM (w4a16_skinny.hip): weights to registers, MFMA
 // per 16 activation rows, LDS reduction over the workgroup's waves, split-K partials.
 constexpr int kSkinnyMinM = 5;

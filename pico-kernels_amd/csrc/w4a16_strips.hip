@@ -1,0 +1,402 @@
+// W4A16 decode GEMV (1 <= M <= 8) on strip-layout weights: one workgroup per 16-column strip
+// sums the whole of K itself, so a call is one launch with no split-K partials and no
+// handoff between workgroups.
+//
+// Computes C[m, n] = tensor_scale * sum_k A[m, k] * q[k, n] * S[k / G, n] (+ bias[n]), the
+// arithmetic of gemm_int4.int4_gemm_kernel (gemm_int4.py:21-55) with group scales.
+//
+// Strip layout (pk_w4a16_gemm_strips; a byte permutation of pack_int4_n's (K, N/2) bytes,
+// gemm_int4.py:65-72, whose byte (k, c) holds columns 2c (low nibble) and 2c+1 (high)):
+//   strip s = columns 16s .. 16s+15; its K rows are contiguous: 1 KB blocks b = rows
+//   128b .. 128b+127 at byte (s * K/128 + b) * 1024. Inside a block, 16-byte chunk
+//   L = 16g + 4rs + cps (g, rs, cps in 0..3) holds rows 32rs + 8g + e (e = 0..7) of the
+//   column pairs 2cps (bytes 0..7, in row order e) and 2cps+1 (bytes 8..15), every nibble
+//   stored as u = v + 8 (0..15, the two's-complement code v XOR 8).
+//   Scales (group mode) are (N/16, K/G, 16) fp16: strip s's scales of group i at
+//   (s * K/G + i) * 16.
+// So lane L of a wave loads chunk L of a block: every wave load instruction reads 1 KB of
+// contiguous weights, and a workgroup streams its strip's K/128 KB in one run.
+//
+// Products on v_mfma_f32_16x16x32_f16 (D = A x B, A 16x32, B 32x16): lane L supplies
+// A[L % 16][8(L / 16) + e] and B[8(L / 16) + e][L % 16] and holds D[4(L / 16) + r][L % 16],
+// r = 0..3. With lane L's chunk as its B operand (8 rows of one column pair), B column j
+// = L % 16 carries column pair 2cps(j)+h of row set rs(j) = j / 4, and A row i carries
+// activation row i % 4 at row set i / 4 (lane L loads the 8 activations of its own chunk's
+// rows), so D[4rs + m][4rs + cps] is the sum over row set rs (32 rows) of activation row m
+// times the column pair: it sits in register m of lane 20rs + cps. Rows 4..7 take a second
+// MFMA set (activation rows i % 4 + 4).
+//
+// Dequantisation is exact, as in the split-K GEMV: a byte permute puts the byte of rows
+// (e, e+1) in the low bytes of the two halves of a dword, i.e. fp16 subnormals
+// (u_lo + 16 u_hi) * 2^-24 ("raw"), and masking with 0x000F000F leaves u_lo * 2^-24 ("lo").
+// With O8 = the MFMA of the constant -8 * 2^-24 and O136 = 17 O8 as accumulator inputs,
+//   lo  = MFMA(A, lo,  O8)   = 2^-24 * sum x * v_lo,
+//   raw = MFMA(A, raw, O136), raw - lo = 2^-20 * sum x * v_hi
+// (MFMA keeps fp16 subnormal inputs; products are exact). Each block's sums are scaled by
+// their group scale in fp32 and added per lane in block order; the workgroup then adds its
+// row sets and waves through LDS in a fixed order, so results are bitwise reproducible.
+#include "pk_internal.h"
+
+namespace pk {
+
+constexpr int kStripCols = 16;       // columns per strip = per workgroup
+constexpr int kStripBlockRows = 128;  // rows per 1 KB block
+constexpr int kStripMaxWaves = 16;
+
+struct StripParams {
+  const pk_half* a;
+  int64_t lda;
+  const uint8_t* qs;     // strip-layout codes
+  const pk_half* ss;     // strip-layout scales, or null (per-tensor mode)
+  int group;             // G (multiple of 32) with scales
+  int group_shift;       // log2(G) when G is a power of two, else -1
+  OutEpi epi;
+  void* c;
+  int c_dtype;
+  int64_t ldc;
+  int M, N, K;
+  int kb;     // K / 128 blocks per strip
+  int nw;     // waves per workgroup
+  int iters;  // rounds of U blocks per wave
+  int spx;    // strips per XCD: ceil(N / 16 / 8)
+};
+
+// Group index of the 32-row row set at row `r0` (r0 % 32 == 0).
+__device__ __forceinline__ int strip_group(const StripParams& p, int r0) {
+  return p.group_shift >= 0 ? (r0 >> p.group_shift) : r0 / p.group;
+}
+
+#define PK_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// LDS staging (ALDS) is per wave: a wave's U blocks of activations (U x 128 columns of each
+// of the M rows, as M runs of 256 U bytes) and their U group-scale rows (32 bytes each), in a
+// region of its own, so no wave waits for another.
+__host__ __device__ __forceinline__ int strip_wave_act_lds(int M, int U) { return (int)cdiv((int64_t)M * U * 256, 1024) * 1024; }
+constexpr int kStripWaveScLds = 1024;
+__host__ __device__ __forceinline__ int strip_wave_lds(int M, int U, bool gs) {
+  return strip_wave_act_lds(M, U) + (gs ? kStripWaveScLds : 0);
+}
+
+// 16 bytes per lane, global -> LDS: lane L writes lds + 16 L.
+__device__ __forceinline__ void strip_dma16(__amdgpu_buffer_rsrc_t r, char* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, PK_LDS_PTR(lds), 16, voff, 0, 0, 0);
+}
+
+// MT: activation rows the kernel carries (1, 2, 4 or 8); U: 1 KB blocks per wave per round.
+// ALDS: each wave DMAs its round's activations and scales into its own LDS region ahead of
+// its weight loads and reads them from there (M * U <= 32); otherwise every lane loads its
+// own from global memory.
+template <int MT, int U, bool HAS_GS, bool ALDS>
+__global__ __launch_bounds__(MT > 4 ? 512 : 64 * kStripMaxWaves) void w4a16_strip_kernel(StripParams p) {
+  constexpr int MS = MT > 4 ? 2 : 1;            // MFMA sets of four activation rows
+  constexpr int RR = MT < 4 ? MT : 4;           // registers of a set that carry rows
+  extern __shared__ __align__(16) char strip_lds[];  // ALDS: one region per wave
+  // Workgroup b runs on XCD b % 8 (round-robin dispatch): XCD x takes the contiguous strips
+  // [x * spx, (x + 1) * spx), so each 128-byte line of the output is written from one L2.
+  const int s = (int)(blockIdx.x & 7) * p.spx + (int)(blockIdx.x >> 3);
+  if (s >= p.N / kStripCols) return;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int j = lane & 15, g = lane >> 4, cps = j & 3, rs = j >> 2;
+  const int rowoff = 32 * rs + 8 * g;           // this lane's 8 rows inside a block
+
+  const int64_t strip_bytes = (int64_t)p.kb * 1024;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.qs + (int64_t)s * strip_bytes, (uint32_t)strip_bytes);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda * 2));
+  const int ngroups = HAS_GS ? p.K / p.group : 1;
+  const __amdgpu_buffer_rsrc_t rsc =
+      make_rsrc(HAS_GS ? (const void*)(p.ss + (int64_t)s * ngroups * kStripCols) : (const void*)p.qs,
+                HAS_GS ? (uint32_t)(ngroups * kStripCols * 2) : 16u);
+  char* const w_act = strip_lds + wave * strip_wave_lds(p.M, U, HAS_GS);
+  char* const w_sc = w_act + strip_wave_act_lds(p.M, U);
+  int xoff[MS];  // this lane's activations inside block i: bytes of A (+ block), or of w_act
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms) {
+    const int m = min((lane & 3) + 4 * ms, p.M - 1);
+    xoff[ms] = ALDS ? (m * U * 128 + rowoff) * 2 : (m * (int)p.lda + rowoff) * 2;
+  }
+  const pk_f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  const pk_u4v neg8 = {0x80088008u, 0x80088008u, 0x80088008u, 0x80088008u};      // -8 * 2^-24
+  pk_f4 acc_lo[MS][2], acc_hi[MS][2];  // [set][column pair h]: 2^-24 / 2^-20 units
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) acc_lo[ms][h] = acc_hi[ms][h] = zero4;
+
+  for (int it = 0; it < p.iters; ++it) {
+    const int b0 = (it * p.nw + wave) * U;
+    if constexpr (ALDS) {
+      // This round's activations (M runs of U * 128 columns from column b0 * 128, the blocks
+      // past the strip clamped to its last) and U scale rows, ahead of the weights.
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the previous round's LDS reads are done
+      const int kp = U * 16, pieces = p.M * kp;  // 16-byte pieces
+      for (int p0 = 0; p0 < pieces; p0 += 64) {
+        const int pc = min(p0 + lane, pieces - 1), m = pc / kp;
+        const int col = min(b0 * 128 + (pc % kp) * 8, p.K - 8);
+        strip_dma16(ra, w_act + p0 * 16, (m * (int)p.lda + col) * 2);
+      }
+      if constexpr (HAS_GS)  // rows of the groups of blocks b0 .. b0+U-1, 2 pieces per row
+        strip_dma16(rsc, w_sc, min(strip_group(p, b0 * kStripBlockRows) * 2 + lane, ngroups * 2 - 1) * 16);
+      asm volatile("" ::: "memory");
+    }
+    // ---- all loads of this round: U blocks of weights (and activations, scales) ----------
+    pk_u4v w[U], x[U][MS];
+    pk_u2v sc[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int b = min(b0 + i, p.kb - 1);  // past the strip: re-read, contributes zero
+      w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16, b * 1024, kPkLoadStream);
+      if constexpr (!ALDS) {
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms)
+          x[i][ms] = __builtin_amdgcn_raw_buffer_load_b128(ra, xoff[ms], b * (kStripBlockRows * 2), 0);
+        if constexpr (HAS_GS)  // the row set's group: per lane where G < 128
+          sc[i] = __builtin_amdgcn_raw_buffer_load_b64(
+              rsc, cps * 8 + strip_group(p, b * kStripBlockRows + 32 * rs) * (kStripCols * 2), 0, 0);
+      }
+    }
+    if constexpr (ALDS) {
+      static_assert(U < 16, "vmcnt field");
+      __builtin_amdgcn_s_waitcnt(0x0f70 | U);  // the wave's DMAs landed; the U weights may fly
+      asm volatile("" ::: "memory");
+      const int g0 = HAS_GS ? strip_group(p, b0 * kStripBlockRows) : 0;
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        const int b = min(b0 + i, p.kb - 1);
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms)
+          x[i][ms] = *reinterpret_cast<const pk_u4v*>(w_act + xoff[ms] + (b - b0) * (kStripBlockRows * 2));
+        if constexpr (HAS_GS)
+          sc[i] = *reinterpret_cast<const pk_u2v*>(
+              w_sc + cps * 8 + (strip_group(p, b * kStripBlockRows + 32 * rs) - g0) * (kStripCols * 2));
+      }
+    }
+    // ---- products, in block order -------------------------------------------------------
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      if (b0 + i >= p.kb) break;  // wave-uniform: the blocks past the strip (last round only)
+      pk_half8 av[MS];
+      pk_f4 o8[MS], o136[MS];
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms) {
+        av[ms] = __builtin_bit_cast(pk_half8, x[i][ms]);
+        o8[ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[ms], __builtin_bit_cast(pk_half8, neg8), zero4, 0, 0, 0);
+        o136[ms] = o8[ms];  // 17 O8 (only the registers that carry rows are used)
+#pragma unroll
+        for (int r = 0; r < RR; ++r) o136[ms][r] = 17.0f * o8[ms][r];
+      }
+      float s_lo[2], s_hi[2];
+      if constexpr (HAS_GS) {
+        const pk_half4 hs = __builtin_bit_cast(pk_half4, sc[i]);
+        s_lo[0] = (float)hs[0]; s_hi[0] = (float)hs[1];
+        s_lo[1] = (float)hs[2]; s_hi[1] = (float)hs[3];
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t d0 = w[i][2 * h], d1 = w[i][2 * h + 1];  // nibbles u = v + 8
+        pk_u4v raw, lo;
+        raw[0] = __builtin_amdgcn_perm(d0, d0, 0x0c010c00u);  // rows e = 0, 1
+        raw[1] = __builtin_amdgcn_perm(d0, d0, 0x0c030c02u);  // rows 2, 3
+        raw[2] = __builtin_amdgcn_perm(d1, d1, 0x0c010c00u);  // rows 4, 5
+        raw[3] = __builtin_amdgcn_perm(d1, d1, 0x0c030c02u);  // rows 6, 7
+#pragma unroll
+        for (int d = 0; d < 4; ++d) lo[d] = raw[d] & 0x000f000fu;
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) {
+          const pk_f4 clo = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[ms], __builtin_bit_cast(pk_half8, lo), o8[ms], 0, 0, 0);
+          const pk_f4 craw = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[ms], __builtin_bit_cast(pk_half8, raw), o136[ms], 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < RR; ++r) {
+            const float hi = craw[r] - clo[r];
+            if constexpr (HAS_GS) {
+              acc_lo[ms][h][r] = __builtin_fmaf(clo[r], s_lo[h], acc_lo[ms][h][r]);
+              acc_hi[ms][h][r] = __builtin_fmaf(hi, s_hi[h], acc_hi[ms][h][r]);
+            } else {
+              acc_lo[ms][h][r] += clo[r];
+              acc_hi[ms][h][r] += hi;
+            }
+          }
+        }
+      }
+    }
+  }
+  // (No MFMA drain before the fold: every MFMA result above is consumed by VALU inside the
+  // loop, and the fold reads only the fp32 accumulators those VALU ops wrote.)
+
+  // ---- row sets and waves, through LDS, in a fixed order ----------------------------------
+  // Lane 20rs + cps holds columns 4cps .. 4cps+3 of row set rs in registers m % 4. Each wave
+  // writes its 4 row sets; then thread (m, part, col) adds the partials of waves
+  // part, part + 4, ... (row sets 0..3 each), and the four parts are added by two shuffles:
+  // ((part 0 + part 1) + (part 2 + part 3)), the same tree on every call.
+  __shared__ pk_f4 red[kStripMaxWaves][4][MT][kStripCols / 4];
+  if ((lane >> 4) == rs) {
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int r = 0; r < RR; ++r)
+        if (4 * ms + r < MT)
+          red[wave][rs][4 * ms + r][cps] = pk_f4{acc_lo[ms][0][r], acc_hi[ms][0][r],
+                                                 acc_lo[ms][1][r], acc_hi[ms][1][r]};
+  }
+  __syncthreads();
+  const int rows = p.M < MT ? p.M : MT;
+  for (int m = wave; m < rows; m += p.nw) {  // wave-uniform: one activation row per wave
+    const int part = lane >> 4, col = lane & 15;
+    const int kmax = (p.nw + 3) >> 2;  // wave-uniform
+    float v = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kStripMaxWaves / 4; ++k) {
+      if (k < kmax) {
+        const int wv = min(part + 4 * k, p.nw - 1);
+        const bool live = part + 4 * k < p.nw;
+        float q4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) q4[q] = red[wv][q][m][col >> 2][col & 3];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v += live ? q4[q] : 0.0f;
+      }
+    }
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (part == 0) {
+      v *= (col & 1) ? 1048576.0f : 16777216.0f;  // exact: powers of two
+      const int n = s * kStripCols + col;
+      store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + n, p.epi(v, n));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Plan: U blocks per wave per round, as many waves as cover the strip in one round (at most
+// 16), more rounds beyond that.
+// ---------------------------------------------------------------------------------------
+static int g_strip_u = 0;  // 0: automatic; 2, 4 or 8 fixes U (pk_w4a16_strips_config)
+
+bool strips_shape_ok(int M, int N, int K, int group, bool has_gs) {
+  if (M < 1 || M > 8 || N % kStripCols || K % kStripBlockRows || K < kStripBlockRows) return false;
+  if (has_gs && (group % 32 || K % group || (group < 128 && 128 % group))) return false;
+  return true;
+}
+
+// Blocks per wave, measured on MI355X at M = 1 (graphs over 40 rotating weight copies;
+// 4096 x 11008: 2 / 4 / 8 blocks 7.26 / 6.40 / 6.93 us; 4096 x 6144: 5.04 / 4.95 / 5.25;
+// 4096 x 14336: 8.98 / 7.76 / 8.07; 4096 x 4096: 4.29 / 4.23 / 4.06; 14336 x 4096: 7.53 /
+// 7.62 / 8.12): 4 (8 waves per workgroup at K = 4096), 8 where the strips leave at most one
+// workgroup per CU, 2 for deep layers (K > 8192: 16 waves, several rounds). More than two
+// rows take at most 4 (the 4-row kernel spills with 8), eight rows at most 2 (their
+// activation and accumulator registers double).
+static int strips_pick_u(int M, int N, int kb) {
+  int u = kb > 64 ? 2 : (N / kStripCols <= 256 ? 8 : 4);
+  if (g_strip_u) u = g_strip_u;
+  if (M > 2 && u > 4) u = 4;
+  if (M > 4 && u > 2) u = 2;
+  while (u > 2 && kb / u < 4) u /= 2;
+  return u;
+}
+
+// Activations and scales staged per wave in LDS: at most 8 KB of activations per wave
+// (M * U <= 32) and the wave's group-scale rows within one 1 KB DMA (at most 32 groups).
+static bool strips_alds(int M, int U, int group, bool has_gs) {
+  if ((int64_t)M * U > 32) return false;
+  if (!has_gs) return true;
+  const int rows = U * kStripBlockRows;  // a wave's rows per round, starting G-aligned if G | 128
+  const int groups = 128 % group == 0 ? rows / group : rows / group + 1;
+  return groups <= 32;
+}
+
+int strips_launch(const void* a, int64_t lda, const uint8_t* qs, const void* ss, int group,
+                  OutEpi epi, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                  hipStream_t stream) {
+  StripParams p;
+  p.a = reinterpret_cast<const pk_half*>(a);
+  p.lda = lda;
+  p.qs = qs;
+  p.ss = reinterpret_cast<const pk_half*>(ss);
+  p.group = ss ? group : K;
+  p.group_shift = -1;
+  if (ss && (group & (group - 1)) == 0) p.group_shift = __builtin_ctz((unsigned)group);
+  p.epi = epi;
+  p.c = c;
+  p.c_dtype = c_dtype;
+  p.ldc = ldc;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.kb = K / kStripBlockRows;
+  const int u = strips_pick_u(M, N, p.kb);
+  const int max_waves = M > 4 ? 8 : kStripMaxWaves;  // the 8-row kernel's launch bound
+  const int waves_one_round = (int)cdiv(p.kb, u);
+  p.nw = waves_one_round < max_waves ? waves_one_round : max_waves;
+  p.iters = (int)cdiv(p.kb, (int64_t)u * p.nw);
+  // (the static fold array takes 16 waves x 4 row sets x rows x 64 bytes)
+  const size_t lds_alds = (size_t)p.nw * strip_wave_lds(M, u, ss != nullptr);
+  const int mt = M == 1 ? 1 : M == 2 ? 2 : M <= 4 ? 4 : 8;
+  const bool alds = strips_alds(M, u, p.group, ss != nullptr) &&
+                    lds_alds + (size_t)kStripMaxWaves * 4 * mt * 64 <= (64u << 10);
+  const size_t lds = alds ? lds_alds : 0;
+  p.spx = (int)cdiv(N / kStripCols, 8);
+  const dim3 grid(8 * p.spx), block(64 * p.nw);
+  auto go = [&](auto MTc, auto Uc, auto AL) {
+    constexpr int mt = decltype(MTc)::value, uu = decltype(Uc)::value;
+    constexpr bool al = decltype(AL)::value != 0;
+    if (ss) w4a16_strip_kernel<mt, uu, true, al><<<grid, block, lds, stream>>>(p);
+    else w4a16_strip_kernel<mt, uu, false, al><<<grid, block, lds, stream>>>(p);
+  };
+  auto by_u = [&](auto MTc, auto AL) {
+    if (u == 2) go(MTc, pk_int_c<2>{}, AL);
+    else if (u == 4) go(MTc, pk_int_c<4>{}, AL);
+    else go(MTc, pk_int_c<8>{}, AL);
+  };
+  auto by_m = [&](auto AL) {
+    if (M == 1) by_u(pk_int_c<1>{}, AL);
+    else if (M == 2) by_u(pk_int_c<2>{}, AL);
+    else if (M <= 4) by_u(pk_int_c<4>{}, AL);
+    else by_u(pk_int_c<8>{}, AL);
+  };
+  if (alds) by_m(pk_int_c<1>{});
+  else by_m(pk_int_c<0>{});
+  PK_LAUNCH_CHECK("w4a16 gemv (strip layout)");
+  return PK_OK;
+}
+
+bool strips_config_set(int u) {
+  if (u != 0 && u != 2 && u != 4 && u != 8) return false;
+  g_strip_u = u;
+  return true;
+}
+
+}  // namespace pk
+
+using namespace pk;
+
+extern "C" int pk_w4a16_strips_config(int blocks_per_wave) {
+  PK_REQUIRE(strips_config_set(blocks_per_wave),
+             "pk_w4a16_strips_config: %d is not 0 (automatic), 2, 4 or 8", blocks_per_wave);
+  return PK_OK;
+}
+
+extern "C" int pk_w4a16_gemm_strips(const void* a, int64_t lda, const uint8_t* qstrips,
+                                    const void* sstrips, int group_size, float tensor_scale,
+                                    const void* bias, int bias_dtype, void* c, int c_dtype,
+                                    int64_t ldc, int M, int N, int K, void* stream) {
+  auto al = [](const void* q, unsigned b) { return (reinterpret_cast<uintptr_t>(q) & (b - 1)) == 0; };
+  PK_REQUIRE(a != nullptr && qstrips != nullptr && c != nullptr, "pk_w4a16_gemm_strips: null pointer");
+  PK_REQUIRE(M >= 1 && M <= 8, "pk_w4a16_gemm_strips: M=%d (the strip layout serves 1..8 rows)", M);
+  PK_REQUIRE(N >= 16 && N % 16 == 0 && K >= 128 && K % 128 == 0,
+             "pk_w4a16_gemm_strips: needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", N, K);
+  PK_REQUIRE(sstrips == nullptr || strips_shape_ok(M, N, K, group_size, true),
+             "pk_w4a16_gemm_strips: group_size=%d must be a multiple of 32 dividing K=%d and "
+             "either divide 128 or be a multiple of it", group_size, K);
+  PK_REQUIRE(lda >= K && lda % 8 == 0 && al(a, 16), "pk_w4a16_gemm_strips: A rows must be 16-byte aligned");
+  PK_REQUIRE((int64_t)M * lda * 2 < (1ll << 31), "pk_w4a16_gemm_strips: A beyond 2 GiB");
+  PK_REQUIRE((int64_t)K * 8 < (1ll << 31), "pk_w4a16_gemm_strips: K=%d too large", K);
+  PK_REQUIRE(al(qstrips, 16) && (sstrips == nullptr || al(sstrips, 8)),
+             "pk_w4a16_gemm_strips: weights must be 16-byte and scales 8-byte aligned");
+  PK_REQUIRE(ldc >= N, "pk_w4a16_gemm_strips: ldc < N");
+  PK_REQUIRE(c_dtype == PK_F32 || c_dtype == PK_F16 || c_dtype == PK_BF16,
+             "pk_w4a16_gemm_strips: output dtype %d", c_dtype);
+  PK_REQUIRE(bias == nullptr || bias_dtype == PK_F32 || bias_dtype == PK_F16 || bias_dtype == PK_BF16,
+             "pk_w4a16_gemm_strips: bias dtype %d", bias_dtype);
+  return strips_launch(a, lda, qstrips, sstrips, group_size, OutEpi(tensor_scale, bias, bias_dtype),
+                       c, c_dtype, ldc, M, N, K, (hipStream_t)stream);
+}

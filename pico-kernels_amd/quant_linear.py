@@ -30,8 +30,15 @@ shape; ``load_quantized`` checks each tensor's shape and dtype before copying an
 In memory, layers whose shape allows it (``in`` and ``out`` multiples of 256, groups of a
 multiple of 64 inputs or per-input scales: ``QuantLinear.tiled``) keep ``qweight`` in blocks
 of 128 inputs x 256 outputs, each 16 KB block contiguous (``_pk.tile_weights``), which the
-kernels stream in long runs (``pk_w4a16_gemm_tiled``). ``codes()`` / ``set_codes()``, the
-state dict and the file format use ``pack_int4_n`` order either way.
+kernels stream in long runs (``pk_w4a16_gemm_tiled``). For decode, layers whose shape allows
+it (``out % 16 == 0``, ``in % 128 == 0``, groups of a multiple of 32 that divide 128 or are
+multiples of it, or per-input scales: ``QuantLinear.decode``) keep a second copy of the codes
+and group scales in the strip layout (``_pk.strip_weights`` / ``strip_scales``: each
+16-output strip's inputs contiguous), and calls of at most ``DECODE_MAX_ROWS`` rows run the
+one-launch strip GEMV on it (``pk_w4a16_gemm_strips``). The int4 codes are a quarter of the
+fp16 weights' bytes, so both copies together are half of them; ``decode_layout=False`` keeps
+one copy. The copies are derived buffers, outside the state dict. ``codes()`` /
+``set_codes()``, the state dict and the file format use ``pack_int4_n`` order either way.
 
 The output has the input's dtype (fp16, bf16 or fp32, as ``nn.Linear``); other inputs are
 computed in fp16. A finite bf16 / fp32 activation whose fp16 form would be infinite (beyond
@@ -58,6 +65,8 @@ FORMAT = "pico-kernels-amd/w4a16"
 FORMAT_VERSION = 2
 SCHEMES = ("group", "per_input")
 _OUT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+# Rows up to which forward runs the strip-layout GEMV (when the layer keeps that copy).
+DECODE_MAX_ROWS = 4
 
 
 class QuantLinear(nn.Module):
@@ -68,7 +77,7 @@ class QuantLinear(nn.Module):
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True,
                  group_size: int = 128, device: torch.device | str | None = None,
-                 scheme: str = "group"):
+                 scheme: str = "group", decode_layout: bool = True):
         super().__init__()
         if scheme not in SCHEMES:
             raise ValueError(f"scheme must be one of {SCHEMES}, not {scheme!r}")
@@ -96,6 +105,14 @@ class QuantLinear(nn.Module):
         else:
             self.bias = None
         self._smax = 1.0  # per_input: max of the scales (the epilogue scale)
+        # the decode copy: codes (and group scales) in the strip layout, derived from the above
+        self.decode = bool(decode_layout) and _pk.strips_ok(in_features, out_features,
+                                                            self.group_size)
+        self.register_buffer("qstrips", torch.zeros_like(self.qweight) if self.decode else None,
+                             persistent=False)
+        self.register_buffer("sstrips", torch.zeros_like(self.scales)
+                             if self.decode and scheme == "group" else None, persistent=False)
+        self._calls: dict = {}  # prepared strip-GEMV calls by output dtype (see _strips_call)
 
     # ---- construction -------------------------------------------------------------------
     @classmethod
@@ -131,6 +148,7 @@ class QuantLinear(nn.Module):
         q.scales.copy_(scales)
         if linear.bias is not None:
             q.bias.copy_(linear.bias.detach().to(torch.float16))
+        q._refresh()
         return q
 
     @classmethod
@@ -160,9 +178,9 @@ class QuantLinear(nn.Module):
         codes = q.t().contiguous().to(torch.int8)       # (in, out)
         layer.set_codes(gemm_int4.pack_int4_n(codes).view(torch.int32))
         layer.scales.copy_(s)
-        layer._smax = float(s.max().item())
         if bias is not None:
             layer.bias.copy_(bias.to(torch.float16))
+        layer._refresh()
         return layer
 
     # ---- codes ------------------------------------------------------------------------
@@ -174,6 +192,8 @@ class QuantLinear(nn.Module):
         """Store ``(in, out/8)`` int32 words given in ``pack_int4_n`` order."""
         words = words.to(self.qweight.device)
         self.qweight.copy_(_pk.tile_weights(words) if self.tiled else words)
+        if self.decode:
+            self.qstrips.copy_(_pk.strip_weights(words))  # in place: prepared calls stay valid
 
     # ---- use ----------------------------------------------------------------------------
     def dequantized_weight(self) -> torch.Tensor:
@@ -183,11 +203,30 @@ class QuantLinear(nn.Module):
         q = gemm_int4.unpack_int4_n(self.codes().contiguous().view(torch.uint8)).float()
         return (q * self.scales.to(q.device)[:, None]).t()
 
+    def _strips_call(self, out_dtype: torch.dtype) -> "_pk.PreparedStrips":
+        call = self._calls.get(out_dtype)
+        # (rebuilt when the copy is no longer this module's buffer: reassigned, or a deep copy)
+        if call is None or call._keep[0] is not self.qstrips or call._keep[2] is not self.bias:
+            scale = self._smax if self.scheme == "per_input" else 1.0
+            call = _pk.PreparedStrips(self.qstrips, self.sstrips, self.group_size, scale, out_dtype,
+                                      self.bias)
+            self._calls[out_dtype] = call
+        return call
+
+    def _apply(self, fn, *args, **kwargs):
+        self._calls = {}  # buffers may move: prepared calls hold their addresses
+        return super()._apply(fn, *args, **kwargs)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         assert x.shape[-1] == self.in_features
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.in_features)
+        if (x2.dtype == torch.float16 and self.scheme == "group" and self.decode
+                and x2.shape[0] <= DECODE_MAX_ROWS):
+            # decode fast path: one prepared strip-GEMV call, no conversions
+            return self._strips_call(torch.float16)(x2).view(*lead, self.out_features)
         out_dtype = x.dtype if x.dtype in _OUT_DTYPES else torch.float16
+        strips = self.decode and x2.shape[0] <= DECODE_MAX_ROWS
         # the bias is added in the matmul's epilogue (before the one rounding to out_dtype)
         if self.scheme == "per_input":
             # x * s / max s in fp16 (the input cast in the same pass), then max s in the epilogue
@@ -195,20 +234,33 @@ class QuantLinear(nn.Module):
             xp = _pk.w4a16_prep_activations(x2, s, 1.0 / self._smax)
             if self.range_check:
                 _pk.check_fp16_range(x2, "QuantLinear", xp)
-            y = _pk.w4a16_gemm(xp, self.qweight, None, 0, self._smax, out_dtype, bias=self.bias,
-                               tiled=self.tiled)
+            if strips:
+                y = self._strips_call(out_dtype)(xp)
+            else:
+                y = _pk.w4a16_gemm(xp, self.qweight, None, 0, self._smax, out_dtype,
+                                   bias=self.bias, tiled=self.tiled)
         else:
             xp = x2 if x2.dtype == torch.float16 else _pk.w4a16_prep_activations(x2, None, 1.0)
             if self.range_check and xp is not x2:
                 _pk.check_fp16_range(x2, "QuantLinear", xp)
-            s = self.scales if self.scales.dtype == torch.float16 else self.scales.half()
-            y = _pk.w4a16_gemm(xp, self.qweight, s, self.group_size, 1.0, out_dtype,
-                               bias=self.bias, tiled=self.tiled)
+            if strips:
+                y = self._strips_call(out_dtype)(xp)
+            else:
+                s = self.scales if self.scales.dtype == torch.float16 else self.scales.half()
+                y = _pk.w4a16_gemm(xp, self.qweight, s, self.group_size, 1.0, out_dtype,
+                                   bias=self.bias, tiled=self.tiled)
         return y.reshape(*lead, self.out_features)
 
     def _refresh(self) -> None:
+        """Rebuild what derives from the buffers: the per-input epilogue scale and the decode
+        copy in the strip layout (call after changing ``qweight`` or ``scales`` directly)."""
+        self._calls = {}
         if self.scheme == "per_input":
             self._smax = float(self.scales.float().max().item())
+        if self.decode:
+            self.qstrips = _pk.strip_weights(self.codes()).to(self.qweight.device)
+            if self.scheme == "group":
+                self.sstrips = _pk.strip_scales(self.scales.half()).to(self.scales.device)
 
     # the state dict holds the codes in pack_int4_n order, whatever the layout in memory
     def _save_to_state_dict(self, destination, prefix, keep_vars):
@@ -228,7 +280,8 @@ class QuantLinear(nn.Module):
         lay = f"group_size={self.group_size}" if self.scheme == "group" else "per-input scales"
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"bias={self.bias is not None}, {lay}, int4"
-                + (", 128x256 blocks" if self.tiled else ""))
+                + (", 128x256 blocks" if self.tiled else "")
+                + (", strip copy for decode" if self.decode else ""))
 
 
 def quantize_model_int4(model: nn.Module, group_size: int = 128, predicate=None,
