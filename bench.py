@@ -4,7 +4,7 @@
 Headline workload: W4A16 decode GEMV, M=1, K=4096, N=11008, int4 group
 128 with fp16 scales, fp16 activations N(0,1), weights N(0, 0.02), seeded CPU generator.
 A "step" is one call over one activation row on the copy of the weights ``QuantLinear`` runs
-decode (at most ``DECODE_MAX_ROWS`` rows) on: the strip layout (``pk_w4a16_gemm_strips``: each
+decode (up to ``QuantLinear.decode_rows`` rows) on: the strip layout (``pk_w4a16_gemm_strips``: each
 16-column strip's K rows contiguous, one workgroup per strip over the whole of K, one launch).
 The same call on ``QuantLinear``'s block layout (``pk_w4a16_gemm_tiled``, 128 x 256 blocks:
 the split-K GEMV, slices added in L2) and on ``pack_int4_n``'s row layout (``pk_w4a16_gemm``)
@@ -257,7 +257,7 @@ def bench_gemv(args, dev) -> dict:
         _pk.w4a16_gemm_strips(ag, qss[i % N_ROTATE], sss[i % N_ROTATE], 128, 1.0,
                               torch.float16, out=out)
 
-    def step_blocks(i):  # QuantLinear's layout above DECODE_MAX_ROWS rows: blocks
+    def step_blocks(i):  # QuantLinear's layout above its decode rows: blocks
         _pk.w4a16_gemm(ag, qts[i % N_ROTATE], scs[i % N_ROTATE], 128, 1.0, torch.float16,
                        split_k=0, out=out, tiled=True)
 
@@ -448,7 +448,7 @@ def bench_llama_sweep(dev, iters: int = 50) -> list:
         for M in (1, 8, 32, 128):
             a = torch.randn(M, K, generator=_gen(7)).half().to(dev)
             out = torch.empty((M, N), dtype=torch.float16, device=dev)
-            strips = M <= quant_linear.DECODE_MAX_ROWS
+            strips = M <= quant_linear.decode_rows(K, N)
 
             def step(i):  # what QuantLinear runs: the strip copy for decode rows, else blocks
                 if strips:

@@ -200,6 +200,22 @@ int pk_w4a16_gemm_strips(const void* a, int64_t lda, const uint8_t* qstrips, con
  * automatic choice; for measurements. No counterpart in the reference. */
 int pk_w4a16_strips_config(int blocks_per_wave);
 
+/* pk_w4a16_gemm_strips bound to one set of strip-layout weights, for eager decode loops that
+ * pay host time per call: pk_w4a16_strips_prepare checks the fixed arguments (weights, scales,
+ * group, tensor scale, bias, output dtype, N, K and the activations' row stride lda) and plans
+ * M = 1..8 once; pk_w4a16_strips_run then takes only the activations, the output and its row
+ * stride, the row count and the stream, and launches the same kernel with the same bits. The
+ * handle holds pointers, not copies: the weights, scales and bias must stay allocated and in
+ * place until pk_w4a16_strips_release. prepare returns NULL on a bad argument
+ * (pk_last_error says which); run returns PK_OK or an error code. A handle is read-only after
+ * prepare, so runs on several streams may share it. No counterpart in the reference (a
+ * Triton launch has no prepared form). */
+void* pk_w4a16_strips_prepare(const uint8_t* qstrips, const void* sstrips, int group_size,
+                              float tensor_scale, const void* bias, int bias_dtype, int c_dtype,
+                              int N, int K, int64_t lda);
+int pk_w4a16_strips_run(void* prepared, const void* a, void* c, int64_t ldc, int M, void* stream);
+void pk_w4a16_strips_release(void* prepared);
+
 /* Rows per kernel call of pk_w4a16_gemm_tiled for M activation rows of stride lda elements:
  * M itself while the activations span less than 2 GiB (M * lda * 2 bytes); beyond that the
  * call runs equal chunks of this many rows (a multiple of 128), since the kernels that read

@@ -62,6 +62,9 @@ _SIGNATURES = {
     "pk_w4a16_gemm_strips": (_i32, [_vp, _i64, _vp, _vp, _i32, _f32, _vp, _i32, _vp, _i32, _i64,
                                     _i32, _i32, _i32, _vp]),
     "pk_w4a16_strips_config": (_i32, [_i32]),
+    "pk_w4a16_strips_prepare": (_vp, [_vp, _vp, _i32, _f32, _vp, _i32, _i32, _i32, _i32, _i64]),
+    "pk_w4a16_strips_run": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp]),
+    "pk_w4a16_strips_release": (None, [_vp]),
     "pk_w4a16_skinny_layout": (_i32, [_i32, _i32]),
     "pk_w4a16_prep_activations": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _vp]),
     "pk_w4a16_gemm_noalloc": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _f32, _vp, _i32, _i64, _i32, _i32,
@@ -417,42 +420,55 @@ def w4a16_gemm_strips(a: torch.Tensor, qstrips: torch.Tensor, sstrips: torch.Ten
 
 
 class PreparedStrips:
-    """``pk_w4a16_gemm_strips`` bound to one strip-layout weight copy: the weight, scale and bias
-    pointers, group, tensor scale and output dtype are converted once, so a call converts only
-    the activations, the output and the stream (what an eager decode loop pays per layer). The
-    tensors must stay alive and in place while the object is used (QuantLinear drops it when
-    its buffers move or change)."""
+    """``pk_w4a16_gemm_strips`` bound to one strip-layout weight copy through
+    ``pk_w4a16_strips_prepare``: the fixed arguments are checked and the launches for 1..8 rows
+    planned once, so a call passes only the activations, the output, the row count and the
+    stream (what an eager decode loop pays per layer). Activations must be 16-byte aligned with
+    row stride ``lda`` (elements; default K). The tensors stay referenced here, and must stay
+    in place, while the object lives (QuantLinear drops it when its buffers move or change)."""
 
-    __slots__ = ("q", "s", "g", "scale", "b", "bd", "od", "out_dtype", "N", "K", "dev", "fn",
-                 "_keep")
+    __slots__ = ("h", "N", "K", "lda", "out_dtype", "dev", "run", "release", "_keep")
 
     def __init__(self, qstrips: torch.Tensor, sstrips: torch.Tensor | None, group_size: int,
-                 tensor_scale: float, out_dtype: torch.dtype, bias: torch.Tensor | None = None):
+                 tensor_scale: float, out_dtype: torch.dtype, bias: torch.Tensor | None = None,
+                 lda: int | None = None):
+        L = lib()
         self.K, W = qstrips.shape
         self.N = 8 * W
-        self.q = qstrips.data_ptr()
-        self.s = None if sstrips is None else sstrips.data_ptr()
-        self.g = int(group_size) if sstrips is not None else 0
-        self.scale = float(tensor_scale)
-        self.b = None if bias is None else bias.data_ptr()
-        self.bd = _TORCH_TO_PK[bias.dtype] if bias is not None else PK_F16
-        self.od = _TORCH_TO_PK[out_dtype]
+        self.lda = self.K if lda is None else int(lda)
         self.out_dtype = out_dtype
         self.dev = qstrips.device.index
-        self.fn = lib().pk_w4a16_gemm_strips
         self._keep = (qstrips, sstrips, bias)
+        self.h = L.pk_w4a16_strips_prepare(
+            qstrips.data_ptr(), None if sstrips is None else sstrips.data_ptr(),
+            int(group_size) if sstrips is not None else 0, float(tensor_scale),
+            None if bias is None else bias.data_ptr(),
+            _TORCH_TO_PK[bias.dtype] if bias is not None else PK_F16, _TORCH_TO_PK[out_dtype],
+            self.N, self.K, self.lda)
+        if not self.h:
+            raise PicoKernelsError("pk_w4a16_strips_prepare failed: "
+                                   + L.pk_last_error().decode(errors="replace"))
+        self.run, self.release = L.pk_w4a16_strips_run, L.pk_w4a16_strips_release
+
+    def __del__(self):
+        h = getattr(self, "h", None)
+        if h:
+            self.release(h)
+            self.h = None
 
     def __call__(self, a: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         M = a.shape[0]
-        if a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16:
-            a = _rows_ok(a)
+        if a.stride(0) != self.lda or a.stride(1) != 1 or a.data_ptr() % 16:
+            a = a.contiguous() if self.lda == self.K else _rows_ok(a)
+            if a.stride(0) != self.lda or a.data_ptr() % 16:
+                raise ValueError(f"PreparedStrips: activations need row stride {self.lda}, "
+                                 "16-byte aligned")
         if out is None:
-            out = torch.empty((M, self.N), dtype=self.out_dtype, device=a.device)
-        rc = self.fn(a.data_ptr(), a.stride(0), self.q, self.s, self.g, self.scale, self.b,
-                     self.bd, out.data_ptr(), self.od, out.stride(0), M, self.N, self.K,
-                     torch._C._cuda_getCurrentRawStream(self.dev))
+            out = a.new_empty((M, self.N), dtype=self.out_dtype)
+        rc = self.run(self.h, a.data_ptr(), out.data_ptr(), out.stride(0), M,
+                      torch._C._cuda_getCurrentRawStream(self.dev))
         if rc != PK_OK:
-            _check(rc, "pk_w4a16_gemm_strips")
+            _check(rc, "pk_w4a16_strips_run")
         return out
 
 

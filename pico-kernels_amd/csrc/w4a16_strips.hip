@@ -35,6 +35,8 @@
 // (MFMA keeps fp16 subnormal inputs; products are exact). Each block's sums are scaled by
 // their group scale in fp32 and added per lane in block order; the workgroup then adds its
 // row sets and waves through LDS in a fixed order, so results are bitwise reproducible.
+#include <new>
+
 #include "pk_internal.h"
 
 namespace pk {
@@ -304,11 +306,19 @@ static bool strips_alds(int M, int U, int group, bool has_gs) {
   return groups <= 32;
 }
 
-int strips_launch(const void* a, int64_t lda, const uint8_t* qs, const void* ss, int group,
-                  OutEpi epi, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
-                  hipStream_t stream) {
-  StripParams p;
-  p.a = reinterpret_cast<const pk_half*>(a);
+// Everything about a launch that depends on the shape and weights only.
+struct StripPlan {
+  StripParams p;  // a, c, ldc and M are filled in per call
+  int u;
+  bool alds;
+  size_t lds;
+  dim3 grid, block;
+};
+
+static void strips_plan(const uint8_t* qs, const void* ss, int group, OutEpi epi, int c_dtype,
+                        int M, int N, int K, int64_t lda, StripPlan* pl) {
+  StripParams& p = pl->p;
+  p.a = nullptr;
   p.lda = lda;
   p.qs = qs;
   p.ss = reinterpret_cast<const pk_half*>(ss);
@@ -316,9 +326,9 @@ int strips_launch(const void* a, int64_t lda, const uint8_t* qs, const void* ss,
   p.group_shift = -1;
   if (ss && (group & (group - 1)) == 0) p.group_shift = __builtin_ctz((unsigned)group);
   p.epi = epi;
-  p.c = c;
+  p.c = nullptr;
   p.c_dtype = c_dtype;
-  p.ldc = ldc;
+  p.ldc = 0;
   p.M = M;
   p.N = N;
   p.K = K;
@@ -331,16 +341,27 @@ int strips_launch(const void* a, int64_t lda, const uint8_t* qs, const void* ss,
   // (the static fold array takes 16 waves x 4 row sets x rows x 64 bytes)
   const size_t lds_alds = (size_t)p.nw * strip_wave_lds(M, u, ss != nullptr);
   const int mt = M == 1 ? 1 : M == 2 ? 2 : M <= 4 ? 4 : 8;
-  const bool alds = strips_alds(M, u, p.group, ss != nullptr) &&
-                    lds_alds + (size_t)kStripMaxWaves * 4 * mt * 64 <= (64u << 10);
-  const size_t lds = alds ? lds_alds : 0;
+  pl->u = u;
+  pl->alds = strips_alds(M, u, p.group, ss != nullptr) &&
+             lds_alds + (size_t)kStripMaxWaves * 4 * mt * 64 <= (64u << 10);
+  pl->lds = pl->alds ? lds_alds : 0;
   p.spx = (int)cdiv(N / kStripCols, 8);
-  const dim3 grid(8 * p.spx), block(64 * p.nw);
+  pl->grid = dim3(8 * p.spx);
+  pl->block = dim3(64 * p.nw);
+}
+
+static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, hipStream_t stream) {
+  StripParams p = pl.p;
+  p.a = reinterpret_cast<const pk_half*>(a);
+  p.c = c;
+  p.ldc = ldc;
+  const int M = p.M, u = pl.u;
+  const bool gs = p.ss != nullptr;
   auto go = [&](auto MTc, auto Uc, auto AL) {
     constexpr int mt = decltype(MTc)::value, uu = decltype(Uc)::value;
     constexpr bool al = decltype(AL)::value != 0;
-    if (ss) w4a16_strip_kernel<mt, uu, true, al><<<grid, block, lds, stream>>>(p);
-    else w4a16_strip_kernel<mt, uu, false, al><<<grid, block, lds, stream>>>(p);
+    if (gs) w4a16_strip_kernel<mt, uu, true, al><<<pl.grid, pl.block, pl.lds, stream>>>(p);
+    else w4a16_strip_kernel<mt, uu, false, al><<<pl.grid, pl.block, pl.lds, stream>>>(p);
   };
   auto by_u = [&](auto MTc, auto AL) {
     if (u == 2) go(MTc, pk_int_c<2>{}, AL);
@@ -353,10 +374,18 @@ int strips_launch(const void* a, int64_t lda, const uint8_t* qs, const void* ss,
     else if (M <= 4) by_u(pk_int_c<4>{}, AL);
     else by_u(pk_int_c<8>{}, AL);
   };
-  if (alds) by_m(pk_int_c<1>{});
+  if (pl.alds) by_m(pk_int_c<1>{});
   else by_m(pk_int_c<0>{});
   PK_LAUNCH_CHECK("w4a16 gemv (strip layout)");
   return PK_OK;
+}
+
+int strips_launch(const void* a, int64_t lda, const uint8_t* qs, const void* ss, int group,
+                  OutEpi epi, void* c, int c_dtype, int64_t ldc, int M, int N, int K,
+                  hipStream_t stream) {
+  StripPlan pl;
+  strips_plan(qs, ss, group, epi, c_dtype, M, N, K, lda, &pl);
+  return strips_run(pl, a, c, ldc, stream);
 }
 
 bool strips_config_set(int u) {
@@ -375,28 +404,83 @@ extern "C" int pk_w4a16_strips_config(int blocks_per_wave) {
   return PK_OK;
 }
 
+namespace {
+int check_strips(const char* name, const void* a, int64_t lda, const uint8_t* qstrips,
+                 const void* sstrips, int group_size, const void* bias, int bias_dtype,
+                 const void* c, int c_dtype, int64_t ldc, int M, int N, int K) {
+  auto al = [](const void* q, unsigned b) { return (reinterpret_cast<uintptr_t>(q) & (b - 1)) == 0; };
+  PK_REQUIRE(qstrips != nullptr, "%s: null weights", name);
+  PK_REQUIRE(M >= 1 && M <= 8, "%s: M=%d (the strip layout serves 1..8 rows)", name, M);
+  PK_REQUIRE(N >= 16 && N % 16 == 0 && K >= 128 && K % 128 == 0,
+             "%s: needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", name, N, K);
+  PK_REQUIRE(sstrips == nullptr || strips_shape_ok(M, N, K, group_size, true),
+             "%s: group_size=%d must be a multiple of 32 dividing K=%d and either divide 128 or "
+             "be a multiple of it", name, group_size, K);
+  PK_REQUIRE(a == nullptr || (lda >= K && lda % 8 == 0 && al(a, 16)),
+             "%s: A rows must be 16-byte aligned", name);
+  PK_REQUIRE((int64_t)M * lda * 2 < (1ll << 31), "%s: A beyond 2 GiB", name);
+  PK_REQUIRE((int64_t)K * 8 < (1ll << 31), "%s: K=%d too large", name, K);
+  PK_REQUIRE(al(qstrips, 16) && (sstrips == nullptr || al(sstrips, 8)),
+             "%s: weights must be 16-byte and scales 8-byte aligned", name);
+  PK_REQUIRE(c == nullptr || ldc >= N, "%s: ldc < N", name);
+  PK_REQUIRE(c_dtype == PK_F32 || c_dtype == PK_F16 || c_dtype == PK_BF16,
+             "%s: output dtype %d", name, c_dtype);
+  PK_REQUIRE(bias == nullptr || bias_dtype == PK_F32 || bias_dtype == PK_F16 || bias_dtype == PK_BF16,
+             "%s: bias dtype %d", name, bias_dtype);
+  return PK_OK;
+}
+
+// A prepared call: the plans of one set of weights for M = 1..8 at one lda (made once, read
+// only afterwards, so concurrent runs on different streams may share it).
+struct StripsPrepared {
+  StripPlan plan[8];  // by M - 1
+  int N;
+  int64_t lda;
+};
+}  // namespace
+
 extern "C" int pk_w4a16_gemm_strips(const void* a, int64_t lda, const uint8_t* qstrips,
                                     const void* sstrips, int group_size, float tensor_scale,
                                     const void* bias, int bias_dtype, void* c, int c_dtype,
                                     int64_t ldc, int M, int N, int K, void* stream) {
-  auto al = [](const void* q, unsigned b) { return (reinterpret_cast<uintptr_t>(q) & (b - 1)) == 0; };
-  PK_REQUIRE(a != nullptr && qstrips != nullptr && c != nullptr, "pk_w4a16_gemm_strips: null pointer");
-  PK_REQUIRE(M >= 1 && M <= 8, "pk_w4a16_gemm_strips: M=%d (the strip layout serves 1..8 rows)", M);
-  PK_REQUIRE(N >= 16 && N % 16 == 0 && K >= 128 && K % 128 == 0,
-             "pk_w4a16_gemm_strips: needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", N, K);
-  PK_REQUIRE(sstrips == nullptr || strips_shape_ok(M, N, K, group_size, true),
-             "pk_w4a16_gemm_strips: group_size=%d must be a multiple of 32 dividing K=%d and "
-             "either divide 128 or be a multiple of it", group_size, K);
-  PK_REQUIRE(lda >= K && lda % 8 == 0 && al(a, 16), "pk_w4a16_gemm_strips: A rows must be 16-byte aligned");
-  PK_REQUIRE((int64_t)M * lda * 2 < (1ll << 31), "pk_w4a16_gemm_strips: A beyond 2 GiB");
-  PK_REQUIRE((int64_t)K * 8 < (1ll << 31), "pk_w4a16_gemm_strips: K=%d too large", K);
-  PK_REQUIRE(al(qstrips, 16) && (sstrips == nullptr || al(sstrips, 8)),
-             "pk_w4a16_gemm_strips: weights must be 16-byte and scales 8-byte aligned");
-  PK_REQUIRE(ldc >= N, "pk_w4a16_gemm_strips: ldc < N");
-  PK_REQUIRE(c_dtype == PK_F32 || c_dtype == PK_F16 || c_dtype == PK_BF16,
-             "pk_w4a16_gemm_strips: output dtype %d", c_dtype);
-  PK_REQUIRE(bias == nullptr || bias_dtype == PK_F32 || bias_dtype == PK_F16 || bias_dtype == PK_BF16,
-             "pk_w4a16_gemm_strips: bias dtype %d", bias_dtype);
+  PK_REQUIRE(a != nullptr && c != nullptr, "pk_w4a16_gemm_strips: null pointer");
+  const int rc = check_strips("pk_w4a16_gemm_strips", a, lda, qstrips, sstrips, group_size, bias,
+                              bias_dtype, c, c_dtype, ldc, M, N, K);
+  if (rc != PK_OK) return rc;
   return strips_launch(a, lda, qstrips, sstrips, group_size, OutEpi(tensor_scale, bias, bias_dtype),
                        c, c_dtype, ldc, M, N, K, (hipStream_t)stream);
+}
+
+extern "C" void* pk_w4a16_strips_prepare(const uint8_t* qstrips, const void* sstrips,
+                                         int group_size, float tensor_scale, const void* bias,
+                                         int bias_dtype, int c_dtype, int N, int K, int64_t lda) {
+  if (check_strips("pk_w4a16_strips_prepare", nullptr, lda, qstrips, sstrips, group_size, bias,
+                   bias_dtype, nullptr, c_dtype, N, 1, N, K) != PK_OK)
+    return nullptr;
+  auto* h = new (std::nothrow) StripsPrepared();
+  if (h == nullptr) {
+    set_error("pk_w4a16_strips_prepare: out of host memory");
+    return nullptr;
+  }
+  h->N = N;
+  h->lda = lda;
+  for (int m = 1; m <= 8; ++m)
+    strips_plan(qstrips, sstrips, group_size, OutEpi(tensor_scale, bias, bias_dtype), c_dtype, m,
+                N, K, lda, &h->plan[m - 1]);
+  return h;
+}
+
+extern "C" int pk_w4a16_strips_run(void* prepared, const void* a, void* c, int64_t ldc, int M,
+                                   void* stream) {
+  auto* h = static_cast<StripsPrepared*>(prepared);
+  PK_REQUIRE(h != nullptr && a != nullptr && c != nullptr, "pk_w4a16_strips_run: null pointer");
+  PK_REQUIRE(M >= 1 && M <= 8, "pk_w4a16_strips_run: M=%d (the strip layout serves 1..8 rows)", M);
+  PK_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15) == 0, "pk_w4a16_strips_run: A must be 16-byte aligned");
+  PK_REQUIRE(ldc >= h->N, "pk_w4a16_strips_run: ldc < N");
+  PK_REQUIRE((int64_t)M * h->lda * 2 < (1ll << 31), "pk_w4a16_strips_run: A beyond 2 GiB");
+  return strips_run(h->plan[M - 1], a, c, ldc, (hipStream_t)stream);
+}
+
+extern "C" void pk_w4a16_strips_release(void* prepared) {
+  delete static_cast<StripsPrepared*>(prepared);
 }

@@ -34,8 +34,9 @@ kernels stream in long runs (``pk_w4a16_gemm_tiled``). For decode, layers whose 
 it (``out % 16 == 0``, ``in % 128 == 0``, groups of a multiple of 32 that divide 128 or are
 multiples of it, or per-input scales: ``QuantLinear.decode``) keep a second copy of the codes
 and group scales in the strip layout (``_pk.strip_weights`` / ``strip_scales``: each
-16-output strip's inputs contiguous), and calls of at most ``DECODE_MAX_ROWS`` rows run the
-one-launch strip GEMV on it (``pk_w4a16_gemm_strips``). The int4 codes are a quarter of the
+16-output strip's inputs contiguous), and calls of at most ``decode_rows`` rows run the
+one-launch strip GEMV on it (``pk_w4a16_gemm_strips``; ``decode_rows``: 8 rows on layers of at
+most 4096 x 6144 weights). The int4 codes are a quarter of the
 fp16 weights' bytes, so both copies together are half of them; ``decode_layout=False`` keeps
 one copy. The copies are derived buffers, outside the state dict. ``codes()`` /
 ``set_codes()``, the state dict and the file format use ``pack_int4_n`` order either way.
@@ -65,8 +66,20 @@ FORMAT = "pico-kernels-amd/w4a16"
 FORMAT_VERSION = 2
 SCHEMES = ("group", "per_input")
 _OUT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
-# Rows up to which forward runs the strip-layout GEMV (when the layer keeps that copy).
+# Rows up to which forward runs the strip-layout GEMV (when the layer keeps that copy): 4, or
+# 8 on layers of at most 4096 x 6144 weights. Measured on MI355X (graphs over rotating weight
+# copies, against the block layout's kernels): M = 1..4 faster on every Llama-3-8B layer
+# (4096 x 11008 M = 4: 8.4 against 10.4 us); M = 8 faster on o_proj (5.5 against 7.7 us) and
+# qkv (7.9 against 9.0), slower on gate_up (14.7 against 12.8) and down (15.6 against 13.8).
 DECODE_MAX_ROWS = 4
+DECODE_MAX_ROWS_SMALL = 8
+DECODE_SMALL_WEIGHTS = 4096 * 6144
+
+
+def decode_rows(in_features: int, out_features: int) -> int:
+    """Rows up to which a layer of this shape runs its strip copy."""
+    small = in_features * out_features <= DECODE_SMALL_WEIGHTS
+    return DECODE_MAX_ROWS_SMALL if small else DECODE_MAX_ROWS
 
 
 class QuantLinear(nn.Module):
@@ -113,6 +126,8 @@ class QuantLinear(nn.Module):
         self.register_buffer("sstrips", torch.zeros_like(self.scales)
                              if self.decode and scheme == "group" else None, persistent=False)
         self._calls: dict = {}  # prepared strip-GEMV calls by output dtype (see _strips_call)
+        self._fast = None       # the fp16 one, for forward's decode fast path
+        self.decode_rows = decode_rows(in_features, out_features)
 
     # ---- construction -------------------------------------------------------------------
     @classmethod
@@ -204,29 +219,56 @@ class QuantLinear(nn.Module):
         return (q * self.scales.to(q.device)[:, None]).t()
 
     def _strips_call(self, out_dtype: torch.dtype) -> "_pk.PreparedStrips":
+        """The prepared strip-GEMV call for this output dtype (made on first use; dropped by
+        _refresh, by moves such as .to() and in copies, which rebuild it from their own
+        buffers)."""
         call = self._calls.get(out_dtype)
-        # (rebuilt when the copy is no longer this module's buffer: reassigned, or a deep copy)
         if call is None or call._keep[0] is not self.qstrips or call._keep[2] is not self.bias:
             scale = self._smax if self.scheme == "per_input" else 1.0
             call = _pk.PreparedStrips(self.qstrips, self.sstrips, self.group_size, scale, out_dtype,
                                       self.bias)
             self._calls[out_dtype] = call
+            if out_dtype == torch.float16 and self.scheme == "group":
+                self._fast = call
         return call
 
+    def _drop_calls(self) -> None:
+        self._calls = {}
+        self._fast = None
+
+    _PREPARED_FROM = frozenset(("qstrips", "sstrips", "bias", "scales", "qweight"))
+
+    def __setattr__(self, name, value):
+        # a prepared call holds the addresses of these buffers: reassigning one drops it
+        if name in QuantLinear._PREPARED_FROM and "_calls" in self.__dict__:
+            self._drop_calls()
+        super().__setattr__(name, value)
+
     def _apply(self, fn, *args, **kwargs):
-        self._calls = {}  # buffers may move: prepared calls hold their addresses
+        self._drop_calls()  # buffers may move: prepared calls hold their addresses
         return super()._apply(fn, *args, **kwargs)
 
+    def __getstate__(self):
+        # prepared calls are derived (and hold a C handle): copies and pickles rebuild them
+        state = super().__getstate__() if hasattr(super(), "__getstate__") else self.__dict__.copy()
+        state = dict(state)
+        state["_calls"], state["_fast"] = {}, None
+        return state
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # decode fast path: fp16 rows of a group layer with a strip copy, one prepared call
+        fast = self._fast
+        if (fast is not None and x.dim() == 2 and x.dtype == torch.float16
+                and x.shape[0] <= self.decode_rows and x.shape[1] == self.in_features):
+            return fast(x)
         assert x.shape[-1] == self.in_features
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.in_features)
         if (x2.dtype == torch.float16 and self.scheme == "group" and self.decode
-                and x2.shape[0] <= DECODE_MAX_ROWS):
-            # decode fast path: one prepared strip-GEMV call, no conversions
+                and x2.shape[0] <= self.decode_rows):
             return self._strips_call(torch.float16)(x2).view(*lead, self.out_features)
         out_dtype = x.dtype if x.dtype in _OUT_DTYPES else torch.float16
-        strips = self.decode and x2.shape[0] <= DECODE_MAX_ROWS
+        strips = self.decode and x2.shape[0] <= self.decode_rows
         # the bias is added in the matmul's epilogue (before the one rounding to out_dtype)
         if self.scheme == "per_input":
             # x * s / max s in fp16 (the input cast in the same pass), then max s in the epilogue
@@ -254,7 +296,7 @@ class QuantLinear(nn.Module):
     def _refresh(self) -> None:
         """Rebuild what derives from the buffers: the per-input epilogue scale and the decode
         copy in the strip layout (call after changing ``qweight`` or ``scales`` directly)."""
-        self._calls = {}
+        self._drop_calls()
         if self.scheme == "per_input":
             self._smax = float(self.scales.float().max().item())
         if self.decode:

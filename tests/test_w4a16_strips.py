@@ -213,7 +213,7 @@ def test_quant_linear_decode_copy_on_cpu():
 @pytest.mark.parametrize("scheme", ["group", "per_input"])
 @pytest.mark.parametrize("M", [1, 2, 4, 5, 8])
 def test_quant_linear_decode_rows_match_blocks(scheme, M, cuda):
-    """Up to DECODE_MAX_ROWS rows QuantLinear runs the strip copy: it agrees with the same layer
+    """Up to its decode_rows QuantLinear runs the strip copy: it agrees with the same layer
     without the copy (block layout) within the W4A16 bar; above that both run the same kernel
     bit for bit."""
     from torch import nn
@@ -234,7 +234,7 @@ def test_quant_linear_decode_rows_match_blocks(scheme, M, cuda):
     assert a.decode and not b.decode
     x = torch.randn(M, 1024, generator=_gen(M + 2)).half().to(cuda)
     ya, yb = a(x), b(x)
-    if M <= ql.DECODE_MAX_ROWS:
+    if M <= a.decode_rows:
         rel = (torch.linalg.norm(ya.float() - yb.float()) / torch.linalg.norm(yb.float())).item()
         assert rel <= 1e-3, rel
     else:
@@ -257,9 +257,40 @@ def test_quant_linear_prepared_call_follows_its_buffers(cuda):
     x = torch.randn(1, 512, device=cuda, dtype=torch.float16)
     y0 = q(x)
     twin = copy.deepcopy(q)
-    twin.set_codes(torch.zeros_like(twin.codes()))   # all-zero codes: output = bias
-    twin._refresh()
-    assert torch.equal(twin(x), twin.bias.expand(1, -1).to(torch.float16))
+    twin.set_codes(torch.zeros_like(twin.codes()))   # all-zero codes: output = bias (to the
+    twin._refresh()                                  # rounding of the biased-code offset)
+    yt = twin(x).float()
+    assert torch.allclose(yt, twin.bias.float().expand(1, -1), atol=1e-3, rtol=0)
+    assert not torch.allclose(yt, y0.float(), atol=1e-3, rtol=0)
     assert torch.equal(q(x), y0)                     # the original is untouched
     q2 = q.to(cuda)
     assert torch.equal(q2(x), y0)
+
+
+@pytest.mark.gpu
+def test_prepared_strips_handle(cuda):
+    """pk_w4a16_strips_prepare / _run give the bits of pk_w4a16_gemm_strips for every row count;
+    a bad fixed argument makes prepare return NULL with the reason; reassigning a QuantLinear's
+    bias rebuilds its prepared call."""
+    from torch import nn
+
+    import quant_linear as ql
+
+    K, N = 2048, 1024
+    a, codes, s16, words = _case(8, K, N, 128, 41)
+    qs = _pk.strip_weights(words).to(cuda)
+    ss = _pk.strip_scales(torch.from_numpy(s16)).to(cuda)
+    bias = torch.randn(N, generator=_gen(42)).half().to(cuda)
+    ag = a.to(cuda)
+    call = _pk.PreparedStrips(qs, ss, 128, 0.5, torch.float32, bias)
+    for M in range(1, 9):
+        ref = _pk.w4a16_gemm_strips(ag[:M], qs, ss, 128, 0.5, torch.float32, bias=bias)
+        assert torch.equal(call(ag[:M]), ref), M
+    with pytest.raises(_pk.PicoKernelsError, match="group_size"):
+        _pk.PreparedStrips(qs, ss, 96, 1.0, torch.float16)
+    lin = nn.Linear(K, N).to(cuda)
+    q = ql.QuantLinear.from_linear(lin, 128)
+    x = ag[:1].contiguous()
+    y0 = q(x)
+    q.bias = q.bias + 1.0
+    assert torch.allclose(q(x).float(), y0.float() + 1.0, atol=2e-3, rtol=0)
