@@ -3,23 +3,28 @@
 
 Headline workload: W4A16 decode GEMV, M=1, K=4096, N=11008, int4 group
 128 with fp16 scales, fp16 activations N(0,1), weights N(0, 0.02), seeded CPU generator.
-A "step" is one call over one activation row on the copy of the weights ``QuantLinear`` runs
-decode (up to ``QuantLinear.decode_rows`` rows) on: the strip layout (``pk_w4a16_gemm_strips``: each
-16-column strip's K rows contiguous, one workgroup per strip over the whole of K, one launch).
-The same call on ``QuantLinear``'s block layout (``pk_w4a16_gemm_tiled``, 128 x 256 blocks:
-the split-K GEMV, slices added in L2) and on ``pack_int4_n``'s row layout (``pk_w4a16_gemm``)
-is timed beside it. ``value`` is the whole-op HBM
-throughput (algorithmic bytes / step time), inputs resident in HBM. 40 distinct copies of the
-packed weights and scales (932 MB, more than twice the 256 MB Infinity Cache) are rotated:
-the W warm-up calls read copies 0..W-1, the timed graph starts at copy W and holds
-max(K, 80) calls, so it reads every copy at least twice and never starts on a copy the
-warm-up has just read.
+A "step" is one decode call over one activation row, made as ``QuantLinear`` makes it: the
+prepared strip GEMV (``_pk.PreparedStrips`` over ``pk_w4a16_strips_run``) on the layer's
+decode copy of the weights (the strip layout: each 16-column strip's K rows contiguous, one
+workgroup per strip over the whole of K, one launch). The same kernel through the generic
+binding (``pk_w4a16_gemm_strips``), and the same call on ``QuantLinear``'s block layout
+(``pk_w4a16_gemm_tiled``, 128 x 256 blocks: the split-K GEMV, slices added in L2) and on
+``pack_int4_n``'s row layout (``pk_w4a16_gemm``), are timed beside it. ``value`` is the
+whole-op HBM throughput (algorithmic bytes / step time), inputs resident in HBM. 40 distinct
+copies of the packed weights and scales (932 MB, more than twice the 256 MB Infinity Cache)
+are rotated: the W warm-up calls read copies 0..W-1, the timed calls start at copy W.
 
-Timing: W eager warm-up steps, then max(K, 80) steps captured in one HIP graph; untimed
-replays for 250 ms (the clocks settle under load), then 3 replays between HIP events on the
-graph's stream (device synchronisation around each replay); the best replay gives
-``ms_per_step``. Every timed line gets the same settling replays. The strip GEMV is one kernel
-launch, so the op is the dominant kernel and the roofline fraction uses its time.
+Timing (``eager_ms``): W eager warm-up steps, then eager steps for 250 ms (the clocks settle
+under load); then 5 repetitions of exactly K steps between two HIP events on the calls'
+stream. Before each repetition, 15 untimed calls read the 15 copies before the first timed
+one (350 MB, as the layers before it would in a decode loop), so a repetition never starts
+on weights its predecessor left in the caches, however small K is; then a spin kernel keeps
+the GPU busy while the host enqueues the timed calls (4.4 us of host time per call against
+6.4 us of kernel), so they run back to back. The median repetition gives ``ms_per_step``;
+the best, and the same K steps replayed as one HIP graph (which adds the graph's launch
+bubble, ~7 us per replay), are reported beside it. The strip GEMV is one kernel launch, so
+the op is the dominant kernel and the roofline fraction uses its time. The other lines
+replay HIP graphs (``GraphTimer``) after the same settling time.
 
 Correctness comes first: before any timing each GPU line checks its own output against the
 reference's test-path expression in fp32 torch on the GPU (unpack, multiply by the repeated
@@ -59,6 +64,8 @@ N_ROTATE = 40
 # (both layouts run the same kernels).
 ROW_LAYOUT = True
 WARM_MS = 250.0  # untimed graph replays before each timed measurement (GraphTimer.run)
+SPIN_CYCLES = 500_000  # spin ahead of each timed repetition: ~0.2 ms at the shader clock
+PREROLL = 15  # untimed calls on other weight copies ahead of each timed GEMV replay (350 MB)
 KERNEL_NAMES = {1: "w4a16_gemv_mfma_kernel", 2: "gemm_v3_f16_kernel", 3: "w4a16_skinny_kernel",
                 4: "w4a16_tr4_kernel", "strips": "w4a16_strip_kernel"}
 
@@ -87,6 +94,8 @@ class GraphTimer:
 
         self.stream = torch.cuda.Stream()
         self.steps = steps
+        self.fn = fn
+        self.start = max(warmup, 1)
         with torch.cuda.stream(self.stream):
             for i in range(max(warmup, 1)):
                 fn(i)
@@ -98,13 +107,22 @@ class GraphTimer:
                 fn(start + i)
         torch.cuda.synchronize()
 
-    def run(self, reps: int = 1, warm_ms: float = WARM_MS) -> float:
-        """Milliseconds per step (best of `reps` replays), after untimed replays for at least
-        `warm_ms` of wall time: the GPU's clocks settle under load over a few hundred
-        milliseconds, and without this the first configuration timed reads ~3% slow."""
+    def run(self, reps: int = 1, warm_ms: float = WARM_MS, preroll: int = 0) -> float:
+        """Milliseconds per step (median of `reps` replays; the best is kept in `self.best`),
+        after untimed replays for at least `warm_ms` of wall time: the GPU's clocks settle
+        under load over a few hundred milliseconds, and without this the first configuration
+        timed reads ~3% slow. With `preroll` > 0, the calls fn(start - preroll .. start - 1)
+        run eagerly (untimed) before every timed replay, as the calls before it in a decode
+        loop would: with fn rotating over weight copies by index modulo their count, these
+        are the copies just before the graph's first, so the replay starts with other weights
+        in the caches rather than the tail of its own previous replay. A short spin kernel
+        ahead of the start event keeps the GPU busy while the host enqueues the replay, so a
+        graph of a few calls is not timed with its launch latency."""
+        import statistics
+
         import torch
 
-        best = float("inf")
+        times = []
         with torch.cuda.stream(self.stream):
             t_end = time.perf_counter() + warm_ms * 1e-3
             while time.perf_counter() < t_end:
@@ -114,12 +132,62 @@ class GraphTimer:
                 e0 = torch.cuda.Event(enable_timing=True)
                 e1 = torch.cuda.Event(enable_timing=True)
                 torch.cuda.synchronize()
+                for j in range(preroll):
+                    self.fn(self.start - preroll + j)
+                torch.cuda._sleep(SPIN_CYCLES)
                 e0.record(self.stream)
                 self.graph.replay()
                 e1.record(self.stream)
                 torch.cuda.synchronize()
-                best = min(best, e0.elapsed_time(e1) / self.steps)
-        return best
+                times.append(e0.elapsed_time(e1) / self.steps)
+        self.best = min(times)
+        return statistics.median(times)
+
+
+def eager_ms(fn, steps: int, warmup: int, reps: int = 5, preroll: int = PREROLL,
+             warm_ms: float = WARM_MS) -> tuple[float, float]:
+    """Milliseconds per step of exactly `steps` eager calls fn(start .. start + steps - 1)
+    (start = max(warmup, 1)) between two HIP events on a private stream: (median, best) of
+    `reps` repetitions. Before the timing: the warm-up calls fn(0 .. warmup - 1), then calls
+    for `warm_ms` of wall time (the clocks settle under load). Before each repetition: the
+    calls fn(start - preroll .. start - 1), untimed, as the calls before them in a decode loop
+    would (with fn rotating over weight copies by index modulo their count, the copies just
+    before the timed ones), then a spin kernel of SPIN_CYCLES, during which the host enqueues
+    the timed calls ahead of the GPU. For a call whose host cost is below its kernel time
+    the GPU then runs the timed calls back to back; a graph replay would add its launch
+    bubble (~7 us here) to every repetition."""
+    import statistics
+
+    import torch
+
+    stream = torch.cuda.Stream()
+    start = max(warmup, 1)
+    times = []
+    with torch.cuda.stream(stream):
+        for i in range(start):
+            fn(i)
+        torch.cuda.synchronize()
+        t_end = time.perf_counter() + warm_ms * 1e-3
+        i = start
+        while time.perf_counter() < t_end:
+            for _ in range(64):
+                fn(i)
+                i += 1
+            torch.cuda.synchronize()
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            for j in range(preroll):
+                fn(start - preroll + j)
+            torch.cuda._sleep(SPIN_CYCLES)
+            e0.record(stream)
+            for j in range(steps):
+                fn(start + j)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / steps)
+    return statistics.median(times), min(times)
 
 
 def per_launch_ms(fn, n: int) -> float:
@@ -253,7 +321,13 @@ def bench_gemv(args, dev) -> dict:
     nbytes = w4a16_bytes(M, K, N)
     kid, split = _pk.w4a16_plan(M, N, K, 128, 0)
 
-    def step(i):  # QuantLinear's decode layout: strips
+    # QuantLinear's decode call: a prepared strip GEMV per layer (here per weight copy)
+    calls = [_pk.PreparedStrips(q, sc, 128, 1.0, torch.float16) for q, sc in zip(qss, sss)]
+
+    def step(i):
+        calls[i % N_ROTATE](ag, out)
+
+    def step_binding(i):  # the same kernel through the generic binding
         _pk.w4a16_gemm_strips(ag, qss[i % N_ROTATE], sss[i % N_ROTATE], 128, 1.0,
                               torch.float16, out=out)
 
@@ -272,21 +346,29 @@ def bench_gemv(args, dev) -> dict:
         return call
 
     check = check_w4a16(once(step), ag, qws[0], scs[0])
+    y_strips = out.clone()
+    check_w4a16(once(step_binding), ag, qws[0], scs[0])
+    check["bitwise_equal_to_binding"] = bool(torch.equal(y_strips, out))
+    if not check["bitwise_equal_to_binding"]:
+        raise RuntimeError("W4A16 GEMV: prepared call and binding disagree")
     check_blocks = check_w4a16(once(step_blocks), ag, qws[0], scs[0])
     y_blocks = out.clone()
     check_rows = check_w4a16(once(step_rows), ag, qws[0], scs[0])
     check_blocks["bitwise_equal_to_row_layout"] = bool(torch.equal(y_blocks, out))
     if not check_blocks["bitwise_equal_to_row_layout"]:
         raise RuntimeError("W4A16 GEMV: block and row layouts disagree")
-    timed = max(args.steps, 2 * N_ROTATE)
-    ms = GraphTimer(step, timed, args.warmup).run(reps=3)
-    ms_blocks = GraphTimer(step_blocks, timed, args.warmup).run(reps=3) if ROW_LAYOUT else None
-    ms_rows = GraphTimer(step_rows, timed, args.warmup).run(reps=3) if ROW_LAYOUT else None
+    timed = args.steps  # exactly K steps per repetition
+    ms, ms_best = eager_ms(step, timed, args.warmup)
+    ms_graph = GraphTimer(step, timed, args.warmup).run(reps=5, preroll=PREROLL)
+    ms_blocks = (GraphTimer(step_blocks, timed, args.warmup).run(reps=5, preroll=PREROLL)
+                 if ROW_LAYOUT else None)
+    ms_rows = (GraphTimer(step_rows, timed, args.warmup).run(reps=5, preroll=PREROLL)
+               if ROW_LAYOUT else None)
 
-    # The op is one launch of the strip kernel: the graph's per-step time is that kernel's
-    # average launch duration (HIP events around the replay on the launch stream; agrees with
-    # rocprof's kernel-trace average). Single launches bracketed by their own events read
-    # ~1.5 us longer (event overhead) and are reported beside it.
+    # The op is one launch of the strip kernel: the timed calls' per-step time is that kernel's
+    # average launch duration (HIP events around the calls on the launch stream). Single
+    # launches bracketed by their own events read ~2.5 us longer (event overhead) and are
+    # reported beside it.
     ms_kernel = ms
     ms_kernel_events = per_launch_ms(step, min(timed, 500))
 
@@ -304,18 +386,21 @@ def bench_gemv(args, dev) -> dict:
         "blocks_layout_plan": {"kernel_id": kid, "split": split,
                                "launches": _pk.w4a16_launches(M, N, K, 128, 0)},
         "bytes": nbytes, "steps_timed": timed, "check": check, "check_blocks": check_blocks,
-        "check_rows": check_rows, "ms_per_step": ms, "ms_blocks": ms_blocks, "ms_rows": ms_rows,
+        "check_rows": check_rows, "ms_per_step": ms, "ms_per_step_best": ms_best,
+        "ms_graph": ms_graph,
+        "ms_blocks": ms_blocks, "ms_rows": ms_rows,
         "ms_kernel": ms_kernel, "ms_kernel_events": ms_kernel_events,
-        "split_sweep_GBs": sweep, "host": host_times(ag, qws[0], scs[0], qss[0], sss[0], out, step),
+        "split_sweep_GBs": sweep,
+        "host": host_times(ag, qws[0], scs[0], qss[0], sss[0], out, step_binding),
         "inputs": (ag, qws[0], scs[0]),
     }
 
 
 def host_times(ag, qw, sc, qs, ss, out, step) -> dict:
     """Eager host cost of one decode call at M = 1 (see host_overhead), three ways: the generic
-    binding (``_pk.w4a16_gemm_strips``, the timed step), the prepared call QuantLinear keeps per
-    layer (``_pk.PreparedStrips``, output given), and ``QuantLinear.forward`` itself (its output
-    allocated per call)."""
+    binding (``_pk.w4a16_gemm_strips``), the prepared call QuantLinear keeps per layer
+    (``_pk.PreparedStrips``, output given: the timed step), and ``QuantLinear.forward`` itself
+    (its output allocated per call)."""
     import _pk
     import quant_linear
 
@@ -374,9 +459,10 @@ def bench_prefill(dev, iters: int = 50, M: int = 2048) -> dict:
 
 def bench_fp8(dev, iters: int = 50, M: int = 4096) -> dict:
     """fp8 e4m3 GEMM at M x 4096 x 4096 (fp16 out). Checked first: relative Frobenius error of
-    this output against the fp32 product, beside the same error of the reference's own fp8
-    expression ``(a8.float() @ b8.float()) * out_scale`` (tests/test_gemm_fp8.py:24), and a
-    bitwise repeat."""
+    this output against the fp32 product (the reference test's comparison,
+    tests/test_gemm_fp8.py:24), beside the same error of the reference kernel's arithmetic in
+    fp32 torch, ``(a8.float() @ b8.float()) * out_scale`` with out_scale = 1 / (a_scale *
+    b_scale) (gemm_fp8.py:98-117), and a bitwise repeat."""
     import torch
 
     import _pk
@@ -620,8 +706,9 @@ def cpu_w4a16(a, qw, sc, y_gpu=None, group: int = 128, runs: int = 5) -> dict:
 
 
 def cpu_fp8(a8, b8, scale: float, runs: int = 5) -> dict:
-    """The reference's fp8 CPU path in torch on the host: e4m3 bytes to fp32, fp32 matmul,
-    times the output scale (tests/test_gemm_fp8.py:24); timed like cpu_w4a16."""
+    """The fp8 call on the host in torch (the reference has no CPU fp8 path; its test compares
+    with the fp16 product, tests/test_gemm_fp8.py:24): e4m3 bytes to fp32, fp32 matmul,
+    times the output scale; timed like cpu_w4a16."""
     ac, bc = a8.cpu(), b8.cpu()
     M, K = ac.shape
     N = bc.shape[1]
@@ -964,6 +1051,8 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(g["ms_per_step"], 5),
+        "ms_per_step_best": round(g["ms_per_step_best"], 5),
+        "ms_per_step_graph": round(g["ms_graph"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -973,8 +1062,9 @@ def main() -> int:
                 "strip's K rows contiguous); "
                 f"{N_ROTATE} copies of the packed weights and scales rotated "
                 f"({N_ROTATE * g['bytes'] / 1e6:.0f} MB > 2x the 256 MB Infinity Cache): warm-up "
-                f"reads copies 0..{args.warmup - 1}, the timed graph {g['steps_timed']} calls "
-                f"from copy {max(args.warmup, 1) % N_ROTATE} on, best of 3 replays",
+                f"reads copies 0..{args.warmup - 1}, the timed {g['steps_timed']} calls start "
+                f"at copy {max(args.warmup, 1) % N_ROTATE}, each timed repetition after "
+                f"{PREROLL} untimed calls on the copies before it, median of 5 repetitions",
         "config": {"workload": "w4a16_decode_gemv", "M": g["M"], "K": g["K"], "N": g["N"],
                    "group_size": 128, "split_k": 1, "out_dtype": "fp16",
                    "weights": "16-column strips (QuantLinear's decode copy, pk_w4a16_gemm_strips): "
@@ -1007,9 +1097,11 @@ def main() -> int:
         table = cpu_baseline_table(dev, g["inputs"])
         head = table["rows"]["w4a16_1x4096x11008"]
         result["cpu_baseline"] = {
-            "value": head["GB/s"], "unit": "GB/s", "cores": table["torch_threads"], "kind": "port",
-            "sample": "the reference's CPU path in torch on the host (unpack + group dequant, then "
-                      "a.float() @ deq) on the headline's own inputs: median of 5 after a warm-up, "
+            "value": head["GB/s"], "unit": "GB/s", "cores": table["torch_threads"],
+            "kind": "reference",
+            "sample": "the reference's own CPU path, its tests' torch expression (unpack + group "
+                      "dequant, then a.float() @ deq, tests/test_gemm_int4.py:26) run by torch on "
+                      "the host, on the headline's own inputs: median of 5 after a warm-up, "
                       f"dequant {head['dequant_ms']} ms + matmul {head['matmul_ms']} ms, "
                       f"together {head['total_ms']} ms",
             "ms_per_step": head["total_ms"], "table": table}
@@ -1018,13 +1110,19 @@ def main() -> int:
                 if entry["workload"] == "w4a16_prefill_gemm":
                     r = table["rows"]["w4a16_2048x4096x4096"]
                     entry["cpu_baseline"] = {"value": round(r["GFLOP/s"] / 1e3, 4), "unit": "TFLOP/s",
-                                             "cores": table["torch_threads"], "kind": "port",
-                                             "sample": f"torch dequant + fp32 matmul, median of 5: {r['total_ms']} ms"}
+                                             "cores": table["torch_threads"], "kind": "reference",
+                                             "sample": "the reference's test expression "
+                                                       "(tests/test_gemm_int4.py:26) in torch on "
+                                                       "the host: dequant + fp32 matmul, median "
+                                                       f"of 5: {r['total_ms']} ms"}
                 elif entry["workload"] == "fp8_e4m3_gemm":
                     r = table["rows"]["fp8_4096^3"]
                     entry["cpu_baseline"] = {"value": round(r["GFLOP/s"] / 1e3, 4), "unit": "TFLOP/s",
                                              "cores": table["torch_threads"], "kind": "port",
-                                             "sample": f"torch e4m3->fp32 + fp32 matmul, median of 5: {r['total_ms']} ms"}
+                                             "sample": "the fp8 call's own semantics in torch on "
+                                                       "the host (the reference has no CPU fp8 "
+                                                       "path): e4m3->fp32, fp32 matmul, times the "
+                                                       f"output scale, median of 5: {r['total_ms']} ms"}
                 elif entry["workload"] == "split_kv_decode_attention":
                     entry["cpu_baseline"] = cpu_baseline_decode()
                 elif entry["workload"] == "gptq_layer":
