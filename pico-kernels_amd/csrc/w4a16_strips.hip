@@ -78,6 +78,14 @@ constexpr int kStripWaveScLds = 1024;
 __host__ __device__ __forceinline__ int strip_wave_lds(int M, int U, bool gs) {
   return strip_wave_act_lds(M, U) + (gs ? kStripWaveScLds : 0);
 }
+// A wave's partial sums for the end fold: 4 row sets x MT rows x 16 columns of fp32. With
+// ALDS they overwrite the wave's own activation region (at least M * 256 bytes, rounded up to
+// 1 KB, which holds the MT * 256 bytes whenever M > MT / 2); otherwise each wave has a
+// region of this size.
+__host__ __device__ __forceinline__ int strip_fold_lds(int MT) { return 4 * MT * 64; }
+__host__ __device__ __forceinline__ int strip_wave_stride(int M, int MT, int U, bool gs, bool alds) {
+  return alds ? strip_wave_lds(M, U, gs) : strip_fold_lds(MT);
+}
 
 // 16 bytes per lane, global -> LDS: lane L writes lds + 16 L.
 __device__ __forceinline__ void strip_dma16(__amdgpu_buffer_rsrc_t r, char* lds, int voff) {
@@ -87,12 +95,13 @@ __device__ __forceinline__ void strip_dma16(__amdgpu_buffer_rsrc_t r, char* lds,
 // MT: activation rows the kernel carries (1, 2, 4 or 8); U: 1 KB blocks per wave per round.
 // ALDS: each wave DMAs its round's activations and scales into its own LDS region ahead of
 // its weight loads and reads them from there (M * U <= 32); otherwise every lane loads its
-// own from global memory.
+// own from global memory. Up to 16 waves per workgroup (the 8-row kernel runs U = 2 only,
+// which keeps it within the 128 registers that allows).
 template <int MT, int U, bool HAS_GS, bool ALDS>
-__global__ __launch_bounds__(MT > 4 ? 512 : 64 * kStripMaxWaves) void w4a16_strip_kernel(StripParams p) {
+__global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripParams p) {
   constexpr int MS = MT > 4 ? 2 : 1;            // MFMA sets of four activation rows
   constexpr int RR = MT < 4 ? MT : 4;           // registers of a set that carry rows
-  extern __shared__ __align__(16) char strip_lds[];  // ALDS: one region per wave
+  extern __shared__ __align__(16) char strip_lds[];  // one region per wave
   // Workgroup b runs on XCD b % 8 (round-robin dispatch): XCD x takes the contiguous strips
   // [x * spx, (x + 1) * spx), so each 128-byte line of the output is written from one L2.
   const int s = (int)(blockIdx.x & 7) * p.spx + (int)(blockIdx.x >> 3);
@@ -173,6 +182,11 @@ __global__ __launch_bounds__(MT > 4 ? 512 : 64 * kStripMaxWaves) void w4a16_stri
               w_sc + cps * 8 + (strip_group(p, b * kStripBlockRows + 32 * rs) - g0) * (kStripCols * 2));
       }
     }
+    // Every load of the round issues before the products: left to itself the scheduler sinks
+    // later blocks' scale and activation loads below earlier blocks' products (to reuse their
+    // registers), and each round then waits a memory latency in its middle (measured at 8 rows
+    // on MI355X: 4096 x 11008 14.0 -> 11.0 us, 14336 x 4096 12.5 -> 11.7 us).
+    if constexpr (!ALDS) __builtin_amdgcn_sched_barrier(0);
     // ---- products, in block order -------------------------------------------------------
 #pragma unroll
     for (int i = 0; i < U; ++i) {
@@ -230,15 +244,20 @@ __global__ __launch_bounds__(MT > 4 ? 512 : 64 * kStripMaxWaves) void w4a16_stri
   // writes its 4 row sets; then thread (m, part, col) adds the partials of waves
   // part, part + 4, ... (row sets 0..3 each), and the four parts are added by two shuffles:
   // ((part 0 + part 1) + (part 2 + part 3)), the same tree on every call.
-  __shared__ pk_f4 red[kStripMaxWaves][4][MT][kStripCols / 4];
+  // red(w)[rs][m][cps]: wave w's partials, in its own region (after its last LDS reads of
+  // staged activations: a wave's LDS accesses complete in order).
+  const int wstride = strip_wave_stride(p.M, MT, U, HAS_GS, ALDS);
+  auto red = [&](int w, int set, int m, int q) {
+    return reinterpret_cast<pk_f4*>(strip_lds + w * wstride) + (set * MT + m) * (kStripCols / 4) + q;
+  };
   if ((lane >> 4) == rs) {
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
       for (int r = 0; r < RR; ++r)
         if (4 * ms + r < MT)
-          red[wave][rs][4 * ms + r][cps] = pk_f4{acc_lo[ms][0][r], acc_hi[ms][0][r],
-                                                 acc_lo[ms][1][r], acc_hi[ms][1][r]};
+          *red(wave, rs, 4 * ms + r, cps) = pk_f4{acc_lo[ms][0][r], acc_hi[ms][0][r],
+                                                  acc_lo[ms][1][r], acc_hi[ms][1][r]};
   }
   __syncthreads();
   const int rows = p.M < MT ? p.M : MT;
@@ -253,7 +272,7 @@ __global__ __launch_bounds__(MT > 4 ? 512 : 64 * kStripMaxWaves) void w4a16_stri
         const bool live = part + 4 * k < p.nw;
         float q4[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) q4[q] = red[wv][q][m][col >> 2][col & 3];
+        for (int q = 0; q < 4; ++q) q4[q] = (*red(wv, q, m, col >> 2))[col & 3];
 #pragma unroll
         for (int q = 0; q < 4; ++q) v += live ? q4[q] : 0.0f;
       }
@@ -285,16 +304,22 @@ bool strips_shape_ok(int M, int N, int K, int group, bool has_gs) {
 // 4096 x 14336: 8.98 / 7.76 / 8.07; 4096 x 4096: 4.29 / 4.23 / 4.06; 14336 x 4096: 7.53 /
 // 7.62 / 8.12): 4 (8 waves per workgroup at K = 4096), 8 where the strips leave at most one
 // workgroup per CU, 2 for deep layers (K > 8192: 16 waves, several rounds). More than two
-// rows take at most 4 (the 4-row kernel spills with 8), eight rows at most 2 (their
-// activation and accumulator registers double).
+// rows take at most 4 (the 4-row kernel spills with 8); more than four rows take 2 (the 8-row
+// kernel's activation and accumulator registers double), whatever the configuration says.
 static int strips_pick_u(int M, int N, int kb) {
+  if (M > 4) return 2;
   int u = kb > 64 ? 2 : (N / kStripCols <= 256 ? 8 : 4);
   if (g_strip_u) u = g_strip_u;
   if (M > 2 && u > 4) u = 4;
-  if (M > 4 && u > 2) u = 2;
   while (u > 2 && kb / u < 4) u /= 2;
   return u;
 }
+
+// 5..8 rows: 8 waves per workgroup, each lane loading its own activations and scales (no LDS
+// staging). Measured on MI355X at M = 8 against 4 and 16 waves and against staging (graphs over
+// rotating weight copies; 4096 x 6144 / 4096 x 4096 / 4096 x 14336 / 14336 x 4096 / 4096 x
+// 11008): 8.09 / 5.56 / 13.3 / 11.7 / 10.9 us; staged, 9.4 / 7.3 / 16.8 / 19.5 / 14.2.
+constexpr int kStripWaves8 = 8;
 
 // Activations and scales staged per wave in LDS: at most 8 KB of activations per wave
 // (M * U <= 32) and the wave's group-scale rows within one 1 KB DMA (at most 32 groups).
@@ -334,17 +359,16 @@ static void strips_plan(const uint8_t* qs, const void* ss, int group, OutEpi epi
   p.K = K;
   p.kb = K / kStripBlockRows;
   const int u = strips_pick_u(M, N, p.kb);
-  const int max_waves = M > 4 ? 8 : kStripMaxWaves;  // the 8-row kernel's launch bound
   const int waves_one_round = (int)cdiv(p.kb, u);
+  const int max_waves = M > 4 ? kStripWaves8 : kStripMaxWaves;
   p.nw = waves_one_round < max_waves ? waves_one_round : max_waves;
   p.iters = (int)cdiv(p.kb, (int64_t)u * p.nw);
-  // (the static fold array takes 16 waves x 4 row sets x rows x 64 bytes)
-  const size_t lds_alds = (size_t)p.nw * strip_wave_lds(M, u, ss != nullptr);
+  const bool gs = ss != nullptr;
   const int mt = M == 1 ? 1 : M == 2 ? 2 : M <= 4 ? 4 : 8;
   pl->u = u;
-  pl->alds = strips_alds(M, u, p.group, ss != nullptr) &&
-             lds_alds + (size_t)kStripMaxWaves * 4 * mt * 64 <= (64u << 10);
-  pl->lds = pl->alds ? lds_alds : 0;
+  pl->alds = M <= 4 && strips_alds(M, u, p.group, gs) &&
+             (size_t)p.nw * strip_wave_lds(M, u, gs) <= (64u << 10);
+  pl->lds = (size_t)p.nw * strip_wave_stride(M, mt, u, gs, pl->alds);
   p.spx = (int)cdiv(N / kStripCols, 8);
   pl->grid = dim3(8 * p.spx);
   pl->block = dim3(64 * p.nw);
@@ -364,17 +388,18 @@ static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, 
     else w4a16_strip_kernel<mt, uu, false, al><<<pl.grid, pl.block, pl.lds, stream>>>(p);
   };
   auto by_u = [&](auto MTc, auto AL) {
-    if (u == 2) go(MTc, pk_int_c<2>{}, AL);
+    if constexpr (decltype(MTc)::value == 8) go(MTc, pk_int_c<2>{}, AL);  // U = 2 only
+    else if (u == 2) go(MTc, pk_int_c<2>{}, AL);
     else if (u == 4) go(MTc, pk_int_c<4>{}, AL);
     else go(MTc, pk_int_c<8>{}, AL);
   };
   auto by_m = [&](auto AL) {
     if (M == 1) by_u(pk_int_c<1>{}, AL);
     else if (M == 2) by_u(pk_int_c<2>{}, AL);
-    else if (M <= 4) by_u(pk_int_c<4>{}, AL);
-    else by_u(pk_int_c<8>{}, AL);
+    else by_u(pk_int_c<4>{}, AL);
   };
-  if (pl.alds) by_m(pk_int_c<1>{});
+  if (M > 4) by_u(pk_int_c<8>{}, pk_int_c<0>{});  // eight rows: never staged
+  else if (pl.alds) by_m(pk_int_c<1>{});
   else by_m(pk_int_c<0>{});
   PK_LAUNCH_CHECK("w4a16 gemv (strip layout)");
   return PK_OK;

@@ -66,20 +66,21 @@ FORMAT = "pico-kernels-amd/w4a16"
 FORMAT_VERSION = 2
 SCHEMES = ("group", "per_input")
 _OUT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
-# Rows up to which forward runs the strip-layout GEMV (when the layer keeps that copy): 4, or
-# 8 on layers of at most 4096 x 6144 weights. Measured on MI355X (graphs over rotating weight
-# copies, against the block layout's kernels): M = 1..4 faster on every Llama-3-8B layer
-# (4096 x 11008 M = 4: 8.4 against 10.4 us); M = 8 faster on o_proj (5.5 against 7.7 us) and
-# qkv (7.9 against 9.0), slower on gate_up (14.7 against 12.8) and down (15.6 against 13.8).
-DECODE_MAX_ROWS = 4
-DECODE_MAX_ROWS_SMALL = 8
-DECODE_SMALL_WEIGHTS = 4096 * 6144
+# Rows up to which forward runs the strip-layout GEMV (when the layer keeps that copy): 8, or 4
+# on layers of more than 768 strips of 16 output columns. Measured on MI355X (graphs over
+# rotating weight copies, against the block layout's kernels): M = 1..4 faster on every
+# Llama-3-8B layer (4096 x 11008 M = 4: 8.5 against 10.4 us); M = 8 faster on qkv (8.1 against
+# 9.0), o_proj (5.6 against 7.7), down (11.7 against 13.7) and 4096 x 11008 (10.9 against 12.2),
+# slower on gate_up, 4096 x 14336 (13.3 against 12.7).
+DECODE_MAX_ROWS = 8
+DECODE_MAX_ROWS_WIDE = 4
+DECODE_WIDE_STRIPS = 768
 
 
 def decode_rows(in_features: int, out_features: int) -> int:
     """Rows up to which a layer of this shape runs its strip copy."""
-    small = in_features * out_features <= DECODE_SMALL_WEIGHTS
-    return DECODE_MAX_ROWS_SMALL if small else DECODE_MAX_ROWS
+    wide = out_features // 16 > DECODE_WIDE_STRIPS
+    return DECODE_MAX_ROWS_WIDE if wide else DECODE_MAX_ROWS
 
 
 class QuantLinear(nn.Module):
