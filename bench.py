@@ -15,14 +15,17 @@ copies of the packed weights and scales (932 MB, more than twice the 256 MB Infi
 are rotated: the W warm-up calls read copies 0..W-1, the timed calls start at copy W.
 
 Timing (``eager_ms``): W eager warm-up steps, then eager steps for 250 ms (the clocks settle
-under load); then 5 repetitions of exactly K steps between two HIP events on the calls'
-stream. Before each repetition, 15 untimed calls read the 15 copies before the first timed
-one (350 MB, as the layers before it would in a decode loop), so a repetition never starts
-on weights its predecessor left in the caches, however small K is; then a spin kernel keeps
-the GPU busy while the host enqueues the timed calls (4.4 us of host time per call against
-6.4 us of kernel), so they run back to back. The median repetition gives ``ms_per_step``;
-the best, and the same K steps replayed as one HIP graph (which adds the graph's launch
-bubble, ~7 us per replay), are reported beside it. The strip GEMV is one kernel launch, so
+under load); then 5 repetitions of exactly K steps. Before each repetition, 15 untimed calls
+read the 15 copies before the first timed one (350 MB, as the layers before it would in a
+decode loop), so a repetition never starts on weights its predecessor left in the caches,
+however small K is; then a spin kernel keeps the GPU busy while the host enqueues the timed
+calls (4.4 us of host time per call against 6.4 us of kernel), so they run back to back.
+The timed region runs from the first timed kernel's start to the last one's end: HIP events
+on the calls' stream that the first and last dispatches record themselves
+(``pk_w4a16_strips_run_events``), so no event packet sits inside it. The median repetition
+gives ``ms_per_step``; the best, the same K steps between two event packets on the stream
+(~4.5 us more per repetition), and the same K steps replayed as one HIP graph (which adds
+the graph's launch bubble, ~7 us per replay) are reported beside it. The strip GEMV is one kernel launch, so
 the op is the dominant kernel and the roofline fraction uses its time. The other lines
 replay HIP graphs (``GraphTimer``) after the same settling time.
 
@@ -145,7 +148,7 @@ class GraphTimer:
 
 
 def eager_ms(fn, steps: int, warmup: int, reps: int = 5, preroll: int = PREROLL,
-             warm_ms: float = WARM_MS) -> tuple[float, float]:
+             warm_ms: float = WARM_MS, fn_timed=None) -> dict:
     """Milliseconds per step of exactly `steps` eager calls fn(start .. start + steps - 1)
     (start = max(warmup, 1)) between two HIP events on a private stream: (median, best) of
     `reps` repetitions. Before the timing: the warm-up calls fn(0 .. warmup - 1), then calls
@@ -155,7 +158,15 @@ def eager_ms(fn, steps: int, warmup: int, reps: int = 5, preroll: int = PREROLL,
     before the timed ones), then a spin kernel of SPIN_CYCLES, during which the host enqueues
     the timed calls ahead of the GPU. For a call whose host cost is below its kernel time
     the GPU then runs the timed calls back to back; a graph replay would add its launch
-    bubble (~7 us here) to every repetition."""
+    bubble (~7 us here) to every repetition.
+
+    Returns the median and best milliseconds per step between two event packets recorded on
+    the stream around the calls ("markers": they add ~4.5 us per repetition, 0.22 us per step
+    at K = 20). With ``fn_timed(i, start, stop)`` -- fn(i) with the dispatch itself recording
+    the events as its kernel starts and ends -- each repetition is also run with the first
+    call recording its kernel's start and the last its kernel's end ("kernels": the GPU time
+    from the first timed kernel's start to the last one's end, the launches between them
+    back to back as before)."""
     import statistics
 
     import torch
@@ -174,6 +185,7 @@ def eager_ms(fn, steps: int, warmup: int, reps: int = 5, preroll: int = PREROLL,
                 fn(i)
                 i += 1
             torch.cuda.synchronize()
+        times_k = []
         for _ in range(reps):
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
@@ -187,7 +199,27 @@ def eager_ms(fn, steps: int, warmup: int, reps: int = 5, preroll: int = PREROLL,
             e1.record(stream)
             torch.cuda.synchronize()
             times.append(e0.elapsed_time(e1) / steps)
-    return statistics.median(times), min(times)
+            if fn_timed is None:
+                continue
+            k0 = torch.cuda.Event(enable_timing=True)
+            k1 = torch.cuda.Event(enable_timing=True)
+            k0.record(stream)  # creates both events before the dispatches record them
+            k1.record(stream)
+            torch.cuda.synchronize()
+            for j in range(preroll):
+                fn(start - preroll + j)
+            torch.cuda._sleep(SPIN_CYCLES)
+            for j in range(steps):
+                if j == 0 or j == steps - 1:
+                    fn_timed(start + j, k0 if j == 0 else None, k1 if j == steps - 1 else None)
+                else:
+                    fn(start + j)
+            torch.cuda.synchronize()
+            times_k.append(k0.elapsed_time(k1) / steps)
+    res = {"markers": statistics.median(times), "markers_best": min(times)}
+    if times_k:
+        res.update(kernels=statistics.median(times_k), kernels_best=min(times_k))
+    return res
 
 
 def per_launch_ms(fn, n: int) -> float:
@@ -327,6 +359,9 @@ def bench_gemv(args, dev) -> dict:
     def step(i):
         calls[i % N_ROTATE](ag, out)
 
+    def step_timed(i, start, stop):  # the same call, its dispatch recording start / stop
+        calls[i % N_ROTATE].timed(ag, out, start, stop)
+
     def step_binding(i):  # the same kernel through the generic binding
         _pk.w4a16_gemm_strips(ag, qss[i % N_ROTATE], sss[i % N_ROTATE], 128, 1.0,
                               torch.float16, out=out)
@@ -358,7 +393,9 @@ def bench_gemv(args, dev) -> dict:
     if not check_blocks["bitwise_equal_to_row_layout"]:
         raise RuntimeError("W4A16 GEMV: block and row layouts disagree")
     timed = args.steps  # exactly K steps per repetition
-    ms, ms_best = eager_ms(step, timed, args.warmup)
+    em = eager_ms(step, timed, args.warmup, fn_timed=step_timed)
+    ms, ms_best = em["kernels"], em["kernels_best"]
+    ms_markers = em["markers"]
     ms_graph = GraphTimer(step, timed, args.warmup).run(reps=5, preroll=PREROLL)
     ms_blocks = (GraphTimer(step_blocks, timed, args.warmup).run(reps=5, preroll=PREROLL)
                  if ROW_LAYOUT else None)
@@ -366,9 +403,9 @@ def bench_gemv(args, dev) -> dict:
                if ROW_LAYOUT else None)
 
     # The op is one launch of the strip kernel: the timed calls' per-step time is that kernel's
-    # average launch duration (HIP events around the calls on the launch stream). Single
-    # launches bracketed by their own events read ~2.5 us longer (event overhead) and are
-    # reported beside it.
+    # average launch duration (from the first timed kernel's start to the last one's end, on
+    # the launch stream). Single launches bracketed by their own event packets read ~2.5 us
+    # longer and are reported beside it.
     ms_kernel = ms
     ms_kernel_events = per_launch_ms(step, min(timed, 500))
 
@@ -387,7 +424,7 @@ def bench_gemv(args, dev) -> dict:
                                "launches": _pk.w4a16_launches(M, N, K, 128, 0)},
         "bytes": nbytes, "steps_timed": timed, "check": check, "check_blocks": check_blocks,
         "check_rows": check_rows, "ms_per_step": ms, "ms_per_step_best": ms_best,
-        "ms_graph": ms_graph,
+        "ms_graph": ms_graph, "ms_markers": ms_markers,
         "ms_blocks": ms_blocks, "ms_rows": ms_rows,
         "ms_kernel": ms_kernel, "ms_kernel_events": ms_kernel_events,
         "split_sweep_GBs": sweep,
@@ -1053,6 +1090,7 @@ def main() -> int:
         "ms_per_step": round(g["ms_per_step"], 5),
         "ms_per_step_best": round(g["ms_per_step_best"], 5),
         "ms_per_step_graph": round(g["ms_graph"], 5),
+        "ms_per_step_event_packets": round(g["ms_markers"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

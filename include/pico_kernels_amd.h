@@ -216,6 +216,14 @@ void* pk_w4a16_strips_prepare(const uint8_t* qstrips, const void* sstrips, int g
 int pk_w4a16_strips_run(void* prepared, const void* a, void* c, int64_t ldc, int M, void* stream);
 void pk_w4a16_strips_release(void* prepared);
 
+/* pk_w4a16_strips_run with timing: the dispatch itself records start_event (a hipEvent_t) as
+ * the kernel starts and stop_event as it ends (either may be NULL; both must exist already),
+ * so a run of calls can be timed from its first kernel's start to its last kernel's end with
+ * no event packet of its own between them. Same launch, same bits. For measurement; no
+ * counterpart in the reference. */
+int pk_w4a16_strips_run_events(void* prepared, const void* a, void* c, int64_t ldc, int M,
+                               void* stream, void* start_event, void* stop_event);
+
 /* Rows per kernel call of pk_w4a16_gemm_tiled for M activation rows of stride lda elements:
  * M itself while the activations span less than 2 GiB (M * lda * 2 bytes); beyond that the
  * call runs equal chunks of this many rows (a multiple of 128), since the kernels that read

@@ -64,6 +64,7 @@ _SIGNATURES = {
     "pk_w4a16_strips_config": (_i32, [_i32]),
     "pk_w4a16_strips_prepare": (_vp, [_vp, _vp, _i32, _f32, _vp, _i32, _i32, _i32, _i32, _i64]),
     "pk_w4a16_strips_run": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp]),
+    "pk_w4a16_strips_run_events": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp]),
     "pk_w4a16_strips_release": (None, [_vp]),
     "pk_w4a16_skinny_layout": (_i32, [_i32, _i32]),
     "pk_w4a16_prep_activations": (_i32, [_vp, _i32, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _vp]),
@@ -427,7 +428,7 @@ class PreparedStrips:
     row stride ``lda`` (elements; default K). The tensors stay referenced here, and must stay
     in place, while the object lives (QuantLinear drops it when its buffers move or change)."""
 
-    __slots__ = ("h", "N", "K", "lda", "out_dtype", "dev", "run", "release", "_keep")
+    __slots__ = ("h", "N", "K", "lda", "out_dtype", "dev", "run", "run_events", "release", "_keep")
 
     def __init__(self, qstrips: torch.Tensor, sstrips: torch.Tensor | None, group_size: int,
                  tensor_scale: float, out_dtype: torch.dtype, bias: torch.Tensor | None = None,
@@ -449,6 +450,7 @@ class PreparedStrips:
             raise PicoKernelsError("pk_w4a16_strips_prepare failed: "
                                    + L.pk_last_error().decode(errors="replace"))
         self.run, self.release = L.pk_w4a16_strips_run, L.pk_w4a16_strips_release
+        self.run_events = L.pk_w4a16_strips_run_events
 
     def __del__(self):
         h = getattr(self, "h", None)
@@ -470,6 +472,24 @@ class PreparedStrips:
         if rc != PK_OK:
             _check(rc, "pk_w4a16_strips_run")
         return out
+
+    def timed(self, a: torch.Tensor, out: torch.Tensor, start=None, stop=None) -> None:
+        """The call above (activations as the prepared stride wants them, output given), with
+        ``torch.cuda.Event`` ``start`` recorded as its kernel starts and ``stop`` as it ends, by
+        the dispatch itself (``pk_w4a16_strips_run_events``). Each event is recorded once on
+        the current stream first if it has no HIP event yet."""
+        if a.stride(0) != self.lda or a.stride(1) != 1 or a.data_ptr() % 16:
+            raise ValueError(f"PreparedStrips.timed: activations need row stride {self.lda}, "
+                             "16-byte aligned")
+        handles = []
+        for ev in (start, stop):
+            if ev is not None and not ev.cuda_event:
+                ev.record()
+            handles.append(None if ev is None else ev.cuda_event)
+        rc = self.run_events(self.h, a.data_ptr(), out.data_ptr(), out.stride(0), a.shape[0],
+                             torch._C._cuda_getCurrentRawStream(self.dev), *handles)
+        if rc != PK_OK:
+            _check(rc, "pk_w4a16_strips_run_events")
 
 
 def w4a16_strips_config(blocks_per_wave: int) -> None:

@@ -37,6 +37,8 @@
 // row sets and waves through LDS in a fixed order, so results are bitwise reproducible.
 #include <new>
 
+#include <hip/hip_ext.h>
+
 #include "pk_internal.h"
 
 namespace pk {
@@ -374,7 +376,10 @@ static void strips_plan(const uint8_t* qs, const void* ss, int group, OutEpi epi
   pl->block = dim3(64 * p.nw);
 }
 
-static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, hipStream_t stream) {
+// start / stop: events the dispatch itself records as the kernel starts and ends (for timing;
+// both null for a plain launch).
+static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, hipStream_t stream,
+                      hipEvent_t start = nullptr, hipEvent_t stop = nullptr) {
   StripParams p = pl.p;
   p.a = reinterpret_cast<const pk_half*>(a);
   p.c = c;
@@ -384,8 +389,11 @@ static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, 
   auto go = [&](auto MTc, auto Uc, auto AL) {
     constexpr int mt = decltype(MTc)::value, uu = decltype(Uc)::value;
     constexpr bool al = decltype(AL)::value != 0;
-    if (gs) w4a16_strip_kernel<mt, uu, true, al><<<pl.grid, pl.block, pl.lds, stream>>>(p);
-    else w4a16_strip_kernel<mt, uu, false, al><<<pl.grid, pl.block, pl.lds, stream>>>(p);
+    auto kernel = gs ? w4a16_strip_kernel<mt, uu, true, al> : w4a16_strip_kernel<mt, uu, false, al>;
+    if (start || stop)
+      hipExtLaunchKernelGGL(kernel, pl.grid, pl.block, (uint32_t)pl.lds, stream, start, stop, 0, p);
+    else
+      kernel<<<pl.grid, pl.block, pl.lds, stream>>>(p);
   };
   auto by_u = [&](auto MTc, auto AL) {
     if constexpr (decltype(MTc)::value == 8) go(MTc, pk_int_c<2>{}, AL);  // U = 2 only
@@ -495,15 +503,30 @@ extern "C" void* pk_w4a16_strips_prepare(const uint8_t* qstrips, const void* sst
   return h;
 }
 
+namespace {
+int strips_run_checked(const char* name, void* prepared, const void* a, void* c, int64_t ldc,
+                       int M, void* stream, void* start, void* stop) {
+  auto* h = static_cast<StripsPrepared*>(prepared);
+  PK_REQUIRE(h != nullptr && a != nullptr && c != nullptr, "%s: null pointer", name);
+  PK_REQUIRE(M >= 1 && M <= 8, "%s: M=%d (the strip layout serves 1..8 rows)", name, M);
+  PK_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15) == 0, "%s: A must be 16-byte aligned", name);
+  PK_REQUIRE(ldc >= h->N, "%s: ldc < N", name);
+  PK_REQUIRE((int64_t)M * h->lda * 2 < (1ll << 31), "%s: A beyond 2 GiB", name);
+  return strips_run(h->plan[M - 1], a, c, ldc, (hipStream_t)stream, (hipEvent_t)start,
+                    (hipEvent_t)stop);
+}
+}  // namespace
+
 extern "C" int pk_w4a16_strips_run(void* prepared, const void* a, void* c, int64_t ldc, int M,
                                    void* stream) {
-  auto* h = static_cast<StripsPrepared*>(prepared);
-  PK_REQUIRE(h != nullptr && a != nullptr && c != nullptr, "pk_w4a16_strips_run: null pointer");
-  PK_REQUIRE(M >= 1 && M <= 8, "pk_w4a16_strips_run: M=%d (the strip layout serves 1..8 rows)", M);
-  PK_REQUIRE((reinterpret_cast<uintptr_t>(a) & 15) == 0, "pk_w4a16_strips_run: A must be 16-byte aligned");
-  PK_REQUIRE(ldc >= h->N, "pk_w4a16_strips_run: ldc < N");
-  PK_REQUIRE((int64_t)M * h->lda * 2 < (1ll << 31), "pk_w4a16_strips_run: A beyond 2 GiB");
-  return strips_run(h->plan[M - 1], a, c, ldc, (hipStream_t)stream);
+  return strips_run_checked("pk_w4a16_strips_run", prepared, a, c, ldc, M, stream, nullptr, nullptr);
+}
+
+extern "C" int pk_w4a16_strips_run_events(void* prepared, const void* a, void* c, int64_t ldc,
+                                          int M, void* stream, void* start_event,
+                                          void* stop_event) {
+  return strips_run_checked("pk_w4a16_strips_run_events", prepared, a, c, ldc, M, stream,
+                            start_event, stop_event);
 }
 
 extern "C" void pk_w4a16_strips_release(void* prepared) {
