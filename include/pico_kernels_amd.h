@@ -189,7 +189,7 @@ int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* qtiled, cons
  * the (K/G, N) fp16 group scales reordered as (N/16, K/G, 16). Requires N % 16 == 0,
  * K % 128 == 0, G a multiple of 32 dividing K that divides 128 or is a multiple of it,
  * 16-byte aligned A rows and weights, 8-byte aligned scales; fp32/fp16/bf16 output and bias.
- * Replaces gemm_int4.int4_gemm (gemm_int4.py:75-92) at M = 1 and the split-K GEMV
+ * Replaces gemm_int4.int4_gemm (gemm_int4.py:75-92) at 1 <= M <= 8 and the split-K GEMV
  * (gemm_splitk.py:26-80) for decode: the reference has no weight layout other than
  * pack_int4_n's. */
 int pk_w4a16_gemm_strips(const void* a, int64_t lda, const uint8_t* qstrips, const void* sstrips,
