@@ -427,13 +427,21 @@ bool tr4_split_ok(int K, int split) { return split >= 1 && K % (128 * split) == 
 // written and read back plus the reduce launch (about 7 us of fixed cost and 0.34 us per MB of
 // planes), while k-tile time rises from 1.4 us with up to 128 busy CUs to 1.9 us with all 256,
 // so the best split stops short of filling every CU.
+// The most slices (dividing the k-tiles, at most 16, tiles x slices <= 224 workgroups), but a
+// power of two when one reaches at least half of that: fewer fp32 partial planes for the
+// reduce to read, and its unrolled form. Measured on MI355X at M = 128, 14336 x 4096 (graphs
+// over 22 rotating block-layout copies, GEMM + reduce): 14 slices 36.1 us, 8 slices 32.0,
+// 7 slices 35.5, 16 slices 37.1; 4096 x 6144: 8 slices 21.5, 4 22.5.
 int tr4_pick_split(int M, int N, int K) {
   const int kt = K / 128;
   const int64_t tiles = cdiv(M, 128) * (int64_t)(N / 256);
-  int best = 1;
+  int best = 1, best_pow2 = 1;
   for (int s = 2; s <= 16 && s <= kt; ++s)
-    if (kt % s == 0 && tiles * s <= 224) best = s;
-  return best;
+    if (kt % s == 0 && tiles * s <= 224) {
+      best = s;
+      if ((s & (s - 1)) == 0) best_pow2 = s;
+    }
+  return 2 * best_pow2 >= best ? best_pow2 : best;
 }
 
 bool tr4_ok(int M, int N, int K, int group, bool has_gs, int64_t lda, const void* b, int64_t ldb,

@@ -92,14 +92,16 @@ def test_tr4_strided_operands(cuda):
 
 
 # (M, K, N, G, automatic split): the sweep's qkv layer at 128 rows, ragged rows with a one-tile
-# slice, group 64 and 256, the largest slice count (16) and a slice count that is not a power
-# of two (14 of 112 k-tiles)
+# slice, group 64 and 256, the largest slice count (16), a power of two chosen over the most
+# slices (8 of 112 k-tiles, not 14) and a slice count that is not a power of two (15 of 15
+# k-tiles, reduced by the generic-count kernel)
 SPLIT_CASES = [
     (128, 4096, 6144, 128, 8),
     (65, 1024, 512, 64, 8),
     (100, 2048, 256, 256, 16),
     (129, 2048, 1024, 128, 16),
-    (128, 14336, 4096, 128, 14),
+    (128, 14336, 4096, 128, 8),
+    (128, 1920, 256, 128, 15),
 ]
 
 
