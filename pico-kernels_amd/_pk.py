@@ -109,6 +109,28 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+_strips_run_fast = None  # _pkcall.strips_run once probed, False when unavailable
+
+
+def strips_run_entry():
+    """``pk_w4a16_strips_run`` as the CPython module ``_pkcall`` exposes it (built beside the
+    library by build.py: six integers in, the status out, no ctypes conversion), when that
+    module is there and the library was loaded from its default path (the one ``_pkcall`` is
+    linked against); else the ctypes function. Both launch the same kernel."""
+    global _strips_run_fast
+    L = lib()
+    if _strips_run_fast is None:
+        _strips_run_fast = False
+        if LIB_PATH.resolve() == (HERE / LIB_NAME).resolve():
+            try:
+                import _pkcall
+
+                _strips_run_fast = _pkcall.strips_run
+            except ImportError:
+                pass
+    return _strips_run_fast or L.pk_w4a16_strips_run
+
+
 def _check(rc: int, what: str) -> None:
     if rc != PK_OK:
         msg = lib().pk_last_error().decode(errors="replace")
@@ -449,7 +471,7 @@ class PreparedStrips:
         if not self.h:
             raise PicoKernelsError("pk_w4a16_strips_prepare failed: "
                                    + L.pk_last_error().decode(errors="replace"))
-        self.run, self.release = L.pk_w4a16_strips_run, L.pk_w4a16_strips_release
+        self.run, self.release = strips_run_entry(), L.pk_w4a16_strips_release
         self.run_events = L.pk_w4a16_strips_run_events
 
     def __del__(self):

@@ -80,6 +80,26 @@ def _link(objs: list[Path], out: Path, verbose: bool) -> None:
     os.replace(tmp, out)
 
 
+def _build_pkcall(lib: Path, verbose: bool) -> Path:
+    """The CPython module ``_pkcall`` (csrc/pkcall.c: the prepared decode call without ctypes),
+    linked against ``lib`` by path (rpath $ORIGIN)."""
+    import sysconfig
+
+    src = CSRC / "pkcall.c"
+    out = HERE / ("_pkcall" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = [shutil.which("gcc") or "gcc", "-O2", "-shared", "-fPIC", "-Wall", "-Werror",
+           f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}", str(src), "-o", str(tmp),
+           f"-L{lib.parent}", "-l:" + lib.name, "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"gcc failed for {src.name}:\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
     """Compile all HIP sources and link the product library and the bench probes library;
     returns the product library's path."""
@@ -99,6 +119,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
             f.result()
     out = HERE / LIB_NAME
     _link(objs, out, verbose)
+    _build_pkcall(out, verbose)
     if probe_objs:
         _link(probe_objs, HERE / PROBES_LIB_NAME, verbose)
     return out

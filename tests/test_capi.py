@@ -205,3 +205,18 @@ def test_tiled_rows_per_call():
         assert rows - M / chunks < 128                   # equal chunks, no small tail call
     assert f(75000, 14336) == 37504
     assert f(100, 1 << 24) == 0                          # even 128 rows exceed 2 GiB
+
+
+def test_pkcall_module_shares_the_library():
+    """The CPython fast-call module that build.py links beside the library: it is the entry
+    PreparedStrips uses, it reaches the very library _pk loaded (a null handle's error shows up
+    in that library's pk_last_error) and it checks its argument count. No device work."""
+    import _pkcall
+
+    assert _pk.strips_run_entry() is _pkcall.strips_run
+    assert _pkcall.strips_run(0, 0, 0, 16, 1, 0) == _pk.PK_EINVAL
+    assert b"null pointer" in _pk.lib().pk_last_error()
+    with pytest.raises(TypeError):
+        _pkcall.strips_run(1, 2, 3)
+    with pytest.raises(OverflowError):
+        _pkcall.strips_run(0, 0, 0, 16, 1 << 40, 0)

@@ -283,9 +283,12 @@ def test_prepared_strips_handle(cuda):
     bias = torch.randn(N, generator=_gen(42)).half().to(cuda)
     ag = a.to(cuda)
     call = _pk.PreparedStrips(qs, ss, 128, 0.5, torch.float32, bias)
+    via_ctypes = _pk.PreparedStrips(qs, ss, 128, 0.5, torch.float32, bias)
+    via_ctypes.run = _pk.lib().pk_w4a16_strips_run  # the entry without the CPython module
     for M in range(1, 9):
         ref = _pk.w4a16_gemm_strips(ag[:M], qs, ss, 128, 0.5, torch.float32, bias=bias)
         assert torch.equal(call(ag[:M]), ref), M
+        assert torch.equal(via_ctypes(ag[:M]), ref), M
     with pytest.raises(_pk.PicoKernelsError, match="group_size"):
         _pk.PreparedStrips(qs, ss, 96, 1.0, torch.float16)
     lin = nn.Linear(K, N).to(cuda)
