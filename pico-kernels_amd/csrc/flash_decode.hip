@@ -288,10 +288,18 @@ extern "C" size_t pk_flash_decode_workspace_bytes(int B, int H, int N, int D, in
   return kWsCounterBytes + (size_t)B * H * fd_bh_stride(N / split, D) * sizeof(float);
 }
 
+namespace {
+// The splits of every (b, h) combine inside the launch when their grid fits the counters and
+// the device's placement allows it (`l2`: splitk_in_l2_ok / splitk_in_l2_possible).
+bool fd_fused(int B, int H, int N, int split, bool l2) {
+  const int64_t bh = (int64_t)B * H, S = N / split;
+  return bh <= kWsMaxTiles && 8 * ((bh + 7) / 8) * S <= 0x7fffffff && l2;
+}
+}  // namespace
+
 extern "C" int pk_flash_decode_launches(int B, int H, int N, int D, int split) {
   if (B < 1 || H < 1 || N < 1 || D < 1 || split < 1 || N % split) return 0;
-  const int64_t bh = (int64_t)B * H, S = N / split;
-  return bh <= kWsMaxTiles && 8 * ((bh + 7) / 8) * S <= 0x7fffffff && splitk_in_l2_ok() ? 1 : 2;
+  return fd_fused(B, H, N, split, splitk_in_l2_possible()) ? 1 : 2;
 }
 
 extern "C" int pk_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k,
@@ -339,7 +347,7 @@ extern "C" int pk_flash_decode(const void* q, int64_t sqb, int64_t sqh, const vo
   const int rg = 256 / (D / 8);
   p.nch = (split + kFdChunkPasses * rg - 1) / (kFdChunkPasses * rg);
   p.sm_scale = sm_scale;
-  const bool fused = pk_flash_decode_launches(B, H, N, D, split) == 1;
+  const bool fused = fd_fused(B, H, N, split, splitk_in_l2_ok((hipStream_t)stream));
   PK_REQUIRE(fused || p.S <= 65535, "pk_flash_decode: N/split=%d splits exceed the grid (at most 65535 "
              "when B*H > %d)", p.S, kWsMaxTiles);
   hipStream_t s = (hipStream_t)stream;

@@ -43,9 +43,14 @@ __host__ __device__ __forceinline__ int qrow_off(const QLayout& q, int k) {
   return (k >> 7) * q.kblock_bytes + (k & 127) * q.row_bytes;
 }
 
-// Host: split-K slices may hand off through one XCD's L2 on the current device (its XCC count
-// divides 8; the environment variable PK_SPLITK_IN_L2=0 turns it off).
-bool splitk_in_l2_ok();
+// Host: split-K slices may hand off through one XCD's L2 on the current device: its XCC
+// count divides 8, PK_SPLITK_IN_L2 is not 0, and a probe launch (run once per device, at the
+// first call from a stream that is not capturing; see splitk_reduce.hip) found every
+// workgroup of a launch on XCD (b + c) mod that count. For a launch on `stream`.
+bool splitk_in_l2_ok(hipStream_t stream);
+// The same answer for queries that launch nothing (launch counts): the probe's result once it
+// has run, before that the XCC-count and environment rule alone.
+bool splitk_in_l2_possible();
 
 // Host: allow `kernel` up to `bytes` of dynamic LDS on the current device. The attribute is
 // set once per (device, kernel): `done` is a per-kernel bit set of the devices already done
@@ -100,7 +105,8 @@ bool skinny_plan(int M, int N, int K, int group, bool has_gs, int split_req, Ski
 bool skinny_layout_set(int cpl, int nw);
 bool skinny_fits(int M, int N, int K, int64_t lda, int64_t ldq, int group, bool has_gs);
 // Split-K of the skinny kernel adds its slices in L2 inside the launch (one launch).
-bool skinny_l2(const SkinnyPlan& pl);
+// `l2`: splitk_in_l2_ok(stream) for a launch, splitk_in_l2_possible() for a query.
+bool skinny_l2(const SkinnyPlan& pl, bool l2);
 size_t skinny_workspace_bytes(const SkinnyPlan& pl, int M, int N);
 int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32_t* qw,
                   int64_t ldq, const void* scales, int group, OutEpi epi, void* c,

@@ -7,6 +7,7 @@
 
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
 
 namespace pk {
 
@@ -24,19 +25,84 @@ int set_lds_limit_once(const void* kernel, int bytes, std::atomic<uint64_t>* don
   return PK_OK;
 }
 
-bool splitk_in_l2_ok() {
-  static std::atomic<int> state[64];  // 0 unknown, 1 on, 2 off
+// The one-launch split-K forms hand partials off through one XCD's L2, which is right only
+// while a launch's workgroup b runs on XCD (b + c) mod the partition's XCC count (c: where
+// the launch starts). Before the first such launch on a device, a probe launch checks that
+// rule on this machine: each of kPlacementGrid workgroups records its XCC id (hwreg XCC_ID)
+// into a static device array (no allocation), the host copies it back on a private stream
+// and checks every workgroup. A device that fails it (or whose XCC count does not divide 8,
+// or with PK_SPLITK_IN_L2=0) uses the reduce launch instead: the same bits, one launch more.
+constexpr int kPlacementGrid = 4096;
+static __device__ __align__(256) uint32_t placement_xcc[kPlacementGrid];
+
+__global__ __launch_bounds__(64) void xcd_placement_kernel(uint32_t* out) {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  if (threadIdx.x == 0) out[blockIdx.x] = v & 0xfu;
+}
+
+namespace {
+std::atomic<int> g_l2_state[64];  // 0 not yet probed, 1 on, 2 off
+
+int xcc_count(int dev) {
+  int n = 0;
+  return hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess ? n : 0;
+}
+
+bool l2_capable(int dev) {
+  const char* env = std::getenv("PK_SPLITK_IN_L2");
+  const int n = xcc_count(dev);
+  return !(env && env[0] == '0') && (n == 1 || n == 2 || n == 4 || n == 8);
+}
+
+// Runs the probe on the current device; true when every workgroup obeyed the rule.
+bool placement_probe(int nxcc) {
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(placement_xcc)) != hipSuccess || ptr == nullptr)
+    return false;
+  hipStream_t s = nullptr;
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return false;
+  static uint32_t ids[kPlacementGrid];  // under the caller's first-use lock
+  xcd_placement_kernel<<<kPlacementGrid, 64, 0, s>>>(static_cast<uint32_t*>(ptr));
+  bool ok = hipGetLastError() == hipSuccess &&
+            hipMemcpyAsync(ids, ptr, sizeof ids, hipMemcpyDeviceToHost, s) == hipSuccess &&
+            hipStreamSynchronize(s) == hipSuccess;
+  hipStreamDestroy(s);
+  if (!ok) return false;
+  const uint32_t c = ids[0];
+  for (int b = 0; b < kPlacementGrid; ++b)
+    if (ids[b] != (uint32_t)((b + c) % nxcc)) return false;
+  return true;
+}
+}  // namespace
+
+bool splitk_in_l2_possible() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-  int v = state[dev].load(std::memory_order_relaxed);
+  const int v = g_l2_state[dev].load(std::memory_order_acquire);
+  return v == 0 ? l2_capable(dev) : v == 1;
+}
+
+bool splitk_in_l2_ok(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  int v = g_l2_state[dev].load(std::memory_order_acquire);
+  if (v != 0) return v == 1;
+  if (!l2_capable(dev)) {
+    g_l2_state[dev].store(2, std::memory_order_release);
+    return false;
+  }
+  // No probe (with its synchronisation) inside a stream capture: this call takes the reduce
+  // launch, and the probe runs at the first call outside one.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (stream != nullptr && hipStreamIsCapturing(stream, &cap) != hipSuccess) return false;
+  if (cap != hipStreamCaptureStatusNone) return false;
+  static std::mutex mu;
+  std::lock_guard<std::mutex> lock(mu);
+  v = g_l2_state[dev].load(std::memory_order_acquire);
   if (v == 0) {
-    const char* env = std::getenv("PK_SPLITK_IN_L2");
-    int nxcc = 0;
-    const bool on = !(env && env[0] == '0') &&
-                    hipDeviceGetAttribute(&nxcc, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess &&
-                    (nxcc == 1 || nxcc == 2 || nxcc == 4 || nxcc == 8);
-    v = on ? 1 : 2;
-    state[dev].store(v, std::memory_order_relaxed);
+    v = placement_probe(xcc_count(dev)) ? 1 : 2;
+    g_l2_state[dev].store(v, std::memory_order_release);
   }
   return v == 1;
 }

@@ -180,8 +180,8 @@ extern "C" int pk_w4a16_launches(int M, int N, int K, int group_size, int split_
   const int split = plan_split(pl);
   if (split <= 1) return 1;
   const bool l2 = pl.kernel == kKernelGemv
-                      ? splitk_in_l2_ok() && pl.gemv.mfma && pl.gemv.tiles <= kWsMaxTiles
-                      : pl.kernel == kKernelSkinny && skinny_l2(pl.skinny);
+                      ? splitk_in_l2_possible() && pl.gemv.mfma && pl.gemv.tiles <= kWsMaxTiles
+                      : pl.kernel == kKernelSkinny && skinny_l2(pl.skinny, splitk_in_l2_possible());
   return l2 ? 1 : 2;
 }
 

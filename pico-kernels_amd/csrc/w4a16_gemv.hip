@@ -610,7 +610,7 @@ int gemv_launch(const GemvPlan& pl, const void* a, int64_t lda, const uint32_t* 
   if (mfma) {
     // Slices hand off through L2 unless the caller wants the partials themselves.
     const bool l2split = pl.split > 1 && !partials_only && pl.tiles <= kWsMaxTiles &&
-                         splitk_in_l2_ok();
+                         splitk_in_l2_ok(s);
     if (l2split) p.counters = ws_counters(workspace);
     switch (M) {
       case 1: launch_gemv_mfma<1>(p, pl.tiles, rb, s, l2split); break;

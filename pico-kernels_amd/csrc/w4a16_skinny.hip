@@ -573,11 +573,10 @@ static void launch_skinny_cfg(const SkinnyPlan& pl, const SkinnyParams& p, bool 
 // 22.7 -> 26.1), and with four blocks it was slower everywhere, so those keep the reduce
 // launch. Group-spanning plans (half the slices, 128-column tiles) gather a quarter of those
 // bytes per tile and hand off in L2 on every layer (down M = 32 with 7 slices: 19.5 -> 18.5).
-bool skinny_l2(const SkinnyPlan& pl) {
+bool skinny_l2(const SkinnyPlan& pl, bool l2) {
   const int64_t weights = (int64_t)pl.split * pl.k_slice * pl.tiles * 16 * pl.cpl;
   const bool blocks_ok = pl.mb == 1 || (pl.mb == 2 && (weights <= 4096ll * 6144 || pl.mg));
-  return pl.split > 1 && blocks_ok && pl.tiles * pl.row_parts <= kWsMaxTiles &&
-         splitk_in_l2_ok();
+  return pl.split > 1 && blocks_ok && pl.tiles * pl.row_parts <= kWsMaxTiles && l2;
 }
 
 size_t skinny_workspace_bytes(const SkinnyPlan& pl, int M, int N) {
@@ -617,7 +616,7 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
   p.counters = ws_counters(workspace);
   p.npad = pl.tiles * 16 * pl.cpl;
   p.ql = qlayout(tiled, ldq, N);
-  const bool l2 = !partials_only && skinny_l2(pl);
+  const bool l2 = !partials_only && pl.split > 1 && skinny_l2(pl, splitk_in_l2_ok(s));
   if (scales) launch_skinny_cfg<true>(pl, p, l2, s);
   else launch_skinny_cfg<false>(pl, p, l2, s);
   PK_LAUNCH_CHECK("w4a16 skinny");
