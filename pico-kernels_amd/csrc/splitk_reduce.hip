@@ -29,8 +29,8 @@ int set_lds_limit_once(const void* kernel, int bytes, std::atomic<uint64_t>* don
 // while a launch's workgroup b runs on XCD (b + c) mod the partition's XCC count (c: where
 // the launch starts). Before the first such launch on a device, a probe launch checks that
 // rule on this machine: each of kPlacementGrid workgroups records its XCC id (hwreg XCC_ID)
-// into a static device array (no allocation), the host copies it back on a private stream
-// and checks every workgroup. A device that fails it (or whose XCC count does not divide 8,
+// into a static device array (no allocation), the host copies it back on the caller's
+// stream (one synchronisation of that stream, once per device) and checks every workgroup. A device that fails it (or whose XCC count does not divide 8,
 // or with PK_SPLITK_IN_L2=0) uses the reduce launch instead: the same bits, one launch more.
 constexpr int kPlacementGrid = 4096;
 static __device__ __align__(256) uint32_t placement_xcc[kPlacementGrid];
@@ -55,19 +55,17 @@ bool l2_capable(int dev) {
   return !(env && env[0] == '0') && (n == 1 || n == 2 || n == 4 || n == 8);
 }
 
-// Runs the probe on the current device; true when every workgroup obeyed the rule.
-bool placement_probe(int nxcc) {
+// Runs the probe on the current device, on the caller's stream (which it synchronises once);
+// true when every workgroup obeyed the rule.
+bool placement_probe(int nxcc, hipStream_t s) {
   void* ptr = nullptr;
   if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(placement_xcc)) != hipSuccess || ptr == nullptr)
     return false;
-  hipStream_t s = nullptr;
-  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return false;
   static uint32_t ids[kPlacementGrid];  // under the caller's first-use lock
   xcd_placement_kernel<<<kPlacementGrid, 64, 0, s>>>(static_cast<uint32_t*>(ptr));
-  bool ok = hipGetLastError() == hipSuccess &&
-            hipMemcpyAsync(ids, ptr, sizeof ids, hipMemcpyDeviceToHost, s) == hipSuccess &&
-            hipStreamSynchronize(s) == hipSuccess;
-  hipStreamDestroy(s);
+  const bool ok = hipGetLastError() == hipSuccess &&
+                  hipMemcpyAsync(ids, ptr, sizeof ids, hipMemcpyDeviceToHost, s) == hipSuccess &&
+                  hipStreamSynchronize(s) == hipSuccess;
   if (!ok) return false;
   const uint32_t c = ids[0];
   for (int b = 0; b < kPlacementGrid; ++b)
@@ -101,7 +99,7 @@ bool splitk_in_l2_ok(hipStream_t stream) {
   std::lock_guard<std::mutex> lock(mu);
   v = g_l2_state[dev].load(std::memory_order_acquire);
   if (v == 0) {
-    v = placement_probe(xcc_count(dev)) ? 1 : 2;
+    v = placement_probe(xcc_count(dev), stream) ? 1 : 2;
     g_l2_state[dev].store(v, std::memory_order_release);
   }
   return v == 1;
