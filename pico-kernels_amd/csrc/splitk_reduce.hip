@@ -55,22 +55,23 @@ bool l2_capable(int dev) {
   return !(env && env[0] == '0') && (n == 1 || n == 2 || n == 4 || n == 8);
 }
 
-// Runs the probe on the current device, on the caller's stream (which it synchronises once);
-// true when every workgroup obeyed the rule.
-bool placement_probe(int nxcc, hipStream_t s) {
+// Runs the probe on the current device, on the caller's stream (which it synchronises once):
+// 1 when every workgroup obeyed the rule, 2 when one did not, 0 when the probe itself could
+// not run (a HIP error: nothing is concluded).
+int placement_probe(int nxcc, hipStream_t s) {
   void* ptr = nullptr;
   if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(placement_xcc)) != hipSuccess || ptr == nullptr)
-    return false;
+    return 0;
   static uint32_t ids[kPlacementGrid];  // under the caller's first-use lock
   xcd_placement_kernel<<<kPlacementGrid, 64, 0, s>>>(static_cast<uint32_t*>(ptr));
-  const bool ok = hipGetLastError() == hipSuccess &&
-                  hipMemcpyAsync(ids, ptr, sizeof ids, hipMemcpyDeviceToHost, s) == hipSuccess &&
-                  hipStreamSynchronize(s) == hipSuccess;
-  if (!ok) return false;
+  const bool ran = hipGetLastError() == hipSuccess &&
+                   hipMemcpyAsync(ids, ptr, sizeof ids, hipMemcpyDeviceToHost, s) == hipSuccess &&
+                   hipStreamSynchronize(s) == hipSuccess;
+  if (!ran) return 0;
   const uint32_t c = ids[0];
   for (int b = 0; b < kPlacementGrid; ++b)
-    if (ids[b] != (uint32_t)((b + c) % nxcc)) return false;
-  return true;
+    if (ids[b] != (uint32_t)((b + c) % nxcc)) return 2;
+  return 1;
 }
 }  // namespace
 
@@ -99,7 +100,11 @@ bool splitk_in_l2_ok(hipStream_t stream) {
   std::lock_guard<std::mutex> lock(mu);
   v = g_l2_state[dev].load(std::memory_order_acquire);
   if (v == 0) {
-    v = placement_probe(xcc_count(dev), stream) ? 1 : 2;
+    v = placement_probe(xcc_count(dev), stream);
+    if (v == 0) {  // the probe failed to run: the reduce launch this time, the probe again later
+      (void)hipGetLastError();
+      return false;
+    }
     g_l2_state[dev].store(v, std::memory_order_release);
   }
   return v == 1;
