@@ -138,9 +138,10 @@ def test_strips_group_sizes(G, M, cuda):
 @pytest.mark.gpu
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("bias_dtype", [None, torch.float16, torch.float32])
-def test_strips_bias_and_dtypes(out_dtype, bias_dtype, cuda):
-    M, K, N = 3, 2048, 768
-    a, codes, s16, words = _case(M, K, N, 128, 77)
+@pytest.mark.parametrize("M", [3, 7])  # the staged four-row kernel and the eight-row one
+def test_strips_bias_and_dtypes(M, out_dtype, bias_dtype, cuda):
+    K, N = 2048, 768
+    a, codes, s16, words = _case(M, K, N, 128, 77 + M)
     bias = None if bias_dtype is None else torch.randn(N, generator=_gen(78)).to(bias_dtype)
     y = _run(a, words, s16, 128, cuda, out_dtype=out_dtype, bias=bias)
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
@@ -152,8 +153,9 @@ def test_strips_bias_and_dtypes(out_dtype, bias_dtype, cuda):
 
 
 @pytest.mark.gpu
-def test_strips_strided_activations_and_output_view(cuda):
-    M, K, N = 4, 4096, 2048
+@pytest.mark.parametrize("M", [4, 8])  # staged activations; per-lane loads (eight rows)
+def test_strips_strided_activations_and_output_view(M, cuda):
+    K, N = 4096, 2048
     a, codes, s16, words = _case(M, K, N, 128, 91)
     big = torch.zeros(M, K + 64, dtype=torch.float16)
     big[:, 32:32 + K] = a
