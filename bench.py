@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X quantized-matmul path (one JSON line on stdout).
 
-Headline workload: W4A16 decode GEMV, M=1, K=4096, N=11008, int4 group
+Headline workload (the decode GEMV configuration): W4A16 decode GEMV, M=1, K=4096, N=11008, int4 group
 128 with fp16 scales, fp16 activations N(0,1), weights N(0, 0.02), seeded CPU generator.
 A "step" is one decode call over one activation row, made as ``QuantLinear`` makes it: the
 prepared strip GEMV (``_pk.PreparedStrips`` over ``pk_w4a16_strips_run``) on the layer's
@@ -547,7 +547,7 @@ SWEEP_LAYERS = (("qkv", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up", 4096, 1
 
 
 def bench_llama_sweep(dev, iters: int = 50) -> list:
-    """Llama-3-8B layer sweep (BASELINE config 5): each layer at M = 1, 8, 32, 128, checked,
+    """Llama-3-8B layer sweep: each layer at M = 1, 8, 32, 128, checked,
     then timed over rotating weight copies (more than 600 MB per layer, at most 40 copies):
     a graph of max(iters, 2 x copies) calls starting after the warm-up's copies, best of 3
     replays. ``frac`` is the applicable roof (slower of streaming the bytes at 8 TB/s and

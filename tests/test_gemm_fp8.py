@@ -147,7 +147,7 @@ def test_fp8_mfma_accumulation_precision(M, K, N, sd, cuda):
 
 
 def test_fp8_full_size_4096(cuda):
-    """BASELINE config: M=N=K=4096, fp16 inputs N(0,1), fp16 output; error vs fp32."""
+    """The fp8 configuration: M=N=K=4096, fp16 inputs N(0,1), fp16 output; error vs fp32."""
     M = K = N = 4096
     a, b, a8, sa, b8, sb = _fp8_case(M, K, N, 4096, cuda)
     c16 = gemm_fp8.fp8_gemm_precast(a8, sa, b8, sb, out_dtype=torch.float16)

@@ -162,7 +162,7 @@ def test_w4a16_output_dtypes(out_dtype, cuda):
 
 
 def test_decode_gemv_splitk_sweep_full_size(cuda):
-    """BASELINE config: M=1, K=4096, N=11008, group 128, split-K in {1,2,4,8,16}."""
+    """The decode GEMV configuration: M=1, K=4096, N=11008, group 128, split-K in {1,2,4,8,16}."""
     M, K, N = 1, 4096, 11008
     a, w, qw, sc, codes, s16 = _group_case(M, K, N, 100, cuda)
     ag = a.to(cuda)
@@ -183,7 +183,7 @@ def test_decode_gemv_splitk_sweep_full_size(cuda):
 
 
 def test_prefill_gemm_full_size(cuda):
-    """BASELINE config: M=2048, K=4096, N=4096 (MFMA path), fp16 output."""
+    """The prefill configuration: M=2048, K=4096, N=4096 (MFMA path), fp16 output."""
     M, K, N = 2048, 4096, 4096
     a, w, qw, sc, codes, s16 = _group_case(M, K, N, 200, cuda)
     out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, 128, out_dtype=torch.float32)
@@ -195,7 +195,7 @@ def test_prefill_gemm_full_size(cuda):
 @pytest.mark.parametrize("M", [1, 8, 32, 128])
 @pytest.mark.parametrize("K,N", [(4096, 6144), (4096, 4096), (4096, 14336), (14336, 4096)])
 def test_llama3_sweep_shapes(M, K, N, cuda):
-    """BASELINE config: Llama-3-8B linear layers (qkv, o, gate/up, down) at M in {1,8,32,128}."""
+    """The Llama-3-8B linear layers (qkv, o, gate/up, down) at M in {1,8,32,128}."""
     a, w, qw, sc, codes, s16 = _group_case(M, K, N, 300 + M + K % 7 + N % 11, cuda)
     out = gemm_int4.w4a16_gemm(a.to(cuda), qw, sc, 128, out_dtype=torch.float32)
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
