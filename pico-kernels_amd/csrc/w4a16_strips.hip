@@ -73,20 +73,19 @@ __device__ __forceinline__ int strip_group(const StripParams& p, int r0) {
 #define PK_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 // LDS staging (ALDS) is per wave: a wave's U blocks of activations (U x 128 columns of each
-// of the M rows, as M runs of 256 U bytes) and their U group-scale rows (32 bytes each), in a
-// region of its own, so no wave waits for another.
-__host__ __device__ __forceinline__ int strip_wave_act_lds(int M, int U) { return (int)cdiv((int64_t)M * U * 256, 1024) * 1024; }
-constexpr int kStripWaveScLds = 1024;
-__host__ __device__ __forceinline__ int strip_wave_lds(int M, int U, bool gs) {
-  return strip_wave_act_lds(M, U) + (gs ? kStripWaveScLds : 0);
-}
+// of the M rows, as M runs of 256 U bytes) in a region of its own, so no wave waits for
+// another. (Group scales are not staged: each lane loads its own 8 bytes per block beside its
+// weights. Staged through LDS with the activations -- one 1 KB DMA per wave, of which a wave
+// at group 128 uses 128 bytes -- the call ran 3-11% slower on MI355X: 4096 x 11008 M = 1
+// 6.37 against 6.14 us, M = 4 8.40 against 7.46; o_proj 4096 x 4096 4.10 against 3.85.)
+__host__ __device__ __forceinline__ int strip_wave_lds(int M, int U) { return (int)cdiv((int64_t)M * U * 256, 1024) * 1024; }
 // A wave's partial sums for the end fold: 4 row sets x MT rows x 16 columns of fp32. With
 // ALDS they overwrite the wave's own activation region (at least M * 256 bytes, rounded up to
 // 1 KB, which holds the MT * 256 bytes whenever M > MT / 2); otherwise each wave has a
 // region of this size.
 __host__ __device__ __forceinline__ int strip_fold_lds(int MT) { return 4 * MT * 64; }
-__host__ __device__ __forceinline__ int strip_wave_stride(int M, int MT, int U, bool gs, bool alds) {
-  return alds ? strip_wave_lds(M, U, gs) : strip_fold_lds(MT);
+__host__ __device__ __forceinline__ int strip_wave_stride(int M, int MT, int U, bool alds) {
+  return alds ? strip_wave_lds(M, U) : strip_fold_lds(MT);
 }
 
 // 16 bytes per lane, global -> LDS: lane L writes lds + 16 L.
@@ -95,9 +94,9 @@ __device__ __forceinline__ void strip_dma16(__amdgpu_buffer_rsrc_t r, char* lds,
 }
 
 // MT: activation rows the kernel carries (1, 2, 4 or 8); U: 1 KB blocks per wave per round.
-// ALDS: each wave DMAs its round's activations and scales into its own LDS region ahead of
-// its weight loads and reads them from there (M * U <= 32); otherwise every lane loads its
-// own from global memory. Up to 16 waves per workgroup (the 8-row kernel runs U = 2 only,
+// ALDS: each wave DMAs its round's activations into its own LDS region ahead of its weight
+// loads and reads them from there (M * U <= 32); otherwise every lane loads its own from
+// global memory. Scales: every lane loads its own, beside its weights. Up to 16 waves per workgroup (the 8-row kernel runs U = 2 only,
 // which keeps it within the 128 registers that allows).
 template <int MT, int U, bool HAS_GS, bool ALDS>
 __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripParams p) {
@@ -120,8 +119,7 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
   const __amdgpu_buffer_rsrc_t rsc =
       make_rsrc(HAS_GS ? (const void*)(p.ss + (int64_t)s * ngroups * kStripCols) : (const void*)p.qs,
                 HAS_GS ? (uint32_t)(ngroups * kStripCols * 2) : 16u);
-  char* const w_act = strip_lds + wave * strip_wave_lds(p.M, U, HAS_GS);
-  char* const w_sc = w_act + strip_wave_act_lds(p.M, U);
+  char* const w_act = strip_lds + wave * strip_wave_lds(p.M, U);
   int xoff[MS];  // this lane's activations inside block i: bytes of A (+ block), or of w_act
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms) {
@@ -140,7 +138,7 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
     const int b0 = (it * p.nw + wave) * U;
     if constexpr (ALDS) {
       // This round's activations (M runs of U * 128 columns from column b0 * 128, the blocks
-      // past the strip clamped to its last) and U scale rows, ahead of the weights.
+      // past the strip clamped to its last), ahead of the weights.
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the previous round's LDS reads are done
       const int kp = U * 16, pieces = p.M * kp;  // 16-byte pieces
       for (int p0 = 0; p0 < pieces; p0 += 64) {
@@ -148,8 +146,6 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
         const int col = min(b0 * 128 + (pc % kp) * 8, p.K - 8);
         strip_dma16(ra, w_act + p0 * 16, (m * (int)p.lda + col) * 2);
       }
-      if constexpr (HAS_GS)  // rows of the groups of blocks b0 .. b0+U-1, 2 pieces per row
-        strip_dma16(rsc, w_sc, min(strip_group(p, b0 * kStripBlockRows) * 2 + lane, ngroups * 2 - 1) * 16);
       asm volatile("" ::: "memory");
     }
     // ---- all loads of this round: U blocks of weights (and activations, scales) ----------
@@ -163,25 +159,22 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
           x[i][ms] = __builtin_amdgcn_raw_buffer_load_b128(ra, xoff[ms], b * (kStripBlockRows * 2), 0);
-        if constexpr (HAS_GS)  // the row set's group: per lane where G < 128
-          sc[i] = __builtin_amdgcn_raw_buffer_load_b64(
-              rsc, cps * 8 + strip_group(p, b * kStripBlockRows + 32 * rs) * (kStripCols * 2), 0, 0);
       }
+      if constexpr (HAS_GS)  // the row set's group (per lane where G < 128)
+        sc[i] = __builtin_amdgcn_raw_buffer_load_b64(
+            rsc, cps * 8 + strip_group(p, b * kStripBlockRows + 32 * rs) * (kStripCols * 2), 0, 0);
     }
     if constexpr (ALDS) {
-      static_assert(U < 16, "vmcnt field");
-      __builtin_amdgcn_s_waitcnt(0x0f70 | U);  // the wave's DMAs landed; the U weights may fly
+      // the wave's DMAs landed; its U weight (and U scale) loads, issued after them, may fly
+      constexpr int nv = (HAS_GS ? 2 : 1) * U;
+      __builtin_amdgcn_s_waitcnt((nv & 15) | (7 << 4) | (15 << 8) | ((nv >> 4) << 14));
       asm volatile("" ::: "memory");
-      const int g0 = HAS_GS ? strip_group(p, b0 * kStripBlockRows) : 0;
 #pragma unroll
       for (int i = 0; i < U; ++i) {
         const int b = min(b0 + i, p.kb - 1);
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
           x[i][ms] = *reinterpret_cast<const pk_u4v*>(w_act + xoff[ms] + (b - b0) * (kStripBlockRows * 2));
-        if constexpr (HAS_GS)
-          sc[i] = *reinterpret_cast<const pk_u2v*>(
-              w_sc + cps * 8 + (strip_group(p, b * kStripBlockRows + 32 * rs) - g0) * (kStripCols * 2));
       }
     }
     // Every load of the round issues before the products: left to itself the scheduler sinks
@@ -248,7 +241,7 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
   // ((part 0 + part 1) + (part 2 + part 3)), the same tree on every call.
   // red(w)[rs][m][cps]: wave w's partials, in its own region (after its last LDS reads of
   // staged activations: a wave's LDS accesses complete in order).
-  const int wstride = strip_wave_stride(p.M, MT, U, HAS_GS, ALDS);
+  const int wstride = strip_wave_stride(p.M, MT, U, ALDS);
   auto red = [&](int w, int set, int m, int q) {
     return reinterpret_cast<pk_f4*>(strip_lds + w * wstride) + (set * MT + m) * (kStripCols / 4) + q;
   };
@@ -323,15 +316,8 @@ static int strips_pick_u(int M, int N, int kb) {
 // 11008): 8.09 / 5.56 / 13.3 / 11.7 / 10.9 us; staged, 9.4 / 7.3 / 16.8 / 19.5 / 14.2.
 constexpr int kStripWaves8 = 8;
 
-// Activations and scales staged per wave in LDS: at most 8 KB of activations per wave
-// (M * U <= 32) and the wave's group-scale rows within one 1 KB DMA (at most 32 groups).
-static bool strips_alds(int M, int U, int group, bool has_gs) {
-  if ((int64_t)M * U > 32) return false;
-  if (!has_gs) return true;
-  const int rows = U * kStripBlockRows;  // a wave's rows per round, starting G-aligned if G | 128
-  const int groups = 128 % group == 0 ? rows / group : rows / group + 1;
-  return groups <= 32;
-}
+// Activations staged per wave in LDS: at most 8 KB per wave (M * U <= 32).
+static bool strips_alds(int M, int U) { return (int64_t)M * U <= 32; }
 
 // Everything about a launch that depends on the shape and weights only.
 struct StripPlan {
@@ -365,12 +351,10 @@ static void strips_plan(const uint8_t* qs, const void* ss, int group, OutEpi epi
   const int max_waves = M > 4 ? kStripWaves8 : kStripMaxWaves;
   p.nw = waves_one_round < max_waves ? waves_one_round : max_waves;
   p.iters = (int)cdiv(p.kb, (int64_t)u * p.nw);
-  const bool gs = ss != nullptr;
   const int mt = M == 1 ? 1 : M == 2 ? 2 : M <= 4 ? 4 : 8;
   pl->u = u;
-  pl->alds = M <= 4 && strips_alds(M, u, p.group, gs) &&
-             (size_t)p.nw * strip_wave_lds(M, u, gs) <= (64u << 10);
-  pl->lds = (size_t)p.nw * strip_wave_stride(M, mt, u, gs, pl->alds);
+  pl->alds = M <= 4 && strips_alds(M, u) && (size_t)p.nw * strip_wave_lds(M, u) <= (64u << 10);
+  pl->lds = (size_t)p.nw * strip_wave_stride(M, mt, u, pl->alds);
   p.spx = (int)cdiv(N / kStripCols, 8);
   pl->grid = dim3(8 * p.spx);
   pl->block = dim3(64 * p.nw);
@@ -396,10 +380,17 @@ static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, 
       kernel<<<pl.grid, pl.block, pl.lds, stream>>>(p);
   };
   auto by_u = [&](auto MTc, auto AL) {
-    if constexpr (decltype(MTc)::value == 8) go(MTc, pk_int_c<2>{}, AL);  // U = 2 only
-    else if (u == 2) go(MTc, pk_int_c<2>{}, AL);
-    else if (u == 4) go(MTc, pk_int_c<4>{}, AL);
-    else go(MTc, pk_int_c<8>{}, AL);
+    constexpr int mt = decltype(MTc)::value;
+    if constexpr (mt == 8) {
+      go(MTc, pk_int_c<2>{}, AL);  // U = 2 only
+    } else if constexpr (mt == 4) {  // U <= 4 (strips_pick_u)
+      if (u == 2) go(MTc, pk_int_c<2>{}, AL);
+      else go(MTc, pk_int_c<4>{}, AL);
+    } else {
+      if (u == 2) go(MTc, pk_int_c<2>{}, AL);
+      else if (u == 4) go(MTc, pk_int_c<4>{}, AL);
+      else go(MTc, pk_int_c<8>{}, AL);
+    }
   };
   auto by_m = [&](auto AL) {
     if (M == 1) by_u(pk_int_c<1>{}, AL);
