@@ -19,7 +19,7 @@ under load); then 5 repetitions of exactly K steps. Before each repetition, 15 u
 read the 15 copies before the first timed one (350 MB, as the layers before it would in a
 decode loop), so a repetition never starts on weights its predecessor left in the caches,
 however small K is; then a spin kernel keeps the GPU busy while the host enqueues the timed
-calls (4.4 us of host time per call against 6.4 us of kernel), so they run back to back.
+calls (4.3 us of host time per call against 6.3 us of kernel), so they run back to back.
 The timed region runs from the first timed kernel's start to the last one's end: HIP events
 on the calls' stream that the first and last dispatches record themselves
 (``pk_w4a16_strips_run_events``), so no event packet sits inside it. The median repetition
