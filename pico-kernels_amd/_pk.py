@@ -62,6 +62,8 @@ _SIGNATURES = {
     "pk_w4a16_gemm_strips": (_i32, [_vp, _i64, _vp, _vp, _i32, _f32, _vp, _i32, _vp, _i32, _i64,
                                     _i32, _i32, _i32, _vp]),
     "pk_w4a16_strips_config": (_i32, [_i32]),
+    "pk_w4a16_strips_plan": (_i32, [_i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32),
+                                    ctypes.POINTER(_i32)]),
     "pk_w4a16_strips_prepare": (_vp, [_vp, _vp, _i32, _f32, _vp, _i32, _i32, _i32, _i32, _i64]),
     "pk_w4a16_strips_run": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp]),
     "pk_w4a16_strips_run_events": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp]),
@@ -517,6 +519,15 @@ class PreparedStrips:
 def w4a16_strips_config(blocks_per_wave: int) -> None:
     """Fix the strip GEMV's 1 KB blocks per wave (2, 4 or 8; 0: automatic)."""
     _check(lib().pk_w4a16_strips_config(int(blocks_per_wave)), "pk_w4a16_strips_config")
+
+
+def w4a16_strips_plan(M: int, N: int, K: int) -> tuple[int, int, int]:
+    """(strips per workgroup, 1 KB blocks per wave, waves per workgroup) of the strip GEMV's
+    launch for M rows of an (N, K) layer."""
+    ns, u, nw = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    _check(lib().pk_w4a16_strips_plan(M, N, K, ctypes.byref(ns), ctypes.byref(u), ctypes.byref(nw)),
+           "pk_w4a16_strips_plan")
+    return ns.value, u.value, nw.value
 
 
 def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | None,

@@ -46,6 +46,7 @@ namespace pk {
 constexpr int kStripCols = 16;       // columns per strip = per workgroup
 constexpr int kStripBlockRows = 128;  // rows per 1 KB block
 constexpr int kStripMaxWaves = 16;
+constexpr int kStripWaves8 = 8;  // waves per workgroup of the 5..8-row kernel
 
 struct StripParams {
   const pk_half* a;
@@ -62,7 +63,7 @@ struct StripParams {
   int kb;     // K / 128 blocks per strip
   int nw;     // waves per workgroup
   int iters;  // rounds of U blocks per wave
-  int spx;    // strips per XCD: ceil(N / 16 / 8)
+  int spx;    // units (strips, or pairs of strips) per XCD: ceil(units / 8)
 };
 
 // Group index of the 32-row row set at row `r0` (r0 % 32 == 0).
@@ -96,29 +97,42 @@ __device__ __forceinline__ void strip_dma16(__amdgpu_buffer_rsrc_t r, char* lds,
 // MT: activation rows the kernel carries (1, 2, 4 or 8); U: 1 KB blocks per wave per round.
 // ALDS: each wave DMAs its round's activations into its own LDS region ahead of its weight
 // loads and reads them from there (M * U <= 32); otherwise every lane loads its own from
-// global memory. Scales: every lane loads its own, beside its weights. Up to 16 waves per workgroup (the 8-row kernel runs U = 2 only,
-// which keeps it within the 128 registers that allows).
-template <int MT, int U, bool HAS_GS, bool ALDS>
-__global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripParams p) {
+// global memory. Scales: every lane loads its own, beside its weights. NS: strips per
+// workgroup. With NS = 2 (eight-row kernel, no staging) each wave takes the same blocks of two
+// neighbouring strips and multiplies both by one load of their activations, which halves the
+// activation bytes the wave reads per weight byte. Up to 16 waves per workgroup with one strip
+// (the 8-row kernel then runs U = 2 only, which keeps it within the 128 registers that
+// allows), up to 8 with two.
+template <int MT, int U, bool HAS_GS, bool ALDS, int NS = 1>
+__global__ __launch_bounds__(64 * (NS == 1 ? kStripMaxWaves : kStripWaves8)) void w4a16_strip_kernel(StripParams p) {
+  static_assert(NS == 1 || (NS == 2 && MT == 8 && !ALDS), "two strips per workgroup: 8-row kernel, unstaged");
   constexpr int MS = MT > 4 ? 2 : 1;            // MFMA sets of four activation rows
   constexpr int RR = MT < 4 ? MT : 4;           // registers of a set that carry rows
   extern __shared__ __align__(16) char strip_lds[];  // one region per wave
-  // Workgroup b runs on XCD b % 8 (round-robin dispatch): XCD x takes the contiguous strips
-  // [x * spx, (x + 1) * spx), so each 128-byte line of the output is written from one L2.
-  const int s = (int)(blockIdx.x & 7) * p.spx + (int)(blockIdx.x >> 3);
-  if (s >= p.N / kStripCols) return;
+  // Workgroup b runs on XCD b % 8 (round-robin dispatch): XCD x takes the contiguous units
+  // (strips, or pairs of strips) [x * spx, (x + 1) * spx), so each 128-byte line of the output
+  // is written from one L2, except where two XCDs' ranges meet.
+  const int nstrips = p.N / kStripCols;
+  const int s0 = NS * ((int)(blockIdx.x & 7) * p.spx + (int)(blockIdx.x >> 3));
+  if (s0 >= nstrips) return;
+  // An odd strip count leaves the last pair one strip: it loads that strip twice and stores it once.
+  const int ns_live = s0 + 1 < nstrips ? NS : 1;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int j = lane & 15, g = lane >> 4, cps = j & 3, rs = j >> 2;
   const int rowoff = 32 * rs + 8 * g;           // this lane's 8 rows inside a block
 
   const int64_t strip_bytes = (int64_t)p.kb * 1024;
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.qs + (int64_t)s * strip_bytes, (uint32_t)strip_bytes);
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda * 2));
   const int ngroups = HAS_GS ? p.K / p.group : 1;
-  const __amdgpu_buffer_rsrc_t rsc =
-      make_rsrc(HAS_GS ? (const void*)(p.ss + (int64_t)s * ngroups * kStripCols) : (const void*)p.qs,
-                HAS_GS ? (uint32_t)(ngroups * kStripCols * 2) : 16u);
+  __amdgpu_buffer_rsrc_t rq[NS], rsc[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int s = s0 + (st < ns_live ? st : 0);
+    rq[st] = make_rsrc(p.qs + (int64_t)s * strip_bytes, (uint32_t)strip_bytes);
+    rsc[st] = make_rsrc(HAS_GS ? (const void*)(p.ss + (int64_t)s * ngroups * kStripCols) : (const void*)p.qs,
+                        HAS_GS ? (uint32_t)(ngroups * kStripCols * 2) : 16u);
+  }
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda * 2));
   char* const w_act = strip_lds + wave * strip_wave_lds(p.M, U);
   int xoff[MS];  // this lane's activations inside block i: bytes of A (+ block), or of w_act
 #pragma unroll
@@ -128,11 +142,13 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
   }
   const pk_f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
   const pk_u4v neg8 = {0x80088008u, 0x80088008u, 0x80088008u, 0x80088008u};      // -8 * 2^-24
-  pk_f4 acc_lo[MS][2], acc_hi[MS][2];  // [set][column pair h]: 2^-24 / 2^-20 units
+  pk_f4 acc_lo[NS][MS][2], acc_hi[NS][MS][2];  // [strip][set][column pair h]: 2^-24 / 2^-20 units
 #pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
+  for (int st = 0; st < NS; ++st)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) acc_lo[ms][h] = acc_hi[ms][h] = zero4;
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) acc_lo[st][ms][h] = acc_hi[st][ms][h] = zero4;
 
   for (int it = 0; it < p.iters; ++it) {
     const int b0 = (it * p.nw + wave) * U;
@@ -149,20 +165,25 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
       asm volatile("" ::: "memory");
     }
     // ---- all loads of this round: U blocks of weights (and activations, scales) ----------
-    pk_u4v w[U], x[U][MS];
-    pk_u2v sc[U];
+    pk_u4v w[NS][U], x[U][MS];
+    pk_u2v sc[NS][U];
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const int b = min(b0 + i, p.kb - 1);  // past the strip: re-read, contributes zero
-      w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16, b * 1024, kPkLoadStream);
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+        w[st][i] = __builtin_amdgcn_raw_buffer_load_b128(rq[st], lane * 16, b * 1024, kPkLoadStream);
       if constexpr (!ALDS) {
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
           x[i][ms] = __builtin_amdgcn_raw_buffer_load_b128(ra, xoff[ms], b * (kStripBlockRows * 2), 0);
       }
-      if constexpr (HAS_GS)  // the row set's group (per lane where G < 128)
-        sc[i] = __builtin_amdgcn_raw_buffer_load_b64(
-            rsc, cps * 8 + strip_group(p, b * kStripBlockRows + 32 * rs) * (kStripCols * 2), 0, 0);
+      if constexpr (HAS_GS) {  // the row set's group (per lane where G < 128)
+#pragma unroll
+        for (int st = 0; st < NS; ++st)
+          sc[st][i] = __builtin_amdgcn_raw_buffer_load_b64(
+              rsc[st], cps * 8 + strip_group(p, b * kStripBlockRows + 32 * rs) * (kStripCols * 2), 0, 0);
+      }
     }
     if constexpr (ALDS) {
       // the wave's DMAs landed; its U weight (and U scale) loads, issued after them, may fly
@@ -196,35 +217,38 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
 #pragma unroll
         for (int r = 0; r < RR; ++r) o136[ms][r] = 17.0f * o8[ms][r];
       }
-      float s_lo[2], s_hi[2];
-      if constexpr (HAS_GS) {
-        const pk_half4 hs = __builtin_bit_cast(pk_half4, sc[i]);
-        s_lo[0] = (float)hs[0]; s_hi[0] = (float)hs[1];
-        s_lo[1] = (float)hs[2]; s_hi[1] = (float)hs[3];
-      }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t d0 = w[i][2 * h], d1 = w[i][2 * h + 1];  // nibbles u = v + 8
-        pk_u4v raw, lo;
-        raw[0] = __builtin_amdgcn_perm(d0, d0, 0x0c010c00u);  // rows e = 0, 1
-        raw[1] = __builtin_amdgcn_perm(d0, d0, 0x0c030c02u);  // rows 2, 3
-        raw[2] = __builtin_amdgcn_perm(d1, d1, 0x0c010c00u);  // rows 4, 5
-        raw[3] = __builtin_amdgcn_perm(d1, d1, 0x0c030c02u);  // rows 6, 7
+      for (int st = 0; st < NS; ++st) {  // O8 and O136 depend on the activations only
+        float s_lo[2], s_hi[2];
+        if constexpr (HAS_GS) {
+          const pk_half4 hs = __builtin_bit_cast(pk_half4, sc[st][i]);
+          s_lo[0] = (float)hs[0]; s_hi[0] = (float)hs[1];
+          s_lo[1] = (float)hs[2]; s_hi[1] = (float)hs[3];
+        }
 #pragma unroll
-        for (int d = 0; d < 4; ++d) lo[d] = raw[d] & 0x000f000fu;
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t d0 = w[st][i][2 * h], d1 = w[st][i][2 * h + 1];  // nibbles u = v + 8
+          pk_u4v raw, lo;
+          raw[0] = __builtin_amdgcn_perm(d0, d0, 0x0c010c00u);  // rows e = 0, 1
+          raw[1] = __builtin_amdgcn_perm(d0, d0, 0x0c030c02u);  // rows 2, 3
+          raw[2] = __builtin_amdgcn_perm(d1, d1, 0x0c010c00u);  // rows 4, 5
+          raw[3] = __builtin_amdgcn_perm(d1, d1, 0x0c030c02u);  // rows 6, 7
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms) {
-          const pk_f4 clo = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[ms], __builtin_bit_cast(pk_half8, lo), o8[ms], 0, 0, 0);
-          const pk_f4 craw = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[ms], __builtin_bit_cast(pk_half8, raw), o136[ms], 0, 0, 0);
+          for (int d = 0; d < 4; ++d) lo[d] = raw[d] & 0x000f000fu;
 #pragma unroll
-          for (int r = 0; r < RR; ++r) {
-            const float hi = craw[r] - clo[r];
-            if constexpr (HAS_GS) {
-              acc_lo[ms][h][r] = __builtin_fmaf(clo[r], s_lo[h], acc_lo[ms][h][r]);
-              acc_hi[ms][h][r] = __builtin_fmaf(hi, s_hi[h], acc_hi[ms][h][r]);
-            } else {
-              acc_lo[ms][h][r] += clo[r];
-              acc_hi[ms][h][r] += hi;
+          for (int ms = 0; ms < MS; ++ms) {
+            const pk_f4 clo = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[ms], __builtin_bit_cast(pk_half8, lo), o8[ms], 0, 0, 0);
+            const pk_f4 craw = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[ms], __builtin_bit_cast(pk_half8, raw), o136[ms], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < RR; ++r) {
+              const float hi = craw[r] - clo[r];
+              if constexpr (HAS_GS) {
+                acc_lo[st][ms][h][r] = __builtin_fmaf(clo[r], s_lo[h], acc_lo[st][ms][h][r]);
+                acc_hi[st][ms][h][r] = __builtin_fmaf(hi, s_hi[h], acc_hi[st][ms][h][r]);
+              } else {
+                acc_lo[st][ms][h][r] += clo[r];
+                acc_hi[st][ms][h][r] += hi;
+              }
             }
           }
         }
@@ -239,24 +263,28 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
   // writes its 4 row sets; then thread (m, part, col) adds the partials of waves
   // part, part + 4, ... (row sets 0..3 each), and the four parts are added by two shuffles:
   // ((part 0 + part 1) + (part 2 + part 3)), the same tree on every call.
-  // red(w)[rs][m][cps]: wave w's partials, in its own region (after its last LDS reads of
-  // staged activations: a wave's LDS accesses complete in order).
+  // red(w, st)[rs][m][cps]: wave w's partials of strip st, in its own region (after its last
+  // LDS reads of staged activations: a wave's LDS accesses complete in order).
   const int wstride = strip_wave_stride(p.M, MT, U, ALDS);
-  auto red = [&](int w, int set, int m, int q) {
-    return reinterpret_cast<pk_f4*>(strip_lds + w * wstride) + (set * MT + m) * (kStripCols / 4) + q;
+  auto red = [&](int w, int st, int set, int m, int q) {
+    return reinterpret_cast<pk_f4*>(strip_lds + w * NS * wstride + st * wstride) + (set * MT + m) * (kStripCols / 4) + q;
   };
   if ((lane >> 4) == rs) {
 #pragma unroll
-    for (int ms = 0; ms < MS; ++ms)
+    for (int st = 0; st < NS; ++st)
 #pragma unroll
-      for (int r = 0; r < RR; ++r)
-        if (4 * ms + r < MT)
-          *red(wave, rs, 4 * ms + r, cps) = pk_f4{acc_lo[ms][0][r], acc_hi[ms][0][r],
-                                                  acc_lo[ms][1][r], acc_hi[ms][1][r]};
+      for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+        for (int r = 0; r < RR; ++r)
+          if (4 * ms + r < MT)
+            *red(wave, st, rs, 4 * ms + r, cps) = pk_f4{acc_lo[st][ms][0][r], acc_hi[st][ms][0][r],
+                                                        acc_lo[st][ms][1][r], acc_hi[st][ms][1][r]};
   }
   __syncthreads();
   const int rows = p.M < MT ? p.M : MT;
-  for (int m = wave; m < rows; m += p.nw) {  // wave-uniform: one activation row per wave
+  // wave-uniform: one (strip, activation row) per wave
+  for (int sm = wave; sm < ns_live * rows; sm += p.nw) {
+    const int st = sm / rows, m = sm - st * rows;
     const int part = lane >> 4, col = lane & 15;
     const int kmax = (p.nw + 3) >> 2;  // wave-uniform
     float v = 0.0f;
@@ -267,7 +295,7 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
         const bool live = part + 4 * k < p.nw;
         float q4[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) q4[q] = (*red(wv, q, m, col >> 2))[col & 3];
+        for (int q = 0; q < 4; ++q) q4[q] = (*red(wv, st, q, m, col >> 2))[col & 3];
 #pragma unroll
         for (int q = 0; q < 4; ++q) v += live ? q4[q] : 0.0f;
       }
@@ -276,7 +304,7 @@ __global__ __launch_bounds__(64 * kStripMaxWaves) void w4a16_strip_kernel(StripP
     v += __shfl_xor(v, 32, 64);
     if (part == 0) {
       v *= (col & 1) ? 1048576.0f : 16777216.0f;  // exact: powers of two
-      const int n = s * kStripCols + col;
+      const int n = (s0 + st) * kStripCols + col;
       store_from_f32(p.c, p.c_dtype, (int64_t)m * p.ldc + n, p.epi(v, n));
     }
   }
@@ -314,7 +342,25 @@ static int strips_pick_u(int M, int N, int kb) {
 // staging). Measured on MI355X at M = 8 against 4 and 16 waves and against staging (graphs over
 // rotating weight copies; 4096 x 6144 / 4096 x 4096 / 4096 x 14336 / 14336 x 4096 / 4096 x
 // 11008): 8.09 / 5.56 / 13.3 / 11.7 / 10.9 us; staged, 9.4 / 7.3 / 16.8 / 19.5 / 14.2.
-constexpr int kStripWaves8 = 8;
+// Strips per workgroup (NS) and blocks per wave for them: at eight rows a wave reads two bytes
+// of activations per weight byte, which costs more than the weights (measured: the same
+// kernel with its activation loads left out ran qkv 8.3 -> 5.8 us, gate_up 13.4 -> 10.2), so
+// layers with strips enough for it give each wave the same blocks of two strips and one load
+// of their activations: with U = 2 (one workgroup per CU: 166 registers) from 320 to 512
+// strips, with U = 1 (two per CU) above 768; never below 32 blocks (K < 4096), where the
+// rounds are few. Measured at M = 8 (one strip / two): 4096 x 5120 8.46 / 7.19 us, 4096 x
+// 6144 8.24 / 7.22, 4096 x 8192 8.08 / 7.59, 8192 x 6144 13.35 / 10.82, 8192 x 8192 13.81 /
+// 11.97; U = 1: 4096 x 14336 13.36 / 12.02, 5120 x 13824 18.47 / 14.06, 4096 x 28672 22.31 /
+// 21.64; left at one strip: 256 strips (4096 x 4096 5.55 against 6.95 for pairs, 14336 x
+// 4096 11.73 against 16.1: half the CUs would idle), 688 and 768 (4096 x 11008 10.95 /
+// 11.05, 4096 x 12288 10.95 / 10.98), 2048 x 8192 (5.58 / 5.70).
+static void strips_pick_pair(int M, int nstrips, int kb, int* ns, int* u) {
+  *ns = 1;
+  *u = 2;
+  if (M <= 4 || kb < 32) return;
+  if (nstrips >= 320 && nstrips <= 512) *ns = 2;
+  else if (nstrips > 768) *ns = 2, *u = 1;
+}
 
 // Activations staged per wave in LDS: at most 8 KB per wave (M * U <= 32).
 static bool strips_alds(int M, int U) { return (int64_t)M * U <= 32; }
@@ -323,6 +369,7 @@ static bool strips_alds(int M, int U) { return (int64_t)M * U <= 32; }
 struct StripPlan {
   StripParams p;  // a, c, ldc and M are filled in per call
   int u;
+  int ns;  // strips per workgroup
   bool alds;
   size_t lds;
   dim3 grid, block;
@@ -346,16 +393,18 @@ static void strips_plan(const uint8_t* qs, const void* ss, int group, OutEpi epi
   p.N = N;
   p.K = K;
   p.kb = K / kStripBlockRows;
-  const int u = strips_pick_u(M, N, p.kb);
+  int u = strips_pick_u(M, N, p.kb), ns = 1;
+  if (M > 4) strips_pick_pair(M, N / kStripCols, p.kb, &ns, &u);
   const int waves_one_round = (int)cdiv(p.kb, u);
   const int max_waves = M > 4 ? kStripWaves8 : kStripMaxWaves;
   p.nw = waves_one_round < max_waves ? waves_one_round : max_waves;
   p.iters = (int)cdiv(p.kb, (int64_t)u * p.nw);
   const int mt = M == 1 ? 1 : M == 2 ? 2 : M <= 4 ? 4 : 8;
   pl->u = u;
+  pl->ns = ns;
   pl->alds = M <= 4 && strips_alds(M, u) && (size_t)p.nw * strip_wave_lds(M, u) <= (64u << 10);
-  pl->lds = (size_t)p.nw * strip_wave_stride(M, mt, u, pl->alds);
-  p.spx = (int)cdiv(N / kStripCols, 8);
+  pl->lds = (size_t)p.nw * ns * strip_wave_stride(M, mt, u, pl->alds);
+  p.spx = (int)cdiv(cdiv(N / kStripCols, ns), 8);
   pl->grid = dim3(8 * p.spx);
   pl->block = dim3(64 * p.nw);
 }
@@ -370,10 +419,10 @@ static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, 
   p.ldc = ldc;
   const int M = p.M, u = pl.u;
   const bool gs = p.ss != nullptr;
-  auto go = [&](auto MTc, auto Uc, auto AL) {
-    constexpr int mt = decltype(MTc)::value, uu = decltype(Uc)::value;
+  auto go = [&](auto MTc, auto Uc, auto AL, auto NSc) {
+    constexpr int mt = decltype(MTc)::value, uu = decltype(Uc)::value, ns = decltype(NSc)::value;
     constexpr bool al = decltype(AL)::value != 0;
-    auto kernel = gs ? w4a16_strip_kernel<mt, uu, true, al> : w4a16_strip_kernel<mt, uu, false, al>;
+    auto kernel = gs ? w4a16_strip_kernel<mt, uu, true, al, ns> : w4a16_strip_kernel<mt, uu, false, al, ns>;
     if (start || stop)
       hipExtLaunchKernelGGL(kernel, pl.grid, pl.block, (uint32_t)pl.lds, stream, start, stop, 0, p);
     else
@@ -381,15 +430,18 @@ static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, 
   };
   auto by_u = [&](auto MTc, auto AL) {
     constexpr int mt = decltype(MTc)::value;
-    if constexpr (mt == 8) {
-      go(MTc, pk_int_c<2>{}, AL);  // U = 2 only
+    constexpr pk_int_c<1> one{};
+    if constexpr (mt == 8) {  // U = 2 with one strip per workgroup; U = 2 or 1 with two
+      if (pl.ns == 1) go(MTc, pk_int_c<2>{}, AL, one);
+      else if (u == 2) go(MTc, pk_int_c<2>{}, AL, pk_int_c<2>{});
+      else go(MTc, pk_int_c<1>{}, AL, pk_int_c<2>{});
     } else if constexpr (mt == 4) {  // U <= 4 (strips_pick_u)
-      if (u == 2) go(MTc, pk_int_c<2>{}, AL);
-      else go(MTc, pk_int_c<4>{}, AL);
+      if (u == 2) go(MTc, pk_int_c<2>{}, AL, one);
+      else go(MTc, pk_int_c<4>{}, AL, one);
     } else {
-      if (u == 2) go(MTc, pk_int_c<2>{}, AL);
-      else if (u == 4) go(MTc, pk_int_c<4>{}, AL);
-      else go(MTc, pk_int_c<8>{}, AL);
+      if (u == 2) go(MTc, pk_int_c<2>{}, AL, one);
+      else if (u == 4) go(MTc, pk_int_c<4>{}, AL, one);
+      else go(MTc, pk_int_c<8>{}, AL, one);
     }
   };
   auto by_m = [&](auto AL) {
@@ -425,6 +477,19 @@ using namespace pk;
 extern "C" int pk_w4a16_strips_config(int blocks_per_wave) {
   PK_REQUIRE(strips_config_set(blocks_per_wave),
              "pk_w4a16_strips_config: %d is not 0 (automatic), 2, 4 or 8", blocks_per_wave);
+  return PK_OK;
+}
+
+extern "C" int pk_w4a16_strips_plan(int M, int N, int K, int* strips_per_workgroup,
+                                    int* blocks_per_wave, int* waves) {
+  PK_REQUIRE(M >= 1 && M <= 8, "pk_w4a16_strips_plan: M=%d (the strip layout serves 1..8 rows)", M);
+  PK_REQUIRE(N >= 16 && N % 16 == 0 && K >= 128 && K % 128 == 0,
+             "pk_w4a16_strips_plan: needs N %% 16 == 0 and K %% 128 == 0 (N=%d K=%d)", N, K);
+  StripPlan pl;
+  strips_plan(nullptr, nullptr, K, OutEpi(1.0f, nullptr, PK_F32), PK_F32, M, N, K, K, &pl);
+  if (strips_per_workgroup) *strips_per_workgroup = pl.ns;
+  if (blocks_per_wave) *blocks_per_wave = pl.u;
+  if (waves) *waves = pl.p.nw;
   return PK_OK;
 }
 

@@ -35,8 +35,8 @@ it (``out % 16 == 0``, ``in % 128 == 0``, groups of a multiple of 32 that divide
 multiples of it, or per-input scales: ``QuantLinear.decode``) keep a second copy of the codes
 and group scales in the strip layout (``_pk.strip_weights`` / ``strip_scales``: each
 16-output strip's inputs contiguous), and calls of at most ``decode_rows`` rows run the
-one-launch strip GEMV on it (``pk_w4a16_gemm_strips``; ``decode_rows``: 8 rows on layers of at
-most 4096 x 6144 weights). The int4 codes are a quarter of the
+one-launch strip GEMV on it (``pk_w4a16_gemm_strips``; ``decode_rows``: 8 rows, or 4 on layers
+of more than 16384 outputs). The int4 codes are a quarter of the
 fp16 weights' bytes, so both copies together are half of them; ``decode_layout=False`` keeps
 one copy. The copies are derived buffers, outside the state dict. ``codes()`` /
 ``set_codes()``, the state dict and the file format use ``pack_int4_n`` order either way.
@@ -67,14 +67,15 @@ FORMAT_VERSION = 2
 SCHEMES = ("group", "per_input")
 _OUT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 # Rows up to which forward runs the strip-layout GEMV (when the layer keeps that copy): 8, or 4
-# on layers of more than 768 strips of 16 output columns. Measured on MI355X (graphs over
+# on layers of more than 1024 strips of 16 output columns. Measured on MI355X (graphs over
 # rotating weight copies, against the block layout's kernels): M = 1..4 faster on every
-# Llama-3-8B layer (4096 x 11008 M = 4: 8.5 against 10.4 us); M = 8 faster on qkv (8.1 against
-# 9.0), o_proj (5.6 against 7.7), down (11.7 against 13.7) and 4096 x 11008 (10.9 against 12.2),
-# slower on gate_up, 4096 x 14336 (13.3 against 12.7).
+# Llama-3-8B layer (4096 x 11008 M = 4: 8.5 against 10.4 us); M = 5..8 faster on qkv (M = 8:
+# 7.4 against 9.0), o_proj (5.6 against 7.7), down (11.7 against 13.7), gate_up (4096 x 14336:
+# 11.9 against 12.8), 4096 x 11008 (11.0 against 12.2) and 5120 x 13824 (14.2 against 16.2);
+# slower on 4096 x 28672 (1792 strips: 22.1 against 21.7).
 DECODE_MAX_ROWS = 8
 DECODE_MAX_ROWS_WIDE = 4
-DECODE_WIDE_STRIPS = 768
+DECODE_WIDE_STRIPS = 1024
 
 
 def decode_rows(in_features: int, out_features: int) -> int:

@@ -56,6 +56,27 @@ def test_strips_ok_rules():
     assert not _pk.strips_ok(4096, 4096, 16)       # not a multiple of 32
 
 
+def test_strips_plan_rule():
+    """Two strips per workgroup only for 5..8 rows, on layers of 320..512 strips (U = 2) or
+    more than 768 (U = 1), with at least 32 blocks of K."""
+    for M in range(1, 9):
+        for N, K in [(6144, 4096), (4096, 4096), (14336, 4096), (11008, 4096), (4096, 14336),
+                     (8192, 2048), (5120, 4096), (8192, 8192), (12304, 4096), (13824, 5120)]:
+            ns, u, nw = _pk.w4a16_strips_plan(M, N, K)
+            strips, kb = N // 16, K // 128
+            want = 1
+            if M > 4 and kb >= 32 and (320 <= strips <= 512 or strips > 768):
+                want = 2
+            assert ns == want, (M, N, K, ns)
+            if ns == 2:
+                assert (u, nw) == ((2 if strips <= 512 else 1), 8), (M, N, K, u, nw)
+            elif M > 4:
+                assert u == 2 and nw <= 8
+    assert _pk.w4a16_strips_plan(8, 6144, 4096) == (2, 2, 8)
+    with pytest.raises(_pk.PicoKernelsError):
+        _pk.w4a16_strips_plan(9, 6144, 4096)
+
+
 def test_strips_rejects_bad_arguments_without_a_gpu():
     f = _pk.lib().pk_w4a16_gemm_strips
     p = 1 << 20  # never dereferenced: every call fails its checks first
@@ -119,6 +140,48 @@ def test_strips_rows(M, K, N, cuda):
     y = _run(a, words, s16, 128, cuda)
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
     assert oracle.rel_fro(y.cpu().numpy(), ref) <= 1e-4, (M, K, N)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [5, 8])
+@pytest.mark.parametrize("K,N,G,plan", [
+    (4096, 5136, 128, (2, 2)),   # 321 strips: the last pair holds one strip
+    (5120, 6144, 64, (2, 2)),    # 40 blocks: a partial last round; groups of 64
+    (4096, 12304, 128, (2, 1)),  # 769 strips, odd
+    (4096, 14336, 0, (2, 1)),    # per-tensor mode
+])
+def test_strips_two_strips_per_workgroup(M, K, N, G, plan, cuda):
+    """The 5..8-row kernel with two strips per workgroup (one activation load for both)
+    against the oracle, and repeatable bit for bit."""
+    assert _pk.w4a16_strips_plan(M, N, K)[:2] == plan
+    a, codes, s16, words = _case(M, K, N, G, 11 * M + N)
+    y = _run(a, words, s16, G, cuda, scale=0.5 if G == 0 else 1.0)
+    if G:
+        ref = oracle.w4a16_ref(a.numpy(), codes, s16, G)
+    else:
+        ref = oracle.int4_gemm_ref(a.numpy(), codes, 0.5)
+    assert oracle.rel_fro(y.cpu().numpy(), ref) <= 1e-4, (M, K, N)
+    assert torch.equal(y, _run(a, words, s16, G, cuda, scale=0.5 if G == 0 else 1.0))
+
+
+@pytest.mark.gpu
+def test_strips_two_strips_bias_bf16_and_views(cuda):
+    """Two strips per workgroup with a bias, bf16 output into a wider view and strided
+    activations: nothing is written past the view."""
+    M, K, N = 7, 4096, 6144
+    assert _pk.w4a16_strips_plan(M, N, K)[0] == 2
+    a, codes, s16, words = _case(M, K, N, 128, 123)
+    bias = torch.randn(N, generator=_gen(124)).half()
+    big = torch.zeros(M, K + 64, dtype=torch.float16)
+    big[:, 32:32 + K] = a
+    av = big.to(cuda)[:, 32:32 + K]
+    qs = _pk.strip_weights(words).to(cuda)
+    ss = _pk.strip_scales(torch.from_numpy(s16)).to(cuda)
+    out = torch.full((M, N + 16), 7.0, dtype=torch.bfloat16, device=cuda)
+    _pk.w4a16_gemm_strips(av, qs, ss, 128, 1.0, torch.bfloat16, out=out[:, :N], bias=bias.to(cuda))
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128) + bias.float().numpy()
+    assert oracle.rel_fro(out[:, :N].float().cpu().numpy(), ref) <= 8e-3
+    assert bool((out[:, N:] == 7.0).all())
 
 
 @pytest.mark.gpu
