@@ -201,7 +201,7 @@ int pk_w4a16_gemm_strips(const void* a, int64_t lda, const uint8_t* qstrips, con
 int pk_w4a16_strips_config(int blocks_per_wave);
 
 /* The launch pk_w4a16_gemm_strips plans for M rows of an (N, K) layer: 16-column strips per
- * workgroup (1, or 2 for 5..8 rows on layers with strips enough: each wave then multiplies
+ * workgroup (1, or 2 for 2..8 rows on layers with strips enough: each wave then multiplies
  * the same blocks of two strips by one load of their activations), 1 KB blocks per wave per
  * round, and waves per workgroup (any output pointer may be NULL). For tests and measurement;
  * no counterpart in the reference. */

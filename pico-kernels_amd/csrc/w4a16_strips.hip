@@ -85,8 +85,11 @@ __host__ __device__ __forceinline__ int strip_wave_lds(int M, int U) { return (i
 // 1 KB, which holds the MT * 256 bytes whenever M > MT / 2); otherwise each wave has a
 // region of this size.
 __host__ __device__ __forceinline__ int strip_fold_lds(int MT) { return 4 * MT * 64; }
-__host__ __device__ __forceinline__ int strip_wave_stride(int M, int MT, int U, bool alds) {
-  return alds ? strip_wave_lds(M, U) : strip_fold_lds(MT);
+// A wave's LDS region: its staged activations (ALDS), later overwritten by its partials of
+// each of its NS strips.
+__host__ __device__ __forceinline__ int strip_wave_stride(int M, int MT, int U, bool alds, int ns) {
+  const int fold = ns * strip_fold_lds(MT);
+  return alds && strip_wave_lds(M, U) > fold ? strip_wave_lds(M, U) : fold;
 }
 
 // 16 bytes per lane, global -> LDS: lane L writes lds + 16 L.
@@ -98,14 +101,14 @@ __device__ __forceinline__ void strip_dma16(__amdgpu_buffer_rsrc_t r, char* lds,
 // ALDS: each wave DMAs its round's activations into its own LDS region ahead of its weight
 // loads and reads them from there (M * U <= 32); otherwise every lane loads its own from
 // global memory. Scales: every lane loads its own, beside its weights. NS: strips per
-// workgroup. With NS = 2 (eight-row kernel, no staging) each wave takes the same blocks of two
-// neighbouring strips and multiplies both by one load of their activations, which halves the
+// workgroup. With NS = 2 each wave takes the same blocks of two neighbouring strips and
+// multiplies both by one load (or one staged copy) of their activations, which halves the
 // activation bytes the wave reads per weight byte. Up to 16 waves per workgroup with one strip
 // (the 8-row kernel then runs U = 2 only, which keeps it within the 128 registers that
 // allows), up to 8 with two.
 template <int MT, int U, bool HAS_GS, bool ALDS, int NS = 1>
 __global__ __launch_bounds__(64 * (NS == 1 ? kStripMaxWaves : kStripWaves8)) void w4a16_strip_kernel(StripParams p) {
-  static_assert(NS == 1 || (NS == 2 && MT == 8 && !ALDS), "two strips per workgroup: 8-row kernel, unstaged");
+  static_assert(NS == 1 || NS == 2, "one or two strips per workgroup");
   constexpr int MS = MT > 4 ? 2 : 1;            // MFMA sets of four activation rows
   constexpr int RR = MT < 4 ? MT : 4;           // registers of a set that carry rows
   extern __shared__ __align__(16) char strip_lds[];  // one region per wave
@@ -133,7 +136,8 @@ __global__ __launch_bounds__(64 * (NS == 1 ? kStripMaxWaves : kStripWaves8)) voi
                         HAS_GS ? (uint32_t)(ngroups * kStripCols * 2) : 16u);
   }
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda * 2));
-  char* const w_act = strip_lds + wave * strip_wave_lds(p.M, U);
+  const int wstride = strip_wave_stride(p.M, MT, U, ALDS, NS);
+  char* const w_act = strip_lds + wave * wstride;
   int xoff[MS];  // this lane's activations inside block i: bytes of A (+ block), or of w_act
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms) {
@@ -265,9 +269,8 @@ __global__ __launch_bounds__(64 * (NS == 1 ? kStripMaxWaves : kStripWaves8)) voi
   // ((part 0 + part 1) + (part 2 + part 3)), the same tree on every call.
   // red(w, st)[rs][m][cps]: wave w's partials of strip st, in its own region (after its last
   // LDS reads of staged activations: a wave's LDS accesses complete in order).
-  const int wstride = strip_wave_stride(p.M, MT, U, ALDS);
   auto red = [&](int w, int st, int set, int m, int q) {
-    return reinterpret_cast<pk_f4*>(strip_lds + w * NS * wstride + st * wstride) + (set * MT + m) * (kStripCols / 4) + q;
+    return reinterpret_cast<pk_f4*>(strip_lds + w * wstride + st * strip_fold_lds(MT)) + (set * MT + m) * (kStripCols / 4) + q;
   };
   if ((lane >> 4) == rs) {
 #pragma unroll
@@ -353,13 +356,22 @@ static int strips_pick_u(int M, int N, int kb) {
 // 11.97; U = 1: 4096 x 14336 13.36 / 12.02, 5120 x 13824 18.47 / 14.06, 4096 x 28672 22.31 /
 // 21.64; left at one strip: 256 strips (4096 x 4096 5.55 against 6.95 for pairs, 14336 x
 // 4096 11.73 against 16.1: half the CUs would idle), 688 and 768 (4096 x 11008 10.95 /
-// 11.05, 4096 x 12288 10.95 / 10.98), 2048 x 8192 (5.58 / 5.70).
+// 11.05, 4096 x 12288 10.95 / 10.98), 2048 x 8192 (5.58 / 5.70). Two to four rows (staged
+// activations, the same U, at most 8 waves) pair on layers of more than 768 strips and 32..64
+// blocks: M = 2 / 3 / 4 on 8192 x 14336 15.9 / 17.4 / 18.1 -> 12.8 / 14.0 / 14.9 us, 5120 x
+// 13824 10.9 / 11.7 / 12.3 -> 10.5 / 11.2 / 11.6, 4096 x 14336 8.4-8.6 / 8.9 / 9.2 -> 8.2 /
+// 8.6 / 8.9, 4096 x 28672 unchanged (13.5 / 15.0 / 15.2); one row stays on one strip
+// (4096 x 11008 6.19 against 7.24, 4096 x 14336 7.48 / 7.51).
 static void strips_pick_pair(int M, int nstrips, int kb, int* ns, int* u) {
   *ns = 1;
-  *u = 2;
-  if (M <= 4 || kb < 32) return;
-  if (nstrips >= 320 && nstrips <= 512) *ns = 2;
-  else if (nstrips > 768) *ns = 2, *u = 1;
+  if (M > 4) *u = 2;
+  if (kb < 32) return;
+  if (M > 4) {
+    if (nstrips >= 320 && nstrips <= 512) *ns = 2;
+    else if (nstrips > 768) *ns = 2, *u = 1;
+  } else if (M >= 2 && nstrips > 768 && kb <= 64) {
+    *ns = 2;  // blocks per wave as for one strip
+  }
 }
 
 // Activations staged per wave in LDS: at most 8 KB per wave (M * U <= 32).
@@ -394,16 +406,16 @@ static void strips_plan(const uint8_t* qs, const void* ss, int group, OutEpi epi
   p.K = K;
   p.kb = K / kStripBlockRows;
   int u = strips_pick_u(M, N, p.kb), ns = 1;
-  if (M > 4) strips_pick_pair(M, N / kStripCols, p.kb, &ns, &u);
+  strips_pick_pair(M, N / kStripCols, p.kb, &ns, &u);
   const int waves_one_round = (int)cdiv(p.kb, u);
-  const int max_waves = M > 4 ? kStripWaves8 : kStripMaxWaves;
+  const int max_waves = M > 4 || ns == 2 ? kStripWaves8 : kStripMaxWaves;  // the kernel's bound
   p.nw = waves_one_round < max_waves ? waves_one_round : max_waves;
   p.iters = (int)cdiv(p.kb, (int64_t)u * p.nw);
   const int mt = M == 1 ? 1 : M == 2 ? 2 : M <= 4 ? 4 : 8;
   pl->u = u;
   pl->ns = ns;
   pl->alds = M <= 4 && strips_alds(M, u) && (size_t)p.nw * strip_wave_lds(M, u) <= (64u << 10);
-  pl->lds = (size_t)p.nw * ns * strip_wave_stride(M, mt, u, pl->alds);
+  pl->lds = (size_t)p.nw * strip_wave_stride(M, mt, u, pl->alds, ns);
   p.spx = (int)cdiv(cdiv(N / kStripCols, ns), 8);
   pl->grid = dim3(8 * p.spx);
   pl->block = dim3(64 * p.nw);
@@ -431,13 +443,21 @@ static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, 
   auto by_u = [&](auto MTc, auto AL) {
     constexpr int mt = decltype(MTc)::value;
     constexpr pk_int_c<1> one{};
+    auto go1 = [&](auto MT2, auto U2, auto AL2) {
+      if (pl.ns == 2) go(MT2, U2, AL2, pk_int_c<2>{});
+      else go(MT2, U2, AL2, one);
+    };
     if constexpr (mt == 8) {  // U = 2 with one strip per workgroup; U = 2 or 1 with two
       if (pl.ns == 1) go(MTc, pk_int_c<2>{}, AL, one);
       else if (u == 2) go(MTc, pk_int_c<2>{}, AL, pk_int_c<2>{});
       else go(MTc, pk_int_c<1>{}, AL, pk_int_c<2>{});
     } else if constexpr (mt == 4) {  // U <= 4 (strips_pick_u)
-      if (u == 2) go(MTc, pk_int_c<2>{}, AL, one);
-      else go(MTc, pk_int_c<4>{}, AL, one);
+      if (u == 2) go1(MTc, pk_int_c<2>{}, AL);
+      else go1(MTc, pk_int_c<4>{}, AL);
+    } else if constexpr (mt == 2) {  // two strips: U <= 4 (kb <= 64, more than 256 strips)
+      if (u == 2) go1(MTc, pk_int_c<2>{}, AL);
+      else if (u == 4) go1(MTc, pk_int_c<4>{}, AL);
+      else go(MTc, pk_int_c<8>{}, AL, one);
     } else {
       if (u == 2) go(MTc, pk_int_c<2>{}, AL, one);
       else if (u == 4) go(MTc, pk_int_c<4>{}, AL, one);

@@ -57,22 +57,31 @@ def test_strips_ok_rules():
 
 
 def test_strips_plan_rule():
-    """Two strips per workgroup only for 5..8 rows, on layers of 320..512 strips (U = 2) or
-    more than 768 (U = 1), with at least 32 blocks of K."""
+    """Two strips per workgroup with at least 32 blocks of K: for 5..8 rows on layers of
+    320..512 strips (U = 2) or more than 768 (U = 1); for 2..4 rows on layers of more than 768
+    strips and at most 64 blocks (U as for one strip). Eight waves at most with two strips."""
     for M in range(1, 9):
         for N, K in [(6144, 4096), (4096, 4096), (14336, 4096), (11008, 4096), (4096, 14336),
-                     (8192, 2048), (5120, 4096), (8192, 8192), (12304, 4096), (13824, 5120)]:
+                     (8192, 2048), (5120, 4096), (8192, 8192), (12304, 4096), (13824, 5120),
+                     (14336, 8192), (14336, 14336), (28672, 4096)]:
             ns, u, nw = _pk.w4a16_strips_plan(M, N, K)
             strips, kb = N // 16, K // 128
             want = 1
             if M > 4 and kb >= 32 and (320 <= strips <= 512 or strips > 768):
                 want = 2
+            if 2 <= M <= 4 and 32 <= kb <= 64 and strips > 768:
+                want = 2
             assert ns == want, (M, N, K, ns)
             if ns == 2:
-                assert (u, nw) == ((2 if strips <= 512 else 1), 8), (M, N, K, u, nw)
+                assert nw <= 8, (M, N, K, nw)
+                if M > 4:
+                    assert u == (2 if strips <= 512 else 1), (M, N, K, u)
+                else:
+                    assert (u, nw) == (4, 8), (M, N, K, u, nw)
             elif M > 4:
                 assert u == 2 and nw <= 8
     assert _pk.w4a16_strips_plan(8, 6144, 4096) == (2, 2, 8)
+    assert _pk.w4a16_strips_plan(2, 14336, 4096) == (2, 4, 8)
     with pytest.raises(_pk.PicoKernelsError):
         _pk.w4a16_strips_plan(9, 6144, 4096)
 
@@ -140,6 +149,20 @@ def test_strips_rows(M, K, N, cuda):
     y = _run(a, words, s16, 128, cuda)
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, 128)
     assert oracle.rel_fro(y.cpu().numpy(), ref) <= 1e-4, (M, K, N)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [2, 3, 4])
+@pytest.mark.parametrize("K,N,G", [(4096, 12304, 128), (8192, 12304, 64)])
+def test_strips_two_strips_staged_rows(M, K, N, G, cuda):
+    """Two to four rows with two strips per workgroup (activations staged per wave in LDS and
+    used for both strips; 769 strips, so the last pair holds one) against the oracle."""
+    assert _pk.w4a16_strips_plan(M, N, K)[0] == 2
+    a, codes, s16, words = _case(M, K, N, G, 13 * M + K)
+    y = _run(a, words, s16, G, cuda)
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, G)
+    assert oracle.rel_fro(y.cpu().numpy(), ref) <= 1e-4, (M, K, N)
+    assert torch.equal(y, _run(a, words, s16, G, cuda))
 
 
 @pytest.mark.gpu
