@@ -190,8 +190,10 @@ __global__ __launch_bounds__(64 * (NS == 1 ? kStripMaxWaves : kStripWaves8)) voi
       }
     }
     if constexpr (ALDS) {
-      // the wave's DMAs landed; its U weight (and U scale) loads, issued after them, may fly
-      constexpr int nv = (HAS_GS ? 2 : 1) * U;
+      // the wave's DMAs landed; its NS * U weight (and NS * U scale) loads, issued after them,
+      // may fly
+      constexpr int nv = (HAS_GS ? 2 : 1) * U * NS;
+      static_assert(nv < 64, "vmcnt holds at most 63");
       __builtin_amdgcn_s_waitcnt((nv & 15) | (7 << 4) | (15 << 8) | ((nv >> 4) << 14));
       asm volatile("" ::: "memory");
 #pragma unroll
@@ -358,10 +360,11 @@ static int strips_pick_u(int M, int N, int kb) {
 // 4096 11.73 against 16.1: half the CUs would idle), 688 and 768 (4096 x 11008 10.95 /
 // 11.05, 4096 x 12288 10.95 / 10.98), 2048 x 8192 (5.58 / 5.70). Two to four rows (staged
 // activations, the same U, at most 8 waves) pair on layers of more than 768 strips and 32..64
-// blocks: M = 2 / 3 / 4 on 8192 x 14336 15.9 / 17.4 / 18.1 -> 12.8 / 14.0 / 14.9 us, 5120 x
-// 13824 10.9 / 11.7 / 12.3 -> 10.5 / 11.2 / 11.6, 4096 x 14336 8.4-8.6 / 8.9 / 9.2 -> 8.2 /
-// 8.6 / 8.9, 4096 x 28672 unchanged (13.5 / 15.0 / 15.2); one row stays on one strip
-// (4096 x 11008 6.19 against 7.24, 4096 x 14336 7.48 / 7.51).
+// blocks: M = 2 / 3 / 4 on 8192 x 14336 15.9 / 17.4 / 18.0 -> 12.8 / 14.0 / 14.5 us, 4096 x
+// 14336 8.3 / 8.8 / 9.2 -> 7.6 / 8.3 / 8.5, 5120 x 13824 10.9 / 11.8 / 12.2 -> 10.7 / 11.3 /
+// 11.7, 4096 x 28672 13.5 / 14.7 / 15.1 -> 13.2 / 14.2 / 14.6; elsewhere pairs at 1..4 rows
+// ran slower or equal (4096 x 11008 M = 1 / 4: 6.21 / 7.63 against 7.11 / 8.53, 4096 x 4096
+// M = 4 4.70 against 5.48, 4096 x 6144 within 2%).
 static void strips_pick_pair(int M, int nstrips, int kb, int* ns, int* u) {
   *ns = 1;
   if (M > 4) *u = 2;
