@@ -372,8 +372,8 @@ static void strips_pick_pair(int M, int nstrips, int kb, int* ns, int* u) {
   if (M > 4) {
     if (nstrips >= 320 && nstrips <= 512) *ns = 2;
     else if (nstrips > 768) *ns = 2, *u = 1;
-  } else if (M >= 2 && nstrips > 768 && kb <= 64) {
-    *ns = 2;  // blocks per wave as for one strip
+  } else if (M >= 2 && nstrips > 768 && kb <= 64 && *u <= 4) {
+    *ns = 2;  // blocks per wave as for one strip (the two-strip kernels take U <= 4)
   }
 }
 
@@ -434,6 +434,9 @@ static int strips_run(const StripPlan& pl, const void* a, void* c, int64_t ldc, 
   p.ldc = ldc;
   const int M = p.M, u = pl.u;
   const bool gs = p.ss != nullptr;
+  // the two-strip kernels exist for U <= 4 at 2..4 rows and U <= 2 at 5..8 (strips_pick_pair)
+  PK_REQUIRE(pl.ns == 1 || (M >= 2 && u <= (M > 4 ? 2 : 4)),
+             "w4a16 gemv (strip layout): no two-strip kernel for M=%d U=%d", M, u);
   auto go = [&](auto MTc, auto Uc, auto AL, auto NSc) {
     constexpr int mt = decltype(MTc)::value, uu = decltype(Uc)::value, ns = decltype(NSc)::value;
     constexpr bool al = decltype(AL)::value != 0;

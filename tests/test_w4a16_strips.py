@@ -82,6 +82,12 @@ def test_strips_plan_rule():
                 assert u == 2 and nw <= 8
     assert _pk.w4a16_strips_plan(8, 6144, 4096) == (2, 2, 8)
     assert _pk.w4a16_strips_plan(2, 14336, 4096) == (2, 4, 8)
+    try:  # a fixed U of 8 (the measurement hook) keeps one strip per workgroup
+        _pk.w4a16_strips_config(8)
+        assert _pk.w4a16_strips_plan(2, 14336, 4096)[:2] == (1, 8)
+        assert _pk.w4a16_strips_plan(8, 14336, 4096)[:2] == (2, 1)
+    finally:
+        _pk.w4a16_strips_config(0)
     with pytest.raises(_pk.PicoKernelsError):
         _pk.w4a16_strips_plan(9, 6144, 4096)
 
