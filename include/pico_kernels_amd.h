@@ -180,7 +180,8 @@ int pk_w4a16_gemm_tiled(const void* a, int64_t lda, const uint32_t* qtiled, cons
 /* W4A16 decode matmul (1 <= M <= 8) on weights in the strip layout: C = tensor_scale * A @
  * dequant(q, S) (+ bias), the arithmetic of pk_w4a16_gemm_bias (gemm_int4.py:21-55, 75-92 with
  * group scales), in ONE launch with no split-K partials: one workgroup per 16-column strip
- * adds the whole of K in LDS, in a fixed order (bitwise reproducible). The strip layout is a
+ * (or per two: pk_w4a16_strips_plan) adds the whole of K in LDS, in a fixed order (bitwise
+ * reproducible). The strip layout is a
  * byte permutation of pack_int4_n's (K, N/2) bytes (gemm_int4.py:65-72): byte (k, c), with
  * k = 128b + 32rs + 8g + e and c = 8s + 2cps + h (b block, rs, g, cps in 0..3, e in 0..7,
  * h in 0..1), sits at byte ((((s * K/128 + b) * 4 + g) * 4 + rs) * 4 + cps) * 16 + 8h + e, both

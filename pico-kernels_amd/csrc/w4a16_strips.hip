@@ -1,6 +1,6 @@
 // W4A16 decode GEMV (1 <= M <= 8) on strip-layout weights: one workgroup per 16-column strip
-// sums the whole of K itself, so a call is one launch with no split-K partials and no
-// handoff between workgroups.
+// (or per two neighbouring strips, where the layer has strips enough) sums the whole of K
+// itself, so a call is one launch with no split-K partials and no handoff between workgroups.
 //
 // Computes C[m, n] = tensor_scale * sum_k A[m, k] * q[k, n] * S[k / G, n] (+ bias[n]), the
 // arithmetic of gemm_int4.int4_gemm_kernel (gemm_int4.py:21-55) with group scales.
@@ -43,7 +43,7 @@
 
 namespace pk {
 
-constexpr int kStripCols = 16;       // columns per strip = per workgroup
+constexpr int kStripCols = 16;       // columns per strip
 constexpr int kStripBlockRows = 128;  // rows per 1 KB block
 constexpr int kStripMaxWaves = 16;
 constexpr int kStripWaves8 = 8;  // waves per workgroup of the 5..8-row kernel
