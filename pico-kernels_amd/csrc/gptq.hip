@@ -137,6 +137,161 @@ __global__ __launch_bounds__(kGptqThreads) void gptq_block_kernel(GptqParams p) 
   }
 }
 
+// The same sweep for scale domains of at most 128 rows (group-wise GPTQ), with the block's
+// values in registers: wave w of 16 holds columns 8w .. 8w + 7 of every row, lane l rows l and
+// l + 64. A column's max is then one wave's (DPP, no barrier). Wave w first takes, column by
+// column in order, the errors of every column before its own: it waits for the column's flag,
+// reads the errors of its rows from LDS and applies them to its eight columns. Then it sweeps
+// its own columns in registers: quantize, write the errors to LDS and raise the flag, apply
+// them to its remaining columns. So every value still takes its updates in column order, the
+// product rounded before the subtraction: bitwise the sweep above. The serial path is one
+// flag hand-off between waves per eight columns instead of two workgroup barriers per column.
+constexpr int kGptqFastRows = 128;
+constexpr int kGptqFastCols = 128;
+constexpr int kGptqFastWaves = 16;
+
+__global__ __launch_bounds__(64 * kGptqFastWaves) void gptq_block_fast_kernel(GptqParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) float lds[];
+  float* rt = lds;                          // [nb][nb]: rt[c][c'] = ratio[b0 + c][b0 + c']
+  float* eb = lds + p.nb * p.nb;            // [nb][128]: column c's errors by row
+  __shared__ int ready[kGptqFastCols];      // ready[c] != 0: eb[c] is written
+  constexpr int CPW = kGptqFastCols / kGptqFastWaves;  // columns per wave
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int r0 = blockIdx.x * p.domain;
+  const int rows = min(p.domain, p.out - r0);
+  const int nb = p.nb;
+  const int c0 = CPW * wave;  // this wave's first column
+
+  {  // the ratios: every load in flight before the first LDS write
+    constexpr int PER = kGptqFastCols * kGptqFastCols / (64 * kGptqFastWaves);
+    float r[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = t + u * 64 * kGptqFastWaves, c = i / nb, c2 = i - c * nb;
+      r[u] = i < nb * nb ? p.ratio[(int64_t)(p.b0 + c) * p.ldr + p.b0 + c2] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = t + u * 64 * kGptqFastWaves;
+      if (i < nb * nb) rt[i] = r[u];
+    }
+  }
+  if (t < kGptqFastCols) ready[t] = 0;
+  bool live[2];
+  float v[CPW][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) live[h] = lane + 64 * h < rows;
+  {  // every load in flight at once: rows past the domain and columns past the block read a
+     // valid element (row r0, column b0) and are never used
+    const int64_t base = (int64_t)r0 * p.ldq + p.b0;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = c0 + j;
+        const int64_t off = (live[h] ? (int64_t)(lane + 64 * h) * p.ldq : 0) + (c < nb ? c : 0);
+        v[j][h] = p.q[base + off];
+      }
+  }
+  __syncthreads();
+  if (c0 >= nb) return;  // wave-uniform: no columns here
+
+  // ---- the errors of every column before this wave's, in column order ----
+  for (int c = 0; c < c0; ++c) {
+    const float* rc = rt + c * nb;
+    float r[CPW];  // read before the wait: the ratios do not change
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) r[j] = rc[min(c0 + j, nb - 1)];
+    // the owner runs in the same workgroup, so it is resident and the wait ends; the bound
+    // only guards against a fault in that reasoning
+    for (int i = 0; i < (1 << 26); ++i) {
+      if (__hip_atomic_load(&ready[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");  // the error reads stay after the flag's
+    float e[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) e[h] = eb[c * kGptqFastRows + lane + 64 * h];  // rows past: unused
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      if (c0 + j < nb) {  // wave-uniform
+#pragma unroll
+        for (int h = 0; h < 2; ++h) v[j][h] = v[j][h] - e[h] * r[j];
+      }
+    }
+  }
+  // this wave's own block of ratios, in registers for the serial part
+  float ro[CPW][CPW];
+#pragma unroll
+  for (int j = 0; j < CPW; ++j)
+#pragma unroll
+    for (int j2 = 0; j2 < CPW; ++j2)
+      ro[j][j2] = j2 > j ? rt[min(c0 + j, nb - 1) * nb + min(c0 + j2, nb - 1)] : 0.0f;
+
+  // ---- this wave's own columns (their codes and errors kept in registers, stored at the end) ----
+  const float fq = (float)p.qmax;
+  float ev[CPW][2];
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const int c = c0 + j;
+    ev[j][0] = ev[j][1] = 0.0f;
+    if (c >= nb) continue;  // wave-uniform
+    unsigned amax = 0u;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (live[h]) amax = max(amax, abs_bits(v[j][h]));
+    const float a = __builtin_bit_cast(float, wave_max_u32(amax));
+    const float s = (a < 1e-12f ? 1e-12f : a) / fq;  // clamp_min: NaN passes through
+    float e[2], qv[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float r = clamp_nan(__builtin_rintf(v[j][h] / s), -fq, fq);
+      qv[h] = r * s;
+      e[h] = v[j][h] - qv[h];
+      if (live[h]) eb[c * kGptqFastRows + lane + 64 * h] = e[h];
+    }
+    // The errors land in LDS before the flag: lgkmcnt(0) orders this wave's LDS writes (a
+    // release fence would also wait for global stores; there are none until the end).
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    if (lane == 0) __hip_atomic_store(&ready[c], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) ev[j][h] = e[h];
+#pragma unroll
+    for (int j2 = j + 1; j2 < CPW; ++j2) {
+      if (c0 + j2 < nb) {  // wave-uniform
+#pragma unroll
+        for (int h = 0; h < 2; ++h) v[j2][h] = v[j2][h] - e[h] * ro[j][j2];
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) v[j][h] = qv[h];  // the column's codes times its scale
+  }
+  // codes and errors of this wave's columns, row by row: 16-byte stores where aligned
+  const int ncols = min(CPW, nb - c0);
+  const bool vec = ncols == CPW && p.ldq % 4 == 0 && p.lde % 4 == 0 &&
+                   (reinterpret_cast<uintptr_t>(p.q + p.b0 + c0) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(p.err + c0) & 15) == 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (!live[h]) continue;
+    float* qrow = p.q + (int64_t)(r0 + lane + 64 * h) * p.ldq + p.b0 + c0;
+    float* erow = p.err + (int64_t)(r0 + lane + 64 * h) * p.lde + c0;
+    if (vec) {
+#pragma unroll
+      for (int j = 0; j < CPW; j += 4) {
+        *reinterpret_cast<pk_f4*>(qrow + j) = pk_f4{v[j][h], v[j + 1][h], v[j + 2][h], v[j + 3][h]};
+        *reinterpret_cast<pk_f4*>(erow + j) = pk_f4{ev[j][h], ev[j + 1][h], ev[j + 2][h], ev[j + 3][h]};
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPW; ++j)
+        if (j < ncols) qrow[j] = v[j][h], erow[j] = ev[j][h];
+    }
+  }
+}
+
 // Columns per block for a scale domain of `rows` rows: the largest power of two up to 128
 // whose ratios and values fit the LDS budget; 0 if not even one column fits.
 inline int gptq_block_cols(int rows) {
@@ -182,10 +337,18 @@ extern "C" int pk_gptq_block(float* q, int64_t ldq, const float* ratio, int64_t 
   p.nb = nb;
   p.domain = domain;
   p.qmax = (1 << (bits - 1)) - 1;
+  const int grid = (out + domain - 1) / domain;
+  if (domain <= kGptqFastRows && nb <= kGptqFastCols) {
+    const size_t lds = ((size_t)nb * nb + (size_t)nb * kGptqFastRows) * sizeof(float);
+    static std::atomic<uint64_t> lds_fast{0};
+    if (const int rc = set_lds_limit_once((const void*)gptq_block_fast_kernel, (int)(kGptqLdsFloats * sizeof(float)), &lds_fast)) return rc;
+    gptq_block_fast_kernel<<<grid, 64 * kGptqFastWaves, lds, (hipStream_t)stream>>>(p);
+    PK_LAUNCH_CHECK("gptq block");
+    return PK_OK;
+  }
   const size_t lds = ((size_t)nb * nb + (size_t)nb * domain) * sizeof(float);
   static std::atomic<uint64_t> lds_done{0};
   if (const int rc = set_lds_limit_once((const void*)gptq_block_kernel, (int)(kGptqLdsFloats * sizeof(float)), &lds_done)) return rc;
-  const int grid = (out + domain - 1) / domain;
   gptq_block_kernel<<<grid, kGptqThreads, lds, (hipStream_t)stream>>>(p);
   PK_LAUNCH_CHECK("gptq block");
   return PK_OK;
