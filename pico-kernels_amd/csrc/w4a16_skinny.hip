@@ -136,19 +136,23 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
     const int srow = (kb / p.group) * p.N * 2;
 #pragma unroll
     for (int i = 0; i < WPL; ++i)
-      sraw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16 + 16 * i, srow, 0);
+      sraw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16 + 16 * i, srow, kPkLoadStream);
   }
 
+  // Weights and scales load non-temporally (read once per call; measured on MI355X on the
+  // Llama-3-8B layers at M = 32 against ordinary loads: qkv 12.15 -> 11.54 us, o_proj 10.37 ->
+  // 9.72, down 18.76 -> 17.83; o_proj at M = 128 16.76 -> 15.96). Activations stay cached:
+  // every workgroup reads them.
   auto load = [&](SkStep<MB, WPL>& b, int s) {
     const int k0 = kb + s * kSkStep;
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       if constexpr (WPL == 2) {
-        const pk_u2v v = __builtin_amdgcn_raw_buffer_load_b64(rq, q_voff, qrow_off(p.ql, k0 + d), 0);
+        const pk_u2v v = __builtin_amdgcn_raw_buffer_load_b64(rq, q_voff, qrow_off(p.ql, k0 + d), kPkLoadStream);
         b.w[d][0] = v[0];
         b.w[d][1] = v[1];
       } else {
-        b.w[d][0] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_voff, qrow_off(p.ql, k0 + d), 0);
+        b.w[d][0] = __builtin_amdgcn_raw_buffer_load_b32(rq, q_voff, qrow_off(p.ql, k0 + d), kPkLoadStream);
       }
     }
 #pragma unroll
@@ -256,7 +260,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void w4a16_skinny_kernel(SkinnyParams
         const int srow = (kb / p.group + gi + 1) * p.N * 2;
 #pragma unroll
         for (int i = 0; i < WPL; ++i)
-          sraw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16 + 16 * i, srow, 0);
+          sraw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, word0 * 16 + 16 * i, srow, kPkLoadStream);
       }
     }
   } else {

@@ -182,11 +182,15 @@ __global__ __launch_bounds__(64 * (NS == 1 ? kStripMaxWaves : kStripWaves8)) voi
         for (int ms = 0; ms < MS; ++ms)
           x[i][ms] = __builtin_amdgcn_raw_buffer_load_b128(ra, xoff[ms], b * (kStripBlockRows * 2), 0);
       }
-      if constexpr (HAS_GS) {  // the row set's group (per lane where G < 128)
+      // The row set's group (per lane where G < 128). Non-temporal like the weights: measured
+      // on MI355X at 4096 x 11008, M = 1, 6.15 -> 5.94 us against ordinary loads (sc0, sc1 or
+      // both beside nt read the same).
+      if constexpr (HAS_GS) {
 #pragma unroll
         for (int st = 0; st < NS; ++st)
           sc[st][i] = __builtin_amdgcn_raw_buffer_load_b64(
-              rsc[st], cps * 8 + strip_group(p, b * kStripBlockRows + 32 * rs) * (kStripCols * 2), 0, 0);
+              rsc[st], cps * 8 + strip_group(p, b * kStripBlockRows + 32 * rs) * (kStripCols * 2), 0,
+              kPkLoadStream);
       }
     }
     if constexpr (ALDS) {
