@@ -296,21 +296,34 @@ __global__ __launch_bounds__(64 * (NS == 1 ? kStripMaxWaves : kStripWaves8)) voi
     const int st = sm / rows, m = sm - st * rows;
     const int part = lane >> 4, col = lane & 15;
     const int kmax = (p.nw + 3) >> 2;  // wave-uniform
+    // Every read first (addresses clamped to the last wave's region), one wait, then the adds
+    // in the fixed order: the fold is one LDS round trip however many waves there are.
+    float q4[kStripMaxWaves / 4][4];
+#pragma unroll
+    for (int k = 0; k < kStripMaxWaves / 4; ++k) {
+      const int wv = min(part + 4 * k, p.nw - 1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) q4[k][q] = (*red(wv, st, q, m, col >> 2))[col & 3];
+    }
     float v = 0.0f;
 #pragma unroll
     for (int k = 0; k < kStripMaxWaves / 4; ++k) {
       if (k < kmax) {
-        const int wv = min(part + 4 * k, p.nw - 1);
         const bool live = part + 4 * k < p.nw;
-        float q4[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) q4[q] = (*red(wv, st, q, m, col >> 2))[col & 3];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v += live ? q4[q] : 0.0f;
+        for (int q = 0; q < 4; ++q) v += live ? q4[k][q] : 0.0f;
       }
     }
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+    // The four parts (16-lane rows) added by row swaps instead of LDS shuffles: after
+    // permlane16_swap(v, v) both rows of a pair hold (row 2i, row 2i+1), so their sum is the
+    // pair's; permlane32_swap does the same for the halves. The same tree as before:
+    // ((part 0 + part 1) + (part 2 + part 3)).
+    {
+      const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      v = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+      const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      v = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+    }
     if (part == 0) {
       v *= (col & 1) ? 1048576.0f : 16777216.0f;  // exact: powers of two
       const int n = (s0 + st) * kStripCols + col;
