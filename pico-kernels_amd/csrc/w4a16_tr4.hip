@@ -2,8 +2,9 @@
 // (gemm_int4.py:21-55 is the operation: C = A @ dequant(B), B int4 codes packed 8 per int32
 // along N as pack_int4_n writes them (gemm_int4.py:65-72), optional fp16 group scales along K).
 //
-// Shape: 128 x 256 workgroup tiles, BK = 128, eight waves. Wave w owns output columns
-// 64 (w % 4) .. +63 of all 128 rows and k half h = w / 4 of every k-tile: waves w and w + 4 run
+// Shape: 128 x 256 workgroup tiles (64 x 256 up to 128 rows of activations), BK = 128, eight
+// waves. Wave w owns output columns 64 (w % 4) .. +63 of all the tile's rows and k half
+// h = w / 4 of every k-tile: waves w and w + 4 run
 // on the same SIMD, compute the same 128 x 64 block over different k and add their
 // accumulators once, at the end. So each SIMD has two independent instruction streams (one
 // covers the other's LDS and dependency waits) while its per-tile work -- MFMAs, LDS reads,
@@ -101,12 +102,13 @@ __device__ __forceinline__ void tr4_tile_of(int bid, int tiles_m, int tiles_n, i
 // s_waitcnt immediate for vmcnt(v) alone.
 constexpr int tr4_wait_vm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >> 4) << 14); }
 
-template <bool GS>
+template <bool GS, int BM>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void w4a16_tr4_kernel(Tr4Params p) {
-  constexpr int BM = 128, BN = 256, WN = 64;
-  constexpr int FM = 4, FN = 2;  // 32 x 32 fragments per wave
-  constexpr int A_DMA = 4;       // 32 KB of A per tile: 4 x 1 KB per wave
+  static_assert(BM == 128 || BM == 64, "tiles of 128 or 64 rows");
+  constexpr int BN = 256, WN = 64;
+  constexpr int FM = BM / 32, FN = 2;  // 32 x 32 fragments per wave
+  constexpr int A_DMA = BM / 32;       // BM x 256 bytes of A per tile: A_DMA x 1 KB per wave
   constexpr int B_DMA = 2;       // 16 KB of packed B per tile: 2 x 1 KB per wave
   constexpr int ASZ = BM * 256, BSZ = 128 * 128, SSZ = GS ? 1024 : 16;
 
@@ -139,7 +141,7 @@ void w4a16_tr4_kernel(Tr4Params p) {
   int a_off[A_DMA], b_off[B_DMA];
 #pragma unroll
   for (int i = 0; i < A_DMA; ++i) {
-    const int r = 4 * (4 * wave + i) + (lane >> 4);
+    const int r = 4 * (A_DMA * wave + i) + (lane >> 4);
     a_off[i] = (int)((int64_t)min(m0 + r, p.M - 1) * p.lda * 2) + tr4_aslot(r, lane & 15) * 16;
   }
 #pragma unroll
@@ -157,7 +159,7 @@ void w4a16_tr4_kernel(Tr4Params p) {
   auto issue = [&](int kt, char* sA, char* sB, char* sS) {
     const int k0 = (kt0 + kt) * 128;
 #pragma unroll
-    for (int i = 0; i < A_DMA; ++i) tr4_dma16(ra, sA + (4 * wave + i) * 1024, a_off[i], k0 * 2);
+    for (int i = 0; i < A_DMA; ++i) tr4_dma16(ra, sA + (A_DMA * wave + i) * 1024, a_off[i], k0 * 2);
 #pragma unroll
     for (int i = 0; i < B_DMA; ++i) tr4_dma16(rb, sB + (2 * wave + i) * 1024, b_off[i], qrow_off(p.ql, k0));
     if constexpr (GS)
@@ -336,15 +338,17 @@ void w4a16_tr4_kernel(Tr4Params p) {
 
   // ---- epilogue ----
   __syncthreads();  // every wave's last LDS reads are done: the stages are free
-  // The k-half-1 waves park their accumulators in LDS, the k-half-0 waves add them: two rounds
-  // of four fragments (16 KB per wave, lane-major per register so each lane reads back its own
-  // values), column wave c in its own 16 KB of stage A memory, which it then reuses to stage
-  // its output slices.
+  // The k-half-1 waves park their accumulators in LDS, the k-half-0 waves add them: rounds of
+  // four fragments (16 KB per wave, lane-major per register so each lane reads back its own
+  // values; two rounds with 128-row tiles, one with 64), column wave c in its own 16 KB of stage
+  // memory, which it then reuses to stage its output slices.
   const int cw = wave & 3;
-  char* const region = (cw < 2 ? sA0 : sA1) + (cw & 1) * 16384;
+  char* region;
+  if constexpr (BM == 128) region = (cw < 2 ? sA0 : sA1) + (cw & 1) * 16384;
+  else region = cw == 0 ? sA0 : cw == 1 ? sA1 : cw == 2 ? sA2 : sB0;
   float* const park = reinterpret_cast<float*>(region);
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int half = 0; half < FM / 2; ++half) {
     if (h == 1) {
 #pragma unroll
       for (int f = 0; f < 4; ++f)
@@ -421,26 +425,39 @@ bool tr4_shape_ok(int M, int N, int K, int group, bool has_gs) {
 
 bool tr4_split_ok(int K, int split) { return split >= 1 && K % (128 * split) == 0; }
 
+// Tile height: 64 rows up to 128 rows of activations -- twice the tiles of 128-row ones, so
+// half the split-K slices and partial planes for the same parallelism. Measured on MI355X at
+// M = 128 (graphs over rotating block-layout copies, GEMM + reduce): 4096 x 6144 22.3 -> 18.2 us
+// (8 -> 4 slices), 4096 x 14336 33.5 -> 27.7 (4 -> 2), 14336 x 4096 32.1 -> 29.2 (8 -> 7).
+int tr4_pick_bm(int M, int N, int K) {
+  (void)N;
+  (void)K;
+  return M <= 128 ? 64 : 128;
+}
+
 // Split-K for the shape: the most equal k-slices (a divisor of K / 128, at most 16) that keep
 // tiles x slices <= 224 workgroups, one slice wherever that is 1. Measured on MI355X (M = 65 to
 // 1024 at K = 4096 and 14336, N = 4096 to 14336): each slice costs its fp32 partial plane
 // written and read back plus the reduce launch (about 7 us of fixed cost and 0.34 us per MB of
 // planes), while k-tile time rises from 1.4 us with up to 128 busy CUs to 1.9 us with all 256,
 // so the best split stops short of filling every CU.
-// The most slices (dividing the k-tiles, at most 16, tiles x slices <= 224 workgroups), but a
-// power of two when one reaches at least half of that: fewer fp32 partial planes for the
-// reduce to read, and its unrolled form. Measured on MI355X at M = 128, 14336 x 4096 (graphs
-// over 22 rotating block-layout copies, GEMM + reduce): 14 slices 36.1 us, 8 slices 32.0,
-// 7 slices 35.5, 16 slices 37.1; 4096 x 6144: 8 slices 21.5, 4 22.5.
+// With 128-row tiles the most slices (dividing the k-tiles, at most 16, tiles x slices <= 224
+// workgroups), but a power of two when one reaches at least half of that: fewer fp32 partial
+// planes for the reduce to read, and its unrolled form. Measured on MI355X with 128-row tiles
+// at M = 128, 14336 x 4096 (graphs over 22 rotating block-layout copies, GEMM + reduce): 14
+// slices 36.1 us, 8 slices 32.0, 7 slices 35.5, 16 slices 37.1; 4096 x 6144: 8 slices 21.5, 4
+// 22.5.
 int tr4_pick_split(int M, int N, int K) {
   const int kt = K / 128;
-  const int64_t tiles = cdiv(M, 128) * (int64_t)(N / 256);
+  const int64_t tiles = cdiv(M, tr4_pick_bm(M, N, K)) * (int64_t)(N / 256);
   int best = 1, best_pow2 = 1;
   for (int s = 2; s <= 16 && s <= kt; ++s)
     if (kt % s == 0 && tiles * s <= 224) {
       best = s;
       if ((s & (s - 1)) == 0) best_pow2 = s;
     }
+  // 64-row tiles take the most slices (14336 x 4096 at M = 128: 7 slices 29.2 us, 4 32.8)
+  if (tr4_pick_bm(M, N, K) == 64) return best;
   return 2 * best_pow2 >= best ? best_pow2 : best;
 }
 
@@ -475,7 +492,8 @@ int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const voi
   p.M = M;
   p.N = N;
   p.K = K;
-  p.tiles_m = (int)cdiv(M, 128);
+  const int bm = tr4_pick_bm(M, N, K);
+  p.tiles_m = (int)cdiv(M, bm);
   p.tiles_n = N / 256;
   p.kt_slice = K / 128 / split;
   p.ql = qlayout(tiled, ldb, N);
@@ -494,8 +512,13 @@ int tr4_launch(const void* a, int64_t lda, const void* b, int64_t ldb, const voi
     p.c_slice = 0;
   }
   const dim3 grid(p.tiles_m * p.tiles_n, split);
-  if (scales) w4a16_tr4_kernel<true><<<grid, 512, 0, s>>>(p);
-  else w4a16_tr4_kernel<false><<<grid, 512, 0, s>>>(p);
+  if (bm == 64) {
+    if (scales) w4a16_tr4_kernel<true, 64><<<grid, 512, 0, s>>>(p);
+    else w4a16_tr4_kernel<false, 64><<<grid, 512, 0, s>>>(p);
+  } else {
+    if (scales) w4a16_tr4_kernel<true, 128><<<grid, 512, 0, s>>>(p);
+    else w4a16_tr4_kernel<false, 128><<<grid, 512, 0, s>>>(p);
+  }
   PK_LAUNCH_CHECK("w4a16 gemm (int4 B in LDS)");
   if (split <= 1 || partials_only) return PK_OK;
   return splitk_reduce(partials, split, M, N, epi, c, c_dtype, ldc, s);

@@ -38,6 +38,9 @@ def _case(M, K, N, G, seed, cuda):
     (512, 768, 512, 128),    # six (one pass of the unrolled loop)
     (257, 896, 256, 64),     # seven (loop + one), one row past a tile
     (2048, 4096, 4096, 128), # the prefill shape
+    (65, 896, 256, 64),      # 64-row tiles (up to 128 rows): seven k-tiles, one row past a tile
+    (128, 640, 512, 128),    # 64-row tiles: five k-tiles, two full tiles
+    (100, 768, 768, 256),    # 64-row tiles: six k-tiles, group 256, ragged rows
 ])
 def test_tr4_matches_oracle(M, K, N, G, cuda):
     a, codes, s16, qw, sc = _case(M, K, N, G, M + K + N, cuda)
@@ -64,43 +67,48 @@ def test_tr4_per_tensor_mode(cuda):
     assert oracle.rel_fro(out.cpu().numpy(), ref) < 1e-5  # codes are exact in fp16
 
 
+@pytest.mark.parametrize("M", [384, 96])  # 128-row tiles, 64-row tiles
 @pytest.mark.parametrize("out_dtype,tol", [(torch.float16, 2e-3), (torch.bfloat16, 1e-2),
                                            (torch.float32, 1e-3)])
-def test_tr4_output_dtypes(out_dtype, tol, cuda):
-    M, K, N, G = 384, 512, 512, 128
+def test_tr4_output_dtypes(M, out_dtype, tol, cuda):
+    K, N, G = 512, 512, 128
     a, codes, s16, qw, sc = _case(M, K, N, G, 5, cuda)
-    out = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, out_dtype)
+    assert _pk.w4a16_plan(M, N, K, G, 1) == (_pk.KERNEL_GEMM_TR4, 1)
+    out = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, out_dtype, split_k=1)
     assert out.dtype == out_dtype
     ref = oracle.w4a16_ref(a.numpy(), codes, s16, G)
     assert oracle.rel_fro(out.float().cpu().numpy(), ref) < tol
 
 
-def test_tr4_strided_operands(cuda):
+@pytest.mark.parametrize("M,split", [(320, 0), (72, 1)])  # automatic (split-K), 64-row tiles
+def test_tr4_strided_operands(M, split, cuda):
     """A with lda > K and an output view into a wider buffer (ldc > N): the same bits as
     contiguous operands."""
-    M, K, N, G = 320, 512, 512, 128
+    K, N, G = 512, 512, 128
     a, codes, s16, qw, sc = _case(M, K, N, G, 9, cuda)
     a_wide = torch.zeros(M, K + 64, dtype=torch.float16)
     a_wide[:, :K] = a
     a_view = a_wide.to(cuda)[:, :K]
     big = torch.full((M, N + 256), 7.0, dtype=torch.float16, device=cuda)
     out_view = big[:, 128:128 + N]
-    _pk.w4a16_gemm(a_view, qw, sc, G, 1.0, torch.float16, out=out_view)
-    ref = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float16)
+    _pk.w4a16_gemm(a_view, qw, sc, G, 1.0, torch.float16, split_k=split, out=out_view)
+    ref = _pk.w4a16_gemm(a.to(cuda), qw, sc, G, 1.0, torch.float16, split_k=split)
     assert torch.equal(out_view, ref)
     assert torch.all(big[:, :128] == 7.0) and torch.all(big[:, 128 + N:] == 7.0)
 
 
-# (M, K, N, G, automatic split): the sweep's qkv layer at 128 rows, ragged rows with a one-tile
-# slice, group 64 and 256, the largest slice count (16), a power of two chosen over the most
-# slices (8 of 112 k-tiles, not 14) and a slice count that is not a power of two (15 of 15
-# k-tiles, reduced by the generic-count kernel)
+# (M, K, N, G, automatic split): the sweep's qkv layer at 128 rows (64-row tiles, 4 slices),
+# ragged rows with a one-tile slice, group 64 and 256, the largest slice count (16), with
+# 128-row tiles a power of two chosen over the most slices (8 of 112 k-tiles, not 14), with
+# 64-row tiles the most slices (7 of 112), and a slice count that is not a power of two (15 of
+# 15 k-tiles, reduced by the generic-count kernel)
 SPLIT_CASES = [
-    (128, 4096, 6144, 128, 8),
+    (128, 4096, 6144, 128, 4),
     (65, 1024, 512, 64, 8),
     (100, 2048, 256, 256, 16),
     (129, 2048, 1024, 128, 16),
-    (128, 14336, 4096, 128, 8),
+    (129, 14336, 2048, 128, 8),
+    (128, 14336, 4096, 128, 7),
     (128, 1920, 256, 128, 15),
 ]
 

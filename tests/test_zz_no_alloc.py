@@ -58,14 +58,15 @@ def test_noalloc_matches_workspace_entry_point(shapes, cuda):
 
 
 def test_noalloc_smaller_automatic_split(cuda):
-    """An automatic packed-B split whose partials exceed the scratch (8 slices of 128 x 6144
-    fp32, 25 MB) runs the largest smaller split that fits (4): the same bits as the workspace
+    """An automatic packed-B split whose partials exceed the scratch (4 slices of 256 x 6144
+    fp32, 25 MB) runs the largest smaller split that fits (2): the same bits as the workspace
     entry point at that split."""
-    M, K, N = 128, 4096, 6144
-    assert _pk.w4a16_plan(M, N, K, 128, 0) == (_pk.KERNEL_GEMM_TR4, 8)
-    assert _pk.lib().pk_w4a16_workspace_bytes(M, N, K, 128, 4) <= 16 << 20
+    M, K, N = 256, 4096, 6144
+    assert _pk.w4a16_plan(M, N, K, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
+    assert _pk.lib().pk_w4a16_workspace_bytes(M, N, K, 128, 4) > 16 << 20
+    assert _pk.lib().pk_w4a16_workspace_bytes(M, N, K, 128, 2) <= 16 << 20
     a, qw, sc = _inputs(M, K, N, 11, cuda)
-    want = _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, split_k=4)
+    want = _pk.w4a16_gemm(a, qw, sc, 128, 1.0, torch.float16, split_k=2)
     got = torch.full((M, N), float("nan"), dtype=torch.float16, device=cuda)
     assert _noalloc(a, qw, sc, 0, got) == _pk.PK_OK, _pk.lib().pk_last_error()
     torch.cuda.synchronize()
