@@ -48,16 +48,17 @@ def test_w4a16_plans():
         assert _pk.w4a16_plan(1, 11008, 4096, 128, s) == (_pk.KERNEL_GEMV, s)
     # prefill: the MFMA GEMM that keeps B packed in LDS, no split needed at 2048 rows
     assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (_pk.KERNEL_GEMM_TR4, 1)
-    # up to 128 rows 64-row tiles with the most slices: 2 x 24 tiles x 4 for qkv, 2 x 16 x 7 at
-    # K = 14336, 2 x 16 x 6 at K = 12288
+    # 64-row tiles (chosen by the tile-height cost model) take the most slices: 2 x 24 tiles x 4
+    # for qkv at 128 rows, 2 x 16 x 7 at K = 14336, 2 x 16 x 6 at K = 12288, 3 x 16 x 4 at 129
+    # rows, 3 x 8 x 8 at N = 2048
     assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
     assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 7)
     assert _pk.w4a16_plan(128, 4096, 12288, 128, 0) == (_pk.KERNEL_GEMM_TR4, 6)
-    # 128-row tiles above that: a power of two when it reaches half the most slices (8, not
-    # 14, at K = 14336 with 16 tiles)
-    assert _pk.w4a16_plan(256, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
     assert _pk.w4a16_plan(129, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
     assert _pk.w4a16_plan(129, 2048, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 8)
+    # 128-row tiles take a power of two when it reaches half the most slices: 4, not 7, for
+    # 2 x 16 tiles at K = 14336
+    assert _pk.w4a16_plan(256, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
     # per-tensor mode (group_size 0) for the drop-in int4_gemm
     assert _pk.w4a16_plan(256, 512, 256, 0, 0)[0] == _pk.KERNEL_GEMM_TR4
     assert _pk.w4a16_plan(256, 520, 256, 0, 0)[0] == _pk.KERNEL_GEMM   # N % 256 != 0
@@ -112,12 +113,13 @@ def test_w4a16_plans_by_row_count():
     assert _pk.w4a16_plan(128, 768, 1024, 128, 0) == (T, 8)       # below 1024^2 weights
     # otherwise above 64 rows: the GEMM that keeps B packed in LDS where its shape rules hold
     # (N % 256, K % 128, group % 64) with the most equal k-slices (at most 16) that keep
-    # tiles x slices <= 224, unsplit where the tiles alone reach that: 64 x 256 tiles up to
-    # 128 rows, 128 x 256 tiles above (a power of two when one reaches half the most slices)
+    # tiles x slices <= 224, unsplit where the tiles alone reach that: 64 x 256 or 128 x 256
+    # tiles by the tile-height cost model (128-row ones take a power of two when one reaches
+    # half the most slices)
     assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (T, 4)      # 2 x 24 tiles x 4
     assert _pk.w4a16_plan(128, 14336, 4096, 128, 0) == (T, 2)     # 2 x 56 tiles x 2
     assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (T, 7)     # 2 x 16 tiles x 7 (112 k-tiles)
-    assert _pk.w4a16_plan(256, 6144, 4096, 128, 0) == (T, 4)      # 48 tiles x 4
+    assert _pk.w4a16_plan(256, 6144, 4096, 128, 0) == (T, 2)      # 4 x 24 tiles of 64 rows x 2
     assert _pk.w4a16_plan(1024, 4096, 4096, 128, 0) == (T, 1)     # 128 tiles (x 2 > 224)
     assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (T, 1)
     assert _pk.w4a16_plan(4096, 4096, 4096, 128, 0) == (T, 1)

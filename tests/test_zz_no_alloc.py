@@ -58,10 +58,10 @@ def test_noalloc_matches_workspace_entry_point(shapes, cuda):
 
 
 def test_noalloc_smaller_automatic_split(cuda):
-    """An automatic packed-B split whose partials exceed the scratch (4 slices of 256 x 6144
-    fp32, 25 MB) runs the largest smaller split that fits (2): the same bits as the workspace
-    entry point at that split."""
-    M, K, N = 256, 4096, 6144
+    """An automatic packed-B split whose partials exceed the scratch (4 slices of 256 x 4096
+    fp32 at K = 14336, 16.8 MB) runs the largest smaller split that fits (2): the same bits as
+    the workspace entry point at that split."""
+    M, K, N = 256, 14336, 4096
     assert _pk.w4a16_plan(M, N, K, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
     assert _pk.lib().pk_w4a16_workspace_bytes(M, N, K, 128, 4) > 16 << 20
     assert _pk.lib().pk_w4a16_workspace_bytes(M, N, K, 128, 2) <= 16 << 20
