@@ -110,8 +110,11 @@ def test_gptq_blocked_sweep_matches_sequential_oracle(cuda):
     ours = gptq_layer(torch.from_numpy(W).to(cuda), torch.from_numpy(X).to(cuda), 4).cpu().numpy()
     ref = oracle.gptq_layer(W, X, 4)
     close = np.isclose(ours, ref, atol=1e-4, rtol=1e-3)
-    assert close.mean() > 0.99
-    assert oracle.rel_fro(ours, ref) < 1e-3
+    # Measured on MI355X: no element outside the tolerance (max |diff| 1.1e-6, relative
+    # Frobenius 1.2e-6: fp32 reassociation only, no code flipped across a rounding tie).
+    assert (~close).sum() == 0, f"{(~close).sum()} of {close.size} differ"
+    assert np.abs(ours - ref).max() <= 1e-5
+    assert oracle.rel_fro(ours, ref) < 1e-5
 
 
 def test_bits16_passthrough(cuda):
