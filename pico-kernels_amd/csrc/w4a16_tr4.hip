@@ -425,41 +425,54 @@ bool tr4_shape_ok(int M, int N, int K, int group, bool has_gs) {
 
 bool tr4_split_ok(int K, int split) { return split >= 1 && K % (128 * split) == 0; }
 
+// Cost in microseconds of a tile height and split, fitted to MI355X measurements (Llama-3-8B
+// layers at M = 128 .. 1024, graphs of back-to-back calls): a workgroup's k-tile of 128 takes
+// about 1.23 us with 128-row tiles and 0.77 us with 64-row ones (half the MFMAs, but each int4
+// fragment dequantised for half the rows and twice the weight reads per FLOP), workgroups
+// beyond the 256 CUs run in further rounds, and split-K adds about 3 us plus 0.5 us per MB of
+// fp32 partial planes, 1 us more for a slice count the reduce has no unrolled form for.
+static double tr4_cost_us(int bm, int s, int M, int N, int K) {
+  const int64_t wgs = cdiv(M, bm) * (int64_t)(N / 256) * s;
+  const double rounds = (double)cdiv(wgs, 256);
+  const double kt = (double)(K / 128 / s);
+  double us = rounds * kt * (bm == 64 ? 0.77 : 1.23);
+  if (s > 1) us += 3.0 + 0.5 * ((double)s * M * N * 4 / 1e6) + ((s & (s - 1)) ? 1.0 : 0.0);
+  return us;
+}
+
 // Split for a tile height (see tr4_pick_split).
 static int tr4_split_for(int bm, int M, int N, int K) {
   const int kt = K / 128;
   const int64_t tiles = cdiv(M, bm) * (int64_t)(N / 256);
+  if (bm == 64) {
+    // 64-row tiles: the cheapest k-split filling at most the 256 CUs by the cost model
+    // (measured at M = 128: 14336 x 4096 8 slices 25.9 us, 7 27.1, 14 35.2; 4096 x 4096 4
+    // slices 16.5, 8 18.4; 4096 x 6144 4 slices 19.2, 8 23.6)
+    int best = 1;
+    for (int s = 2; s <= 16 && s <= kt; ++s)
+      if (kt % s == 0 && tiles * s <= 256 && tr4_cost_us(64, s, M, N, K) < tr4_cost_us(64, best, M, N, K))
+        best = s;
+    return best;
+  }
   int best = 1, best_pow2 = 1;
   for (int s = 2; s <= 16 && s <= kt; ++s)
     if (kt % s == 0 && tiles * s <= 224) {
       best = s;
       if ((s & (s - 1)) == 0) best_pow2 = s;
     }
-  // 64-row tiles take the most slices (14336 x 4096 at M = 128: 7 slices 29.2 us, 4 32.8)
-  if (bm == 64) return best;
   return 2 * best_pow2 >= best ? best_pow2 : best;
 }
 
-// Tile height, 64 or 128 rows, by a cost model fitted to MI355X measurements (Llama-3-8B layers
-// at M = 128 .. 512, graphs of back-to-back calls): a workgroup's k-tile of 128 takes about
-// 1.23 us with 128-row tiles and 0.77 us with 64-row ones (half the MFMAs, but each int4
-// fragment dequantised for half the rows and twice the weight reads per FLOP), workgroups
-// beyond the 256 CUs run in further rounds, and split-K adds about 3 us plus 0.5 us per MB of
-// fp32 partial planes. 64-row tiles win where they replace split-K slices by tiles: 4096 x
-// 6144 at M = 128 22.3 -> 18.2 us, 4096 x 14336 33.5 -> 27.7, 14336 x 4096 32.1 -> 29.2; at
-// M = 192 every layer 6-24%; 128-row ones where the 64-row tiles would add rounds or double a
-// workgroup's k-range at the same count (14336 x 4096 at M = 256: 45.8 against 50.6 us).
-static double tr4_cost_us(int bm, int M, int N, int K) {
-  const int s = tr4_split_for(bm, M, N, K);
-  const int64_t wgs = cdiv(M, bm) * (int64_t)(N / 256) * s;
-  const double rounds = (double)cdiv(wgs, 256);
-  const double kt = (double)(K / 128 / s);
-  const double planes_mb = s > 1 ? (double)s * M * N * 4 / 1e6 : 0.0;
-  return rounds * kt * (bm == 64 ? 0.77 : 1.23) + (s > 1 ? 3.0 + 0.5 * planes_mb : 0.0);
-}
-
+// Tile height, 64 or 128 rows, whichever the cost model prices lower at its split. 64-row
+// tiles win where they replace split-K slices by tiles: 4096 x 6144 at M = 128 22.3 -> 18.2
+// us, 4096 x 14336 33.5 -> 27.7, 14336 x 4096 32.1 -> 29.2; at M = 192 every layer 6-24%;
+// 128-row ones where the 64-row tiles would add rounds or double a workgroup's k-range at the
+// same count (14336 x 4096 at M = 256: 45.8 against 50.6 us).
 int tr4_pick_bm(int M, int N, int K) {
-  return tr4_cost_us(64, M, N, K) < tr4_cost_us(128, M, N, K) ? 64 : 128;
+  return tr4_cost_us(64, tr4_split_for(64, M, N, K), M, N, K) <
+                 tr4_cost_us(128, tr4_split_for(128, M, N, K), M, N, K)
+             ? 64
+             : 128;
 }
 
 // Split-K for the shape: the most equal k-slices (a divisor of K / 128, at most 16) that keep

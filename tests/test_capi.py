@@ -48,12 +48,12 @@ def test_w4a16_plans():
         assert _pk.w4a16_plan(1, 11008, 4096, 128, s) == (_pk.KERNEL_GEMV, s)
     # prefill: the MFMA GEMM that keeps B packed in LDS, no split needed at 2048 rows
     assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (_pk.KERNEL_GEMM_TR4, 1)
-    # 64-row tiles (chosen by the tile-height cost model) take the most slices: 2 x 24 tiles x 4
-    # for qkv at 128 rows, 2 x 16 x 7 at K = 14336, 2 x 16 x 6 at K = 12288, 3 x 16 x 4 at 129
-    # rows, 3 x 8 x 8 at N = 2048
+    # 64-row tiles (chosen by the tile-height cost model) take the k-split the model prices
+    # lowest within 256 workgroups: 2 x 24 tiles x 4 for qkv at 128 rows, 2 x 16 x 8 at K =
+    # 14336 and at K = 12288, 3 x 16 x 4 at 129 rows, 3 x 8 x 8 at N = 2048
     assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
-    assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 7)
-    assert _pk.w4a16_plan(128, 4096, 12288, 128, 0) == (_pk.KERNEL_GEMM_TR4, 6)
+    assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 8)
+    assert _pk.w4a16_plan(128, 4096, 12288, 128, 0) == (_pk.KERNEL_GEMM_TR4, 8)
     assert _pk.w4a16_plan(129, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
     assert _pk.w4a16_plan(129, 2048, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 8)
     # 128-row tiles take a power of two when it reaches half the most slices: 4, not 7, for
@@ -63,7 +63,7 @@ def test_w4a16_plans():
     assert _pk.w4a16_plan(256, 512, 256, 0, 0)[0] == _pk.KERNEL_GEMM_TR4
     assert _pk.w4a16_plan(256, 520, 256, 0, 0)[0] == _pk.KERNEL_GEMM   # N % 256 != 0
     assert _pk.w4a16_plan(256, 512, 192, 0, 0)[0] == _pk.KERNEL_GEMM   # K % 128 != 0
-    assert _pk.w4a16_plan(128, 512, 256, 0, 0) == (_pk.KERNEL_GEMM_TR4, 2)
+    assert _pk.w4a16_plan(128, 512, 256, 0, 0) == (_pk.KERNEL_GEMM_TR4, 1)  # two k-tiles: unsplit
     assert _pk.w4a16_plan(64, 512, 256, 0, 0)[0] == _pk.KERNEL_SKINNY
     # slices may cut a group (scales are applied per 16-row chunk) ...
     assert _pk.w4a16_plan(1, 4096, 4096, 128, 64) == (_pk.KERNEL_GEMV, 64)
@@ -91,7 +91,7 @@ def test_w4a16_plans_by_row_count():
     assert _pk.w4a16_plan(8, 4096, 4096, 128, 0) == (S, 8)           # 32 tiles x 8 x 8
     assert _pk.w4a16_plan(8, 4096, 14336, 128, 0) == (S, 14)         # 16 wide tiles x 14 x 8
     # 33..64 rows of layers of more than 4096 x 8192 weights: the packed-B GEMM
-    assert _pk.w4a16_plan(48, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 14)  # 64-row tiles
+    assert _pk.w4a16_plan(48, 4096, 14336, 128, 0) == (_pk.KERNEL_GEMM_TR4, 16)  # 64-row tiles
     assert _pk.w4a16_plan(40, 11008, 4096, 128, 0) == (_pk.KERNEL_GEMM_TR4, 4)
     assert _pk.w4a16_plan(64, 8192, 4096, 128, 0) == (S, 4)
     assert _pk.w4a16_plan(48, 4096, 14336, 128, 14) == (S, 14)      # explicit split
@@ -109,8 +109,8 @@ def test_w4a16_plans_by_row_count():
     assert _pk.w4a16_plan(128, 4096, 4096, 128, 0) == (S, 4)      # 32 tiles x 2 parts x 4
     assert _pk.w4a16_plan(96, 4096, 4096, 128, 0) == (S, 4)
     assert _pk.w4a16_plan(72, 1024, 1024, 128, 0) == (S, 4)
-    assert _pk.w4a16_plan(128, 1024, 4096, 128, 0) == (T, 16)     # its plan would need 16
-    assert _pk.w4a16_plan(128, 768, 1024, 128, 0) == (T, 8)       # below 1024^2 weights
+    assert _pk.w4a16_plan(128, 1024, 4096, 128, 0) == (T, 8)      # its plan would need 16
+    assert _pk.w4a16_plan(128, 768, 1024, 128, 0) == (T, 4)       # below 1024^2 weights
     # otherwise above 64 rows: the GEMM that keeps B packed in LDS where its shape rules hold
     # (N % 256, K % 128, group % 64) with the most equal k-slices (at most 16) that keep
     # tiles x slices <= 224, unsplit where the tiles alone reach that: 64 x 256 or 128 x 256
@@ -118,7 +118,7 @@ def test_w4a16_plans_by_row_count():
     # half the most slices)
     assert _pk.w4a16_plan(128, 6144, 4096, 128, 0) == (T, 4)      # 2 x 24 tiles x 4
     assert _pk.w4a16_plan(128, 14336, 4096, 128, 0) == (T, 2)     # 2 x 56 tiles x 2
-    assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (T, 7)     # 2 x 16 tiles x 7 (112 k-tiles)
+    assert _pk.w4a16_plan(128, 4096, 14336, 128, 0) == (T, 8)     # 2 x 16 tiles x 8 (112 k-tiles)
     assert _pk.w4a16_plan(256, 6144, 4096, 128, 0) == (T, 2)      # 4 x 24 tiles of 64 rows x 2
     assert _pk.w4a16_plan(1024, 4096, 4096, 128, 0) == (T, 1)     # 128 tiles (x 2 > 224)
     assert _pk.w4a16_plan(2048, 4096, 4096, 128, 0) == (T, 1)

@@ -99,16 +99,16 @@ def test_tr4_strided_operands(M, split, cuda):
 
 # (M, K, N, G, automatic split): the sweep's qkv layer at 128 rows (64-row tiles, 4 slices),
 # ragged rows with a one-tile slice, group 64 and 256, the largest slice count (16), 64-row
-# tiles at 129 rows (8 of 112 k-tiles), the most slices with 64-row tiles (7 of 112), 128-row
+# tiles at 129 rows (8 of 16 and of 112 k-tiles), the sweep's down layer (8 of 112), 128-row
 # tiles with a power of two chosen over the most slices (4 of 112, not 7), and a slice count
 # that is not a power of two (15 of 15 k-tiles, reduced by the generic-count kernel)
 SPLIT_CASES = [
     (128, 4096, 6144, 128, 4),
     (65, 1024, 512, 64, 8),
     (100, 2048, 256, 256, 16),
-    (129, 2048, 1024, 128, 16),
+    (129, 2048, 1024, 128, 8),
     (129, 14336, 2048, 128, 8),
-    (128, 14336, 4096, 128, 7),
+    (128, 14336, 4096, 128, 8),
     (256, 14336, 4096, 128, 4),
     (128, 1920, 256, 128, 15),
 ]
