@@ -991,7 +991,22 @@ def hbm_ceiling(dev) -> dict:
                         "frac_of_8TBs": round(tbs / (HBM_PEAK_GBS / 1000), 4)}
         rows.append(best)
         del bufs
-    return {"hbm_read_ceiling": rows}
+    # The headline GEMV's own read pattern (688 strips of 32 KB, one workgroup of 8 waves per
+    # strip, U blocks of 1 KB per wave) with no other work, over 40 rotating copies of the
+    # packed weights (22,544,384 B; the GEMV also reads 704,512 B of scales and the activations).
+    strips, strip_bytes = 11008 // 16, 4096 // 2 * 16
+    nbytes = strips * strip_bytes
+    bufs = [torch.empty(nbytes // 4, dtype=torch.int32, device=dev).fill_(i) for i in range(N_ROTATE)]
+    out = torch.empty(64 * -(-strips // 8), dtype=torch.int32, device=dev)
+    pattern = []
+    for u in (2, 4, 8):
+        ms = GraphTimer(lambda i: _probes.strip_read_probe(bufs[i % N_ROTATE], strips, u, out),
+                        2000, 2).run(reps=3, preroll=PREROLL)
+        tbs = nbytes / (ms * 1e-3) / 1e12
+        pattern.append({"bytes": nbytes, "blocks_per_wave": u, "us": round(ms * 1e3, 3),
+                        "TB/s": round(tbs, 3), "frac_of_8TBs": round(tbs / (HBM_PEAK_GBS / 1000), 4)})
+    del bufs
+    return {"hbm_read_ceiling": rows, "strip_read_pattern": pattern}
 
 
 def measured_traffic():

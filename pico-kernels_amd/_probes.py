@@ -20,6 +20,7 @@ _vp, _i32, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 _SIGNATURES = {
     "pkb_mfma_probe": (_i32, [_i32, _i32, _i32, _i32, _vp, _vp]),
     "pkb_read_probe": (_i32, [_vp, _sz, _vp, _i32, _vp]),
+    "pkb_strip_read_probe": (_i32, [_vp, _i32, ctypes.c_int64, _i32, _vp, _vp]),
     "pkb_xcc_count": (_i32, []),
     "pkb_xcc_probe": (_i32, [_i32, _i32, _i32, _i32, _vp, _vp]),
 }
@@ -82,3 +83,14 @@ def xcc_probe(grid: int, threads: int, lds_bytes: int, spin: int, out: torch.Ten
     assert out.dtype == torch.int32 and out.numel() >= grid and out.is_cuda
     _check(lib().pkb_xcc_probe(int(grid), int(threads), int(lds_bytes), int(spin), out.data_ptr(),
                                _stream(out)), "pkb_xcc_probe")
+
+
+def strip_read_probe(src: torch.Tensor, strips: int, u: int, out: torch.Tensor) -> None:
+    """The strip GEMV's read pattern alone on the current stream: ``src`` holds ``strips``
+    contiguous strips of equal size (a multiple of 1 KB); ``out`` holds at least
+    ``64 * ceil(strips / 8)`` int32 words."""
+    nbytes = src.numel() * src.element_size()
+    assert out.dtype == torch.int32 and out.numel() >= 64 * -(-strips // 8) and out.is_cuda
+    assert nbytes % strips == 0
+    _check(lib().pkb_strip_read_probe(src.data_ptr(), int(strips), nbytes // strips, int(u),
+                                      out.data_ptr(), _stream(src)), "pkb_strip_read_probe")

@@ -23,6 +23,13 @@ int pkb_mfma_probe(int fp8, int random, int grid, int iters, float* out, void* s
  * writes one 32-bit word per workgroup (the XOR of the words it read) to out. */
 int pkb_read_probe(const void* src, size_t bytes, uint32_t* out, int grid, void* stream);
 
+/* The strip GEMV's read pattern alone: one workgroup of 8 waves per strip of strip_bytes
+ * (a multiple of 1024, below 2 GiB) contiguous bytes at src (16-byte aligned), each wave
+ * loading u (1, 2, 4 or 8) consecutive 1 KB blocks per round; out receives 8 words per
+ * workgroup (8 * 8 * ceil(strips / 8) in all). */
+int pkb_strip_read_probe(const void* src, int strips, int64_t strip_bytes, int u, uint32_t* out,
+                         void* stream);
+
 /* The partition's XCD count (hipDeviceAttributeNumberOfXccs of the current device), or -1. */
 int pkb_xcc_count(void);
 

@@ -85,6 +85,34 @@ __global__ __launch_bounds__(256) void hbm_read_probe_kernel(const pk_u4v* src, 
   if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
+// The decode GEMV's read pattern with nothing else: one workgroup of 8 waves per 16-column
+// strip (strip_bytes contiguous bytes, strips in the GEMV's XCD order), each wave loading its
+// `u` consecutive 1 KB blocks with 16-byte non-temporal loads (lane L: bytes 16 L of each
+// block), XOR-reducing them and writing one word per wave. No activations, scales, products or
+// fold: the floor the strip GEMV's launch is read against.
+__global__ __launch_bounds__(512) void strip_read_probe_kernel(const uint8_t* src, int strips,
+                                                              int64_t strip_bytes, int u, int spx,
+                                                              uint32_t* out) {
+  const int s = (int)(blockIdx.x & 7) * spx + (int)(blockIdx.x >> 3);
+  if (s >= strips) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(src + (int64_t)s * strip_bytes, (uint32_t)strip_bytes);
+  const int kb = (int)(strip_bytes / 1024);
+  uint32_t x = 0u;
+  for (int b0 = wave * u; b0 < kb; b0 += 8 * u) {
+    pk_u4v v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      v[i] = i < u && b0 + i < kb
+                 ? __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, (b0 + i) * 1024, kPkLoadStream)
+                 : pk_u4v{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+  }
+  for (int o = 32; o > 0; o >>= 1) x ^= (uint32_t)__shfl_xor((int)x, o, 64);
+  if (lane == 0) out[blockIdx.x * 8 + wave] = x;
+}
+
 // The XCD (XCC id in the partition) each workgroup runs on. Each workgroup holds `lds_bytes`
 // of dynamic LDS and sleeps about `spin` x 64 clocks before it records, so a grid larger
 // than the machine is dispatched in several waves of residency, as the product's grids are.
@@ -125,6 +153,18 @@ extern "C" int pkb_read_probe(const void* src, size_t bytes, uint32_t* out, int 
   if (bytes < 16 || bytes % 16 || (reinterpret_cast<uintptr_t>(src) & 15)) return -1;
   hbm_read_probe_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(
       reinterpret_cast<const pk_u4v*>(src), (int64_t)(bytes / 16), out);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pkb_strip_read_probe(const void* src, int strips, int64_t strip_bytes, int u,
+                                    uint32_t* out, void* stream) {
+  if (src == nullptr || out == nullptr || strips < 1 || strip_bytes < 1024 || strip_bytes % 1024 ||
+      (u != 1 && u != 2 && u != 4 && u != 8) || (reinterpret_cast<uintptr_t>(src) & 15) ||
+      strip_bytes >= (1ll << 31))
+    return -1;
+  const int spx = (strips + 7) / 8;
+  strip_read_probe_kernel<<<8 * spx, 512, 0, (hipStream_t)stream>>>(
+      reinterpret_cast<const uint8_t*>(src), strips, strip_bytes, u, spx, out);
   return (int)hipGetLastError();
 }
 

@@ -1,7 +1,8 @@
-"""The measurement probes behind `bench.py --hbm-ceiling` and `--mfma-ceiling`: the read probe
-visits every word of the buffer exactly once (the XOR of its per-workgroup results equals the
-XOR of all words, for several grids and a ragged length), and the MFMA probe's constant-operand
-run gives the closed-form sum."""
+"""The measurement probes behind `bench.py --hbm-ceiling` and `--mfma-ceiling`: the read probes
+visit every word of the buffer exactly once (the XOR of their per-workgroup or per-wave results
+equals the XOR of all words: the grid-stride probe for several grids and a ragged length, the
+strip-pattern probe for several strip counts, strip sizes and blocks per wave), and the MFMA
+probe's constant-operand run gives the closed-form sum."""
 
 from __future__ import annotations
 
@@ -23,6 +24,19 @@ def test_read_probe_reads_every_word_once(grid, words, cuda):
     src = host.to(cuda)
     out = torch.zeros(grid, dtype=torch.int32, device=cuda)
     _probes.read_probe(src, out, grid)
+    got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+    want = np.bitwise_xor.reduce(host.numpy().view(np.uint32))
+    assert got == want
+
+
+@pytest.mark.parametrize("strips,kb,u", [(688, 32, 4), (9, 11, 2), (16, 5, 8), (1, 1, 1)])
+def test_strip_read_probe_reads_every_word_once(strips, kb, u, cuda):
+    g = torch.Generator()
+    g.manual_seed(strips * 100 + kb * 10 + u)
+    words = strips * kb * 256  # kb blocks of 1 KB per strip
+    host = torch.randint(-2**31, 2**31 - 1, (words,), generator=g, dtype=torch.int64).to(torch.int32)
+    out = torch.zeros(64 * -(-strips // 8), dtype=torch.int32, device=cuda)
+    _probes.strip_read_probe(host.to(cuda), strips, u, out)
     got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
     want = np.bitwise_xor.reduce(host.numpy().view(np.uint32))
     assert got == want
