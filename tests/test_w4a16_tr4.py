@@ -169,3 +169,23 @@ def test_tr4_mid_rows_on_large_layers(M, K, N, cuda):
     assert oracle.rel_fro(out.cpu().numpy(), oracle.w4a16_ref(a.numpy(), codes, s16, 128)) <= 1e-3
     tiles = _pk.w4a16_gemm(ag, _pk.tile_weights(qw), sc, 128, 1.0, torch.float32, tiled=True)
     assert torch.equal(out, tiles)
+
+
+@pytest.mark.parametrize("pad,offset", [(4, 0), (1, 0), (4, 1)])
+def test_tr4_strided_and_offset_weight_views(pad, offset, cuda):
+    """Row-layout weights as a view into a wider buffer (ldq = N/8 + pad words) starting
+    `offset` words in: a 16-byte aligned base and row pitch run the packed-B GEMM, anything
+    else the GEMM that gathers B through registers; both against the oracle, bitwise repeatable."""
+    M, K, N, G = 128, 1024, 512, 128
+    a, codes, s16, qw, sc = _case(M, K, N, G, 77 + pad + offset, cuda)
+    wide = torch.zeros((K, N // 8 + pad + offset), dtype=torch.int32, device=cuda)
+    view = wide[:, offset:offset + N // 8]
+    view.copy_(qw)
+    assert view.stride(0) == N // 8 + pad + offset and view.data_ptr() % 16 == 4 * offset % 16
+    ag = a.to(cuda)
+    out = _pk.w4a16_gemm(ag, view, sc, G, 1.0, torch.float32)
+    assert torch.equal(out, _pk.w4a16_gemm(ag, view, sc, G, 1.0, torch.float32))
+    ref = oracle.w4a16_ref(a.numpy(), codes, s16, G)
+    assert oracle.rel_fro(out.cpu().numpy(), ref) < 1e-3
+    if pad % 4 == 0 and offset == 0:  # aligned: the same kernel and bits as contiguous weights
+        assert torch.equal(out, _pk.w4a16_gemm(ag, qw, sc, G, 1.0, torch.float32))
