@@ -1,5 +1,6 @@
-// e4m3 fp8 GEMM for gfx950, 256 x 256 (or 256 x 128) tiles, 4-stage LDS pipeline, B in
-// either layout through LDS DMA (v_mfma_f32_32x32x64_f8f6f4).
+// e4m3 fp8 GEMM for gfx950, 256 x 256 (or 256 x 128) tiles, LDS pipeline of four B stages
+// and three A buffers of two k-tiles, both operands through LDS DMA
+// (v_mfma_f32_32x32x64_f8f6f4).
 //
 // C[m, n] = out_scale * sum_k A[m, k] * B[k, n] (gemm_fp8.py:38-117), A (M, K) row-major,
 // B (K, N) row-major (BLAYOUT 0) or (N, K) row-major (BLAYOUT 1, a transposed view).
@@ -9,16 +10,21 @@
 //    256 x 128 tiles (for outputs whose 256 x 256 tiles would leave CUs idle: 2048 x 4096
 //    is 128 of them for 256 CUs) use 4 x 2 waves of 64 x 64 (2 x 2 fragments), a B stage of
 //    8 KB and one B DMA per wave and tile.
-//  * K tiles of 64. A tile = 256 rows x 64 bytes, B tile = 64 k x 256 n (BLAYOUT 0) or
-//    256 n x 64 k (BLAYOUT 1); both go global -> LDS with buffer DMA (no VGPR staging).
-//  * Four LDS stages (32 KB each). One barrier per tile, in its middle: each tile's first
-//    half of MFMAs runs on fragments read during the previous tile, the barrier publishes
-//    tile t+1 (whose DMAs went out two tiles earlier; tile t+2's stay outstanding), the DMAs
-//    of tile t+3 go into tile t-1's stage, and the second half of MFMAs runs while tile t+1's
+//  * K tiles of 64. B tile = 64 k x 256 n (BLAYOUT 0) or 256 n x 64 k (BLAYOUT 1) per stage;
+//    A goes in pairs of k-tiles, 256 rows x 128 bytes per buffer, so every A DMA reads whole
+//    128-byte lines (one k-tile per DMA read half lines: measured on MI355X, 4096^3 +2.3%,
+//    2048 x 4096 x 4096 +6% with pairs). Both go global -> LDS with buffer DMA (no VGPR
+//    staging).
+//  * Four B stages and three A pair buffers (160 KB at 256 x 256). One barrier per tile, in
+//    its middle: each tile's first half of MFMAs runs on fragments read during the previous
+//    tile, the barrier publishes tile t+1 (whose DMAs went out two or more tiles earlier), the
+//    DMAs of B tile t+3 go into tile t-1's stage and, at even t, those of A pair t/2 + 2 into
+//    the buffer of tiles t-2 and t-1, and the second half of MFMAs runs while tile t+1's
 //    fragments are read into registers -- no wave waits on LDS reads after the barrier.
-//  * k-contiguous tiles (A; B^T) use 64-byte rows in 4 chunks of 16 B, chunk c of row r in
-//    slot c ^ ((r >> 2) & 3): 16 lanes reading 16 consecutive rows at one chunk hit 16
-//    distinct 16-byte bank groups.
+//  * LDS rows: A's 128-byte rows in 8 chunks of 16 B, chunk c of row r in slot
+//    c ^ ((r >> 1) & 7); B^T's 64-byte rows in 4 chunks, chunk c of row r in slot
+//    c ^ ((r >> 2) & 3): 16 lanes reading 16 consecutive rows at one chunk hit 16 distinct
+//    16-byte bank groups.
 //  * (K, N) B keeps n contiguous (256-byte rows, 16 chunks, chunk c of row k in slot
 //    c ^ 2(k & 7)) and is read with ds_read_b64_tr_b8: within a 16-lane group lane j gets
 //    byte b from the address of lane 2b + j/8 at offset j % 8. Even lanes address row k0 + b
@@ -27,8 +33,8 @@
 //  * The MFMAs take B as the first operand, so each accumulator is C^T and every lane ends
 //    with four consecutive columns of one row per register quad. Stored directly, one store
 //    instruction would write 8 or 16 bytes into each of 32 rows; instead each wave stages its
-//    block through a free stage array and writes whole 128-byte lines (measured on MI355X:
-//    the 4096^3 fp16-output GEMM 10% faster).
+//    block through free LDS (a half pair buffer or a B stage) and writes whole 128-byte lines
+//    (measured on MI355X: the 4096^3 fp16-output GEMM 10% faster).
 #include "pk_internal.h"
 
 namespace pk {
@@ -84,20 +90,29 @@ __device__ __forceinline__ void f8_tile_of(int bid, int tiles_m, int tiles_n, in
   *tn = in_g / gm;
 }
 
+template <int I, int N, class F>
+__device__ __forceinline__ void f8_static_for(F&& f) {
+  if constexpr (I < N) {
+    f(pk_int_c<I>{});
+    f8_static_for<I + 1, N>(f);
+  }
+}
+
 template <int BLAYOUT, int BN>
 __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
   constexpr int BM = 256, BK = 64;
   constexpr int WAVES_N = BN / 64, WAVES_M = 8 / WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = 64, FM = WTM / 32, FN = 2;
-  constexpr int STAGE = BM * BK;      // bytes of A per stage (16 KB)
+  constexpr int APAIR = 2 * BM * BK;  // bytes of A per pair of k-tiles (32 KB): 128-byte rows
   constexpr int STAGE_B = BN * BK;    // bytes of B per stage
   constexpr int NBD = BN / 128;       // B DMA instructions per wave and tile
-  constexpr int PARTS = 2 + NBD;      // DMA instructions per wave and tile
+  constexpr int NAD = APAIR / 8192;   // A DMA instructions per wave and pair of k-tiles (4)
 
-  __shared__ __align__(16) char sA0[STAGE];
-  __shared__ __align__(16) char sA1[STAGE];
-  __shared__ __align__(16) char sA2[STAGE];
-  __shared__ __align__(16) char sA3[STAGE];
+  // A in three buffers of a k-tile pair each (every DMA reads whole 128-byte lines: a row's
+  // 128 k-bytes of two k-tiles), B in four stages of one k-tile.
+  __shared__ __align__(16) char sAP0[APAIR];
+  __shared__ __align__(16) char sAP1[APAIR];
+  __shared__ __align__(16) char sAP2[APAIR];
   __shared__ __align__(16) char sB0[STAGE_B];
   __shared__ __align__(16) char sB1[STAGE_B];
   __shared__ __align__(16) char sB2[STAGE_B];
@@ -110,15 +125,22 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
   const int m0 = tm * BM, n0 = tn * BN;
   const int ktiles = p.K / BK;
 
-  // ---- DMA sources: two 1 KB instructions per wave per operand per tile ----
+  // ---- DMA sources. A: NAD = 4 1 KB instructions per wave and k-tile pair, instruction i
+  // rows (4 wave + i) * 8 .. +7 of 128 bytes (lane L: row + L / 8, slot L % 8 holding chunk
+  // (L % 8) ^ ((row >> 1) & 7)); instructions 2 and 3 are 0 and 1 sixteen rows on (the same
+  // chunk pattern), by the scalar offset. Rows past M read zeros (past the buffer's end: M *
+  // lda < 2^31 and lda < 2^23, so the offsets stay below 2^32) and are never stored. B: NBD
+  // per wave and k-tile ----
+  static_assert(NAD == 4, "four A instructions per wave and pair");
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
   int a_off[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int r = (wave * 2 + i) * 16 + (lane >> 2);  // 16 rows of 64 bytes per instruction
-    const int c = (lane & 3) ^ ((r >> 2) & 3);
-    a_off[i] = (int)((int64_t)min(m0 + r, p.M - 1) * p.lda) + c * 16;
+    const int r = (wave * NAD + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_off[i] = (int)((int64_t)(m0 + r) * p.lda) + c * 16;
   }
+  const int a_skip = 16 * (int)p.lda;  // bytes of 16 rows
   __amdgpu_buffer_rsrc_t rb;
   int b_off[NBD];
   if constexpr (BLAYOUT == 1) {
@@ -139,41 +161,47 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
       b_off[i] = (int)((int64_t)k * p.ldb) + min(n0 + c * 16, p.N - 16);
     }
   }
-  // DMA `part` (0, 1: A; 2 .. PARTS-1: B) of tile kt
-  auto issue_part = [&](int kt, char* sA, char* sB, int part) {
-    if (part < 2) {
-      f8_dma16(ra, sA + (wave * 2 + part) * 1024, a_off[part], kt * BK);
-    } else {
-      const int bs = BLAYOUT == 1 ? kt * BK : (int)((int64_t)kt * BK * p.ldb);
-      f8_dma16(rb, sB + (wave * NBD + part - 2) * 1024, b_off[part - 2], bs);
-    }
-  };
-  auto issue = [&](int kt, char* sA, char* sB) {
+  // B of k-tile kt; A of k-tile pair kp (k-tiles 2 kp, 2 kp + 1: past K when K / 64 is odd, a
+  // pair's second half reads bytes no MFMA uses -- the next row's, or zeros past the buffer).
+  auto issue_b = [&](int kt, char* sB) {
+    const int bs = BLAYOUT == 1 ? kt * BK : (int)((int64_t)kt * BK * p.ldb);
 #pragma unroll
-    for (int part = 0; part < PARTS; ++part) issue_part(kt, sA, sB, part);
+    for (int i = 0; i < NBD; ++i) f8_dma16(rb, sB + (wave * NBD + i) * 1024, b_off[i], bs);
+  };
+  auto issue_a = [&](int kp, char* sAP) {
+#pragma unroll
+    for (int i = 0; i < NAD; ++i)
+      f8_dma16(ra, sAP + (wave * NAD + i) * 1024, a_off[i & 1], kp * 2 * BK + (i >> 1) * a_skip);
   };
 
-  // ---- fragment offsets inside a stage ----
-  int aoff[FM][2];
+  // ---- fragment offsets. A, in a pair buffer: row r, 16-byte chunk c of k-tile half hf at
+  // slot (4 hf + c) ^ ((r >> 1) & 7) -- the second half's offset is the first's XOR 64. The 16
+  // rows a 16-lane group reads at one chunk cover all 16 bank groups. ----
+  // Fragment row i adds 32 * 128 bytes (the swizzle depends on (lane & 31) only, wm0 and 32 i
+  // being multiples of 32), so one register per (half, chunk) covers every fragment row.
+  int aoff[2][2];  // [k-tile half][chunk of the lane's pair]
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) aoff[i][h] = f8_swz64(wm0 + 32 * i + (lane & 31), 2 * (lane >> 5) + h);
-  int boff[FN][4];  // BLAYOUT 1: [j][h] chunk pair; BLAYOUT 0: [j][q] transposing reads
+    for (int h = 0; h < 2; ++h) {
+      const int r = wm0 + (lane & 31), c = 4 * hf + 2 * (lane >> 5) + h;
+      aoff[hf][h] = r * 128 + ((c ^ ((r >> 1) & 7)) << 4);
+    }
+  // BLAYOUT 1: [j][h] chunk pair, fragment j adding 32 rows of 64 bytes to j = 0's (the swizzle
+  // depends on (lane & 31) only); BLAYOUT 0: [j][0] transposing reads, read q adding 8 k rows
+  // (the swizzle depends on k & 7 only).
+  int boff[FN][2];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     if constexpr (BLAYOUT == 1) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) boff[j][h] = f8_swz64(wn0 + 32 * j + (lane & 31), 2 * (lane >> 5) + h);
-      boff[j][2] = boff[j][3] = 0;
+      for (int h = 0; h < 2; ++h) boff[j][h] = f8_swz64(wn0 + (lane & 31), 2 * (lane >> 5) + h);
     } else {
       const int i16 = lane & 15;
       const int cs = wn0 + 32 * j + 16 * ((lane >> 4) & 1) + 8 * (i16 & 1);  // first column
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int k = 32 * (lane >> 5) + 8 * q + (i16 >> 1);
-        boff[j][q] = f8_swzB<BN>(k, cs >> 4) + (cs & 15);
-      }
+      const int k = 32 * (lane >> 5) + (i16 >> 1);
+      boff[j][0] = f8_swzB<BN>(k, cs >> 4) + (cs & 15);
+      boff[j][1] = 0;
     }
   }
 
@@ -193,23 +221,24 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       if constexpr (BLAYOUT == 1) {
-        const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sB + boff[j][0]);
-        const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sB + boff[j][1]);
+        const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sB + boff[0][0] + 2048 * j);
+        const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sB + boff[0][1] + 2048 * j);
         bf[par][j] = (pk_i8v){(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
       } else {
+        constexpr int KQ = 8 * BN;  // bytes of 8 k rows
         const pk_i2v y0 = f8_read_tr(sB + boff[j][0]);
-        const pk_i2v y1 = f8_read_tr(sB + boff[j][1]);
-        const pk_i2v y2 = f8_read_tr(sB + boff[j][2]);
-        const pk_i2v y3 = f8_read_tr(sB + boff[j][3]);
+        const pk_i2v y1 = f8_read_tr(sB + boff[j][0] + KQ);
+        const pk_i2v y2 = f8_read_tr(sB + boff[j][0] + 2 * KQ);
+        const pk_i2v y3 = f8_read_tr(sB + boff[j][0] + 3 * KQ);
         bf[par][j] = (pk_i8v){y0[0], y0[1], y1[0], y1[1], y2[0], y2[1], y3[0], y3[1]};
       }
     }
   };
-  auto read_a = [&](const char* sA, int i0, int i1) {
+  auto read_a = [&](const char* sAP, int hf, int i0, int i1) {
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
-      const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sA + aoff[i][0]);
-      const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sA + aoff[i][1]);
+      const pk_u4v x0 = *reinterpret_cast<const pk_u4v*>(sAP + aoff[hf][0] + 4096 * i);
+      const pk_u4v x1 = *reinterpret_cast<const pk_u4v*>(sAP + aoff[hf][1] + 4096 * i);
       af[i] = (pk_i8v){(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
     }
   };
@@ -234,57 +263,71 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
     }
   };
 
-  // ---- pipeline. Tile t (stage t % 4) starts with its B fragments and first-half A
-  // fragments in registers. First half: MFMAs of rows 0 .. HF-1 while the second half's A
-  // fragments are read. Then every wave waits for its DMAs of tile t+1 and the workgroup meets
-  // (tile t+1 is in LDS everywhere; every wave has finished tile t-1, so its stage is free)
-  // and the DMAs of tile t+3 go into that stage, between the second half's MFMAs, which also
-  // read tile t+1's B and first-half A fragments: the next tile starts with its operands in
-  // registers and no wave waits on LDS after the barrier. Tiles past the end are re-reads of
-  // the last tile into a stage nobody reads, so every tile has the same DMA count in flight.
-  const int last = ktiles - 1;
-  issue(0, sA0, sB0);
-  issue(min(1, last), sA1, sB1);
-  issue(min(2, last), sA2, sB2);
+  // ---- pipeline. Tile t (B stage t % 4, A pair buffer (t / 2) % 3, half t % 2) starts with
+  // its B fragments and first-half A fragments in registers. First half: MFMAs of rows
+  // 0 .. HF-1 while the second half's A fragments are read. Then every wave waits for its DMAs
+  // of tile t+1 and the workgroup meets (tile t+1 is in LDS everywhere; every wave has
+  // finished tile t-1, so its B stage is free, and at even t so is the pair buffer of tiles
+  // t-2 and t-1), and the DMAs of B tile t+3 and, at even t, of A pair t/2 + 2 (tiles t+4 and
+  // t+5) go into those, between the second half's MFMAs, which also read tile t+1's B and
+  // first-half A fragments: the next tile starts with its operands in registers and no wave
+  // waits on LDS after the barrier. Tiles past the end are re-reads of the last tile (pair)
+  // into a stage nobody reads, so the DMA count in flight is the same at every barrier: after
+  // B tile t+1 come B tile t+2 and one A pair, NBD + NAD instructions.
+  const int last = ktiles - 1, lastp = last / 2;
+  issue_a(0, sAP0);
+  issue_b(0, sB0);
+  issue_b(min(1, last), sB1);
+  issue_a(min(1, lastp), sAP1);
+  issue_b(min(2, last), sB2);
   // s_waitcnt vmcnt(n) expcnt(7) lgkmcnt(15). The barrier is a bare s_barrier: __syncthreads()
   // adds a workgroup release fence, which waits for *every* outstanding LDS DMA (vmcnt(0)) and
   // would serialise the pipeline. The explicit wait covers the data the barrier publishes, and
   // the asm memory clobber keeps the compiler from moving LDS accesses across it.
-  constexpr int kWaitTile0 = 0x0f70 | (2 * PARTS);  // tile 0 landed, tiles 1 and 2 in flight
-  constexpr int kWaitNext = 0x0f70 | PARTS;         // tile t+1 landed, tile t+2 in flight
+  constexpr int kWaitTile0 = 0x0f70 | (2 * NBD + NAD);  // A pair 0 and B tile 0 landed
+  constexpr int kWaitNext = 0x0f70 | (NBD + NAD);       // B tile t+1 (and A of t+1) landed
+  static_assert(2 * NBD + NAD < 16, "vmcnt fits the immediate's low field");
   __builtin_amdgcn_s_waitcnt(kWaitTile0);
   asm volatile("s_barrier" ::: "memory");
   read_b(sB0, 0);
-  read_a(sA0, 0, P1);
+  read_a(sAP0, 0, 0, P1);
 
-  auto step = [&](int kt, const char* sAc, const char* sAn, const char* sBn, char* sAx, char* sBx,
-                  auto PAR) {
-    constexpr int par = decltype(PAR)::value;
+  auto step = [&](int kt, const char* sAPc, const char* sAPn, const char* sBn, char* sBx,
+                  char* sAPx, auto U) {
+    constexpr int u = decltype(U)::value;
+    constexpr int par = u & 1, hc = u & 1, hn = (u + 1) & 1;
+    constexpr bool issue_pair = (u & 1) == 0;
     fence();
     mfma_rows(0, P1, par);
-    read_a(sAc, P1, FM);
+    read_a(sAPc, hc, P1, FM);
     pattern(pk_int_c<P1 * FN>{}, pk_int_c<2 * (FM - P1)>{}, pk_int_c<0>{});
     fence();
     __builtin_amdgcn_s_waitcnt(kWaitNext);
     asm volatile("s_barrier" ::: "memory");
     fence();
-    issue(min(kt + 3, last), sAx, sBx);
+    issue_b(min(kt + 3, last), sBx);
+    if constexpr (issue_pair) issue_a(min(kt / 2 + 2, lastp), sAPx);
     mfma_rows(P1, FM, par);
     read_b(sBn, par ^ 1);
-    read_a(sAn, 0, P1);
-    pattern(pk_int_c<(FM - P1) * FN>{}, pk_int_c<(BLAYOUT == 1 ? 2 : 4) * FN + 2 * P1>{}, pk_int_c<PARTS>{});
+    read_a(sAPn, hn, 0, P1);
+    pattern(pk_int_c<(FM - P1) * FN>{}, pk_int_c<(BLAYOUT == 1 ? 2 : 4) * FN + 2 * P1>{},
+            pk_int_c<NBD + (issue_pair ? NAD : 0)>{});
     fence();
   };
+  // 12 tiles per pass: the B stages cycle every 4, the A pair buffers every 6.
+  auto sap = [&](int i) -> char* { return i == 0 ? sAP0 : i == 1 ? sAP1 : sAP2; };
+  auto sbs = [&](int i) -> char* { return i == 0 ? sB0 : i == 1 ? sB1 : i == 2 ? sB2 : sB3; };
+  auto step_u = [&](int kt, auto U) {
+    constexpr int u = decltype(U)::value;
+    step(kt, sap((u / 2) % 3), sap(((u + 1) / 2) % 3), sbs((u + 1) % 4), sbs((u + 3) % 4),
+         sap((u / 2 + 2) % 3), U);
+  };
   int kt = 0;
-  for (; kt + 3 < ktiles; kt += 4) {
-    step(kt, sA0, sA1, sB1, sA3, sB3, pk_int_c<0>{});
-    step(kt + 1, sA1, sA2, sB2, sA0, sB0, pk_int_c<1>{});
-    step(kt + 2, sA2, sA3, sB3, sA1, sB1, pk_int_c<0>{});
-    step(kt + 3, sA3, sA0, sB0, sA2, sB2, pk_int_c<1>{});
-  }
-  if (kt < ktiles) step(kt, sA0, sA1, sB1, sA3, sB3, pk_int_c<0>{});
-  if (kt + 1 < ktiles) step(kt + 1, sA1, sA2, sB2, sA0, sB0, pk_int_c<1>{});
-  if (kt + 2 < ktiles) step(kt + 2, sA2, sA3, sB3, sA1, sB1, pk_int_c<0>{});
+  for (; kt + 11 < ktiles; kt += 12)
+    f8_static_for<0, 12>([&](auto U) { step_u(kt + decltype(U)::value, U); });
+  f8_static_for<0, 11>([&](auto U) {
+    if (kt + decltype(U)::value < ktiles) step_u(kt + decltype(U)::value, U);
+  });
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): no DMA into LDS outlives the waves
   mfma_drain();
 
@@ -302,11 +345,11 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
     __syncthreads();                     // and every other wave's: the stages are free
     // a wave-uniform region of 64 rows x 64 fp32 (16 KB; 256 x 128 tiles: 32 rows, 8 KB)
     char* sW;
-    if constexpr (BN == 256)
-      sW = wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sA2 : wave == 3 ? sA3
-         : wave == 4 ? sB0 : wave == 5 ? sB1 : wave == 6 ? sB2 : sB3;
-    else
-      sW = (wave < 2 ? sA0 : wave < 4 ? sA1 : wave < 6 ? sA2 : sA3) + (wave & 1) * 8192;
+    if constexpr (BN == 256)  // 16 KB each: halves of the pair buffers, B stages 0 and 1
+      sW = wave < 2 ? sAP0 + wave * 16384 : wave < 4 ? sAP1 + (wave - 2) * 16384
+         : wave < 6 ? sAP2 + (wave - 4) * 16384 : wave == 6 ? sB0 : sB1;
+    else  // 8 KB each: quarters of pair buffers 0 and 1
+      sW = (wave < 4 ? sAP0 : sAP1) + (wave & 3) * 8192;
     with_dtype(p.c_dtype, [&](auto DT) {
       constexpr int dt = decltype(DT)::value;
       constexpr int E = dt == PK_F32 ? 4 : 2;
