@@ -122,15 +122,17 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
   const int wm0 = (wave / WAVES_N) * WTM, wn0 = (wave % WAVES_N) * WTN;
   int tm, tn;
   f8_tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  // The last row of tiles ends at row M (M >= BM): where M % BM != 0 it overlaps the row of
+  // tiles before it, whose rows it computes to the same bits, so no A row past M is read.
+  const int m0 = min(tm * BM, p.M - BM), n0 = tn * BN;
   const int ktiles = p.K / BK;
 
   // ---- DMA sources. A: NAD = 4 1 KB instructions per wave and k-tile pair, instruction i
   // rows (4 wave + i) * 8 .. +7 of 128 bytes (lane L: row + L / 8, slot L % 8 holding chunk
   // (L % 8) ^ ((row >> 1) & 7)); instructions 2 and 3 are 0 and 1 sixteen rows on (the same
-  // chunk pattern), by the scalar offset. Rows past M read zeros (past the buffer's end: M *
-  // lda < 2^31 and lda < 2^23, so the offsets stay below 2^32) and are never stored. B: NBD
-  // per wave and k-tile ----
+  // chunk pattern), by the scalar offset. Every row read is < M (the tile row above) and
+  // every k < K (K % 128 == 0: whole pairs), so no access depends on how the hardware
+  // range-checks the scalar offset. B: NBD per wave and k-tile ----
   static_assert(NAD == 4, "four A instructions per wave and pair");
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
   int a_off[2];
@@ -161,8 +163,7 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
       b_off[i] = (int)((int64_t)k * p.ldb) + min(n0 + c * 16, p.N - 16);
     }
   }
-  // B of k-tile kt; A of k-tile pair kp (k-tiles 2 kp, 2 kp + 1: past K when K / 64 is odd, a
-  // pair's second half reads bytes no MFMA uses -- the next row's, or zeros past the buffer).
+  // B of k-tile kt; A of k-tile pair kp (k-tiles 2 kp, 2 kp + 1).
   auto issue_b = [&](int kt, char* sB) {
     const int bs = BLAYOUT == 1 ? kt * BK : (int)((int64_t)kt * BK * p.ldb);
 #pragma unroll
@@ -416,7 +417,7 @@ __global__ __launch_bounds__(512) void gemm_f8_v3_kernel(F8Params p) {
 }
 
 bool f8_v3_ok(int M, int N, int K, int64_t lda, int64_t ldb, int b_layout, const void* b) {
-  if (M < 256 || N < 256 || K % 64 || N % 16 || lda % 16 || ldb % 16) return false;
+  if (M < 256 || N < 256 || K % 128 || N % 16 || lda % 16 || ldb % 16) return false;
   if ((reinterpret_cast<uintptr_t>(b) & 15) != 0) return false;
   if ((int64_t)M * lda >= (1ll << 31)) return false;
   return (b_layout == 1 ? (int64_t)N * ldb : (int64_t)K * ldb) < (1ll << 31);

@@ -108,12 +108,15 @@ def _fp8_case(M, K, N, seed, cuda):
 
 @pytest.mark.parametrize("M,K,N", [(256, 256, 256), (100, 384, 264), (1, 128, 8), (513, 1024, 520),
                                    (2048, 2048, 2048),
-                                   # large-tile kernel: ragged M/N tiles, 2-, 6- and 10-tile K loops
+                                   # large-tile kernel: ragged M/N tiles (the last row of tiles
+                                   # moved up to end at row M, overlapping the one before it),
+                                   # 2-, 6- and 10-tile K loops
                                    (600, 384, 784), (300, 128, 272), (257, 640, 528),
                                    # 128 x 128 kernel, (K, N) B, odd tile count
                                    (100, 384, 272), (128, 384, 256),
-                                   # K not a multiple of 128: 4-stage kernel (K % 64), fallback
-                                   # kernel with a partial last k-tile (K % 16)
+                                   # K not a multiple of 128 (whole k-tile pairs, which the
+                                   # large-tile kernels need): the fallback kernel, with a
+                                   # partial last k-tile where K % 64 != 0
                                    (512, 320, 512), (300, 64, 272), (100, 208, 264), (64, 16, 64),
                                    (513, 1040, 520)])
 def test_fp8_gemm_matches_closed_form(M, K, N, cuda):
