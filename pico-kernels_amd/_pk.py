@@ -151,6 +151,15 @@ def to_gpu(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_cuda else t.to(gpu_device())
 
 
+def _gpu_args(what: str, first: torch.Tensor, *others: torch.Tensor | None) -> None:
+    """Raise unless every tensor given (None skipped) lives on the GPU of ``first``: a host or
+    other-device pointer handed to a kernel would fault the device instead of failing the call."""
+    dev = first.get_device() if first.is_cuda else -1
+    if dev < 0 or any(t is not None and (not t.is_cuda or t.get_device() != dev) for t in others):
+        raise ValueError(f"{what}: every tensor must be on one GPU (got "
+                         + ", ".join(str(t.device) for t in (first, *others) if t is not None) + ")")
+
+
 def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -206,7 +215,7 @@ def workspace(device: torch.device, nbytes: int, stream: int | None = None) -> t
 # ---------------------------------------------------------------------------------------
 def absmax(x: torch.Tensor) -> torch.Tensor:
     """max|x| as a 0-d fp32 device tensor."""
-    assert x.is_cuda
+    _gpu_args("absmax", x)
     x = x.contiguous()
     n = x.numel()
     out = torch.empty((), dtype=torch.float32, device=x.device)
@@ -218,6 +227,7 @@ def absmax(x: torch.Tensor) -> torch.Tensor:
 
 
 def quantize_int4(w: torch.Tensor, scale: float) -> torch.Tensor:
+    _gpu_args("quantize_int4", w)
     w = w.contiguous()
     q = torch.empty(w.shape, dtype=torch.int8, device=w.device)
     _check(lib().pk_quantize_int4(w.data_ptr(), pk_dtype(w.dtype), w.numel(), float(scale),
@@ -226,6 +236,7 @@ def quantize_int4(w: torch.Tensor, scale: float) -> torch.Tensor:
 
 
 def pack_int4(q: torch.Tensor) -> torch.Tensor:
+    _gpu_args("pack_int4", q)
     assert q.dim() == 2 and q.dtype == torch.int8
     if q.stride(1) != 1:
         q = q.contiguous()
@@ -237,6 +248,7 @@ def pack_int4(q: torch.Tensor) -> torch.Tensor:
 
 
 def unpack_int4(packed: torch.Tensor) -> torch.Tensor:
+    _gpu_args("unpack_int4", packed)
     assert packed.dim() == 2 and packed.dtype == torch.uint8
     packed = packed.contiguous()
     rows, half = packed.shape
@@ -251,7 +263,8 @@ def quantize_group(w: torch.Tensor, bits: int, group_size: int | None, *, half_m
                    scale_dtype: torch.dtype = torch.float16,
                    fake_dtype: torch.dtype | None = None):
     """Group RTN along dim 0 of a 2-D (K, N) tensor. Returns (qweight, scales, fake)."""
-    assert w.dim() == 2 and w.is_cuda
+    _gpu_args("quantize_group", w)
+    assert w.dim() == 2
     if w.stride(1) != 1:
         w = w.contiguous()
     K, N = w.shape
@@ -269,6 +282,7 @@ def quantize_group(w: torch.Tensor, bits: int, group_size: int | None, *, half_m
 
 
 def cast_e4m3(x: torch.Tensor, scale: float) -> torch.Tensor:
+    _gpu_args("cast_e4m3", x)
     x = x.contiguous()
     out = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
     _check(lib().pk_cast_e4m3(x.data_ptr(), pk_dtype(x.dtype), x.numel(), float(scale),
@@ -287,6 +301,7 @@ def w4a16_prep_activations(x: torch.Tensor, in_scale: torch.Tensor | None, mul: 
                            out: torch.Tensor | None = None) -> torch.Tensor:
     """fp16 ``x * in_scale[k] * mul`` for (M, K) activations of any float dtype (no scale:
     the cast alone)."""
+    _gpu_args("w4a16_prep_activations", x, in_scale, out)
     M, K = x.shape
     if x.stride(1) != 1:
         x = x.contiguous()
@@ -425,6 +440,7 @@ def w4a16_gemm_strips(a: torch.Tensor, qstrips: torch.Tensor, sstrips: torch.Ten
                       bias: torch.Tensor | None = None) -> torch.Tensor:
     """out = tensor_scale * (a @ dequant(q, s)) (+ bias) for 1..8 rows of fp16 activations on
     strip-layout codes and scales (strip_weights / strip_scales; pk_w4a16_gemm_strips)."""
+    _gpu_args("w4a16_gemm_strips", a, qstrips, sstrips, out, bias)
     M, K = a.shape
     N = qstrips.shape[1] * 8
     a = _rows_ok(a)
@@ -483,6 +499,10 @@ class PreparedStrips:
             self.h = None
 
     def __call__(self, a: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        if (a.dtype != torch.float16 or a.dim() != 2 or a.shape[1] != self.K or not a.is_cuda
+                or a.get_device() != self.dev):
+            raise ValueError(f"PreparedStrips: activations must be (M, {self.K}) fp16 on "
+                             f"cuda:{self.dev} (got {tuple(a.shape)} {a.dtype} on {a.device})")
         M = a.shape[0]
         if a.stride(0) != self.lda or a.stride(1) != 1 or a.data_ptr() % 16:
             a = a.contiguous() if self.lda == self.K else _rows_ok(a)
@@ -491,6 +511,11 @@ class PreparedStrips:
                                  "16-byte aligned")
         if out is None:
             out = a.new_empty((M, self.N), dtype=self.out_dtype)
+        elif (out.dtype != self.out_dtype or out.dim() != 2 or out.shape[0] != M
+              or out.shape[1] != self.N or out.stride(1) != 1 or not out.is_cuda
+              or out.get_device() != self.dev):
+            raise ValueError(f"PreparedStrips: out must be ({M}, {self.N}) {self.out_dtype} with "
+                             f"unit column stride on cuda:{self.dev}")
         rc = self.run(self.h, a.data_ptr(), out.data_ptr(), out.stride(0), M,
                       torch._C._cuda_getCurrentRawStream(self.dev))
         if rc != PK_OK:
@@ -502,6 +527,12 @@ class PreparedStrips:
         ``torch.cuda.Event`` ``start`` recorded as its kernel starts and ``stop`` as it ends, by
         the dispatch itself (``pk_w4a16_strips_run_events``). Each event is recorded once on
         the current stream first if it has no HIP event yet."""
+        if (a.dtype != torch.float16 or a.dim() != 2 or a.shape[1] != self.K or not a.is_cuda
+                or a.get_device() != self.dev or out.dtype != self.out_dtype
+                or tuple(out.shape) != (a.shape[0], self.N) or out.stride(1) != 1
+                or out.get_device() != self.dev):
+            raise ValueError("PreparedStrips.timed: (M, K) fp16 activations and an (M, N) output "
+                             "of the prepared dtype, both on the prepared device")
         if a.stride(0) != self.lda or a.stride(1) != 1 or a.data_ptr() % 16:
             raise ValueError(f"PreparedStrips.timed: activations need row stride {self.lda}, "
                              "16-byte aligned")
@@ -537,6 +568,7 @@ def w4a16_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor | No
     """out = tensor_scale * (a @ dequant(qweight, scales)) (+ bias, N values of fp32 / fp16 /
     bf16 added in the kernels' epilogue: pk_w4a16_gemm_bias). ``tiled``: qweight holds the
     codes in 128 x 256 blocks (tile_weights; pk_w4a16_gemm_tiled)."""
+    _gpu_args("w4a16_gemm", a, qweight, scales, out, bias)
     M, K = a.shape
     N = qweight.shape[1] * 8
     if bias is not None and (bias.numel() != N or bias.dtype not in _TORCH_TO_PK
@@ -600,6 +632,7 @@ def w4a16_gemm_partials(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Te
                         group_size: int, split_k: int, partials: torch.Tensor | None = None
                         ) -> torch.Tensor:
     """Per-slice fp32 partial sums (split, M, N) of a split-K W4A16 matmul."""
+    _gpu_args("w4a16_gemm_partials", a, qweight, scales, partials)
     M, K = a.shape
     N = qweight.shape[1] * 8
     g = int(group_size) if scales is not None else 0
@@ -614,6 +647,7 @@ def w4a16_gemm_partials(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Te
 
 
 def splitk_reduce(partials: torch.Tensor, scale: float, out: torch.Tensor) -> torch.Tensor:
+    _gpu_args("splitk_reduce", partials, out)
     split, M, N = partials.shape
     _check(lib().pk_splitk_reduce(partials.data_ptr(), split, M, N, float(scale), out.data_ptr(),
                                   pk_dtype(out.dtype), out.stride(0), stream_of(partials)),
@@ -624,6 +658,7 @@ def splitk_reduce(partials: torch.Tensor, scale: float, out: torch.Tensor) -> to
 def gemm_dense(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype, split_k: int) -> torch.Tensor:
     """C = A @ B for fp16 or bf16 A and B (same dtype), fp32 accumulate (pk_gemm_f16 /
     pk_gemm_bf16)."""
+    _gpu_args("gemm_dense", a, b)
     M, K = a.shape
     N = b.shape[1]
     a, b = _rows_ok(a), _rows_ok(b)
@@ -643,6 +678,7 @@ gemm_f16 = gemm_dense  # the fp16 name used by earlier callers
 
 def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, out_scale: float, out_dtype: torch.dtype,
              out: torch.Tensor | None = None) -> torch.Tensor:
+    _gpu_args("fp8_gemm", a8, b8, out)
     M, K = a8.shape
     N = b8.shape[1]
     a8 = _rows_ok(a8)
@@ -670,6 +706,7 @@ def gptq_block(q: torch.Tensor, ratio: torch.Tensor, err: torch.Tensor, b0: int,
                group: int) -> None:
     """Sweep columns [b0, b0 + nb) of q (fp32 [out, in], row stride q.stride(0)) in place;
     err[:, :nb] receives the quantization errors (pk_gptq_block)."""
+    _gpu_args("gptq_block", q, ratio, err)
     assert q.dtype == ratio.dtype == err.dtype == torch.float32
     assert q.stride(1) == 1 and ratio.stride(1) == 1 and err.stride(1) == 1
     out, n_in = q.shape
@@ -687,6 +724,7 @@ def flash_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, split: int,
                  sm_scale: float) -> torch.Tensor:
     """(B, H, D) fp32 single-query attention of q (B, H, D) over k, v (B, H, N, D), all fp16
     with unit stride along D (pk_flash_decode)."""
+    _gpu_args("flash_decode", q, k, v)
     B, H, N, D = k.shape
 
     def _d_unit(t: torch.Tensor) -> torch.Tensor:

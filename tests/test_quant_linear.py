@@ -211,3 +211,15 @@ def test_save_load_reference_layout_and_rejections(tmp_path, cuda):
         fresh = nn.Sequential(nn.Linear(256, 512), nn.ReLU(), nn.Linear(512, 256, bias=False)).to(cuda)
         with pytest.raises(ValueError):
             ql.load_quantized(fresh, p2)
+
+
+def test_host_activations_raise(cuda):
+    """Activations left on the host (of any dtype and row count: the decode fast path, the
+    strip call, the input cast and the block GEMM) raise instead of reaching a kernel."""
+    torch.manual_seed(7)
+    q = ql.QuantLinear.from_linear(nn.Linear(256, 512).to(cuda), 128)
+    q(torch.randn(1, 256, device=cuda).half())  # the fast path prepared
+    for x in (torch.randn(1, 256).half(), torch.randn(16, 256), torch.randn(16, 256).half(),
+              torch.randn(2, 256).bfloat16()):
+        with pytest.raises(ValueError, match="GPU|cuda"):
+            q(x)

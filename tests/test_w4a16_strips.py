@@ -364,8 +364,9 @@ def test_quant_linear_prepared_call_follows_its_buffers(cuda):
 @pytest.mark.gpu
 def test_prepared_strips_handle(cuda):
     """pk_w4a16_strips_prepare / _run give the bits of pk_w4a16_gemm_strips for every row count;
-    a bad fixed argument makes prepare return NULL with the reason; reassigning a QuantLinear's
-    bias rebuilds its prepared call."""
+    a bad fixed argument makes prepare return NULL with the reason; activations or outputs of
+    the wrong dtype, device or shape raise; reassigning a QuantLinear's bias rebuilds its
+    prepared call."""
     from torch import nn
 
     import quant_linear as ql
@@ -385,6 +386,15 @@ def test_prepared_strips_handle(cuda):
         assert torch.equal(via_ctypes(ag[:M]), ref), M
     with pytest.raises(_pk.PicoKernelsError, match="group_size"):
         _pk.PreparedStrips(qs, ss, 96, 1.0, torch.float16)
+    # activations or an output the prepared call cannot take raise before any launch
+    for bad in (ag[:2].float(), ag[:2].cpu(), ag[:2, : K // 2]):
+        with pytest.raises(ValueError, match="fp16"):
+            call(bad)
+    for bad_out in (torch.empty((2, N), dtype=torch.float16, device=cuda),
+                    torch.empty((3, N), dtype=torch.float32, device=cuda),
+                    torch.empty((N, 2), dtype=torch.float32, device=cuda).t()):
+        with pytest.raises(ValueError, match="out must be"):
+            call(ag[:2], bad_out)
     lin = nn.Linear(K, N).to(cuda)
     q = ql.QuantLinear.from_linear(lin, 128)
     x = ag[:1].contiguous()
