@@ -57,9 +57,15 @@ bool splitk_in_l2_possible();
 // (64 at most); concurrent first calls may both set it, which is harmless.
 int set_lds_limit_once(const void* kernel, int bytes, std::atomic<uint64_t>* done);
 
-// C = scale * sum over slices of the (S, M, N) fp32 partials, in slice order.
+// C = scale * sum over slices of the (S, M, N) fp32 partials, in slice order. `small_groups`:
+// workgroups of 64 threads instead of 256 (for 2, 4 or 8 slices), what the register-dequant
+// kernel's partials reduce fastest with -- measured on MI355X at 72..128 rows of 1024^2 ..
+// 4096^2 weights, the whole call: o_proj 4096 x 4096 M = 128 15.8 -> 12.9 us, M = 72 14.1 ->
+// 12.7, 2048 x 2048 M = 128 13.0 -> 10.3 -- while after the packed-B GEMM's planes 256 stay
+// faster (qkv M = 128 18.7 against 19.0, down 26.6 against 27.6; 128 and 512 within 1% of 256
+// everywhere).
 int splitk_reduce(const float* partials, int S, int M, int N, OutEpi epi, void* c, int c_dtype,
-                  int64_t ldc, hipStream_t s);
+                  int64_t ldc, hipStream_t s, bool small_groups = false);
 
 struct GemvPlan {
   int rpt, rl, split, k_slice, tiles;

@@ -112,9 +112,10 @@ bool splitk_in_l2_ok(hipStream_t stream) {
 
 // One thread per 4 consecutive outputs; the S slice loads are unrolled so they are all in
 // flight at once (the kernel is one memory round trip, not S of them). The four outputs go
-// out as one 8-byte (fp16 / bf16) or 16-byte (fp32) store when `vec` (aligned rows).
-template <int S, int DT>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partials,
+// out as one 8-byte (fp16 / bf16) or 16-byte (fp32) store when `vec` (aligned rows). TB
+// threads per workgroup (256, or 64 after the register-dequant kernel: see splitk_reduce).
+template <int S, int DT, int TB = 256>
+__global__ __launch_bounds__(TB) void splitk_reduce_kernel(const float* __restrict__ partials,
                                                             int M, int N, OutEpi epi,
                                                             void* __restrict__ c, bool vec,
                                                             int64_t ldc) {
@@ -165,17 +166,27 @@ __global__ __launch_bounds__(256) void splitk_reduce_any_kernel(const float* __r
 }
 
 int splitk_reduce(const float* partials, int S, int M, int N, OutEpi epi, void* c, int c_dtype,
-                  int64_t ldc, hipStream_t s) {
+                  int64_t ldc, hipStream_t s, bool small_groups) {
   const int64_t quads = (int64_t)M * N / 4;
-  const unsigned blocks = (unsigned)cdiv(quads, 256);
+  const bool g64 = small_groups && (S == 2 || S == 4 || S == 8);
+  const unsigned blocks = (unsigned)cdiv(quads, g64 ? 64 : 256);
   const int esz = c_dtype == PK_F32 ? 4 : 2;
   const bool vec = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & (4 * esz - 1)) == 0;
   auto go = [&](auto DTC) {
     constexpr int dt = decltype(DTC)::value;
     switch (S) {
-      case 2: splitk_reduce_kernel<2, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
-      case 4: splitk_reduce_kernel<4, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
-      case 8: splitk_reduce_kernel<8, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
+      case 2:
+        if (g64) splitk_reduce_kernel<2, dt, 64><<<blocks, 64, 0, s>>>(partials, M, N, epi, c, vec, ldc);
+        else splitk_reduce_kernel<2, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc);
+        break;
+      case 4:
+        if (g64) splitk_reduce_kernel<4, dt, 64><<<blocks, 64, 0, s>>>(partials, M, N, epi, c, vec, ldc);
+        else splitk_reduce_kernel<4, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc);
+        break;
+      case 8:
+        if (g64) splitk_reduce_kernel<8, dt, 64><<<blocks, 64, 0, s>>>(partials, M, N, epi, c, vec, ldc);
+        else splitk_reduce_kernel<8, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc);
+        break;
       case 16: splitk_reduce_kernel<16, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
       case 32: splitk_reduce_kernel<32, dt><<<blocks, 256, 0, s>>>(partials, M, N, epi, c, vec, ldc); break;
       default:

@@ -625,7 +625,7 @@ int skinny_launch(const SkinnyPlan& pl, const void* a, int64_t lda, const uint32
   else launch_skinny_cfg<false>(pl, p, l2, s);
   PK_LAUNCH_CHECK("w4a16 skinny");
   if (pl.split > 1 && !partials_only && !l2)
-    return splitk_reduce(p.partials, pl.split, M, N, epi, c, c_dtype, ldc, s);
+    return splitk_reduce(p.partials, pl.split, M, N, epi, c, c_dtype, ldc, s, true);
   return PK_OK;
 }
 
