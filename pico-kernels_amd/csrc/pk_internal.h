@@ -59,11 +59,11 @@ int set_lds_limit_once(const void* kernel, int bytes, std::atomic<uint64_t>* don
 
 // C = scale * sum over slices of the (S, M, N) fp32 partials, in slice order. `small_groups`:
 // workgroups of 64 threads instead of 256 (for 2, 4 or 8 slices), what the register-dequant
-// kernel's partials reduce fastest with -- measured on MI355X at 72..128 rows of 1024^2 ..
-// 4096^2 weights, the whole call: o_proj 4096 x 4096 M = 128 15.8 -> 12.9 us, M = 72 14.1 ->
-// 12.7, 2048 x 2048 M = 128 13.0 -> 10.3 -- while after the packed-B GEMM's planes 256 stay
-// faster (qkv M = 128 18.7 against 19.0, down 26.6 against 27.6; 128 and 512 within 1% of 256
-// everywhere).
+// kernel's partials reduce fastest with -- measured on MI355X, the whole call in graphs: with
+// weights streamed from HBM (rotating copies) o_proj 4096 x 4096 M = 128 16.15 -> 15.6 us;
+// with one cached weight copy 15.8 -> 12.9 us, M = 72 14.1 -> 12.7, 2048 x 2048 M = 128
+// 13.0 -> 10.3 -- while after the packed-B GEMM's planes 256 stay faster (cached copy: qkv
+// M = 128 18.7 against 19.0, down 26.6 against 27.6; 128 and 512 within 1% of 256).
 int splitk_reduce(const float* partials, int S, int M, int N, OutEpi epi, void* c, int c_dtype,
                   int64_t ldc, hipStream_t s, bool small_groups = false);
 
