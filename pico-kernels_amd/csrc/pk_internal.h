@@ -62,8 +62,9 @@ int set_lds_limit_once(const void* kernel, int bytes, std::atomic<uint64_t>* don
 // kernel's partials reduce fastest with -- measured on MI355X, the whole call in graphs: with
 // weights streamed from HBM (rotating copies) o_proj 4096 x 4096 M = 128 16.15 -> 15.6 us;
 // with one cached weight copy 15.8 -> 12.9 us, M = 72 14.1 -> 12.7, 2048 x 2048 M = 128
-// 13.0 -> 10.3 -- while after the packed-B GEMM's planes 256 stay faster (cached copy: qkv
-// M = 128 18.7 against 19.0, down 26.6 against 27.6; 128 and 512 within 1% of 256).
+// 13.0 -> 10.3 -- while after the packed-B GEMM's planes 256 stay faster (streamed weights:
+// qkv M = 128 18.0 against 18.2, down 27.6 against 28.4; cached copy: qkv 18.7 against 19.0,
+// down 26.6 against 27.6; 128 and 512 within 1% of 256).
 int splitk_reduce(const float* partials, int S, int M, int N, OutEpi epi, void* c, int c_dtype,
                   int64_t ldc, hipStream_t s, bool small_groups = false);
 
